@@ -1,0 +1,91 @@
+/*
+ * nanochat_amd: the C ABI of the MI355X (gfx950) fp8-KV decode path, libnanochat_amd.so.
+ *
+ * Conventions (the reference's, model/kernels/*.cu with native.py:43-65): every tensor is a raw device pointer,
+ * counts are C ints, the HIP stream is the last argument, and every launch is stream-ordered and asynchronous.
+ * Two error classes:
+ *   - argument errors are checked on the host before any launch: the call returns a negative status and
+ *     nc_last_error() names the problem (the reference validates in Python, inference/decoder.py:197-201);
+ *   - a failed HIP runtime call or launch aborts the process with file:line (model/kernels/decode.cu:47-53).
+ * Device-side, rows or keys whose position, sequence or block is out of range are skipped, never written or read
+ * out of bounds.
+ *
+ * Cache layout (per layer), PAGE = 16 positions per block, D = 128:
+ *   k_cache  uint8 [num_blocks][Hkv][16][128]   row-major keys
+ *   v_cache  uint8 [num_blocks][Hkv][4][128][4] quad-transposed: key t, dim d at byte (t/4)*512 + d*4 + t%4
+ *   k_scale, v_scale  fp32 [num_blocks][Hkv][16]   one absmax/448 scale per (token, kv head)
+ *   block_table int32 [num_seqs][max_blocks], or NULL: contiguous, sequence s's page i is block s*max_blocks + i
+ * Codes are OCP float8 e4m3fn, rounded to nearest even from x / scale; the reference caches bf16 instead
+ * (model/kernels/decode.cu:4-7, 726).
+ */
+#ifndef NANOCHAT_AMD_H
+#define NANOCHAT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header (1). */
+int nc_abi_version(void);
+
+/* Message of the last failed call on this thread. */
+const char *nc_last_error(void);
+
+/* Training-layout q/k prologue: RMS norm with fp32 gains gq, gk (128), then RoPE by cos/sin fp32 [T][64] at
+ * position t % T. q, k: bf16 (B, T, H, 128) column blocks of a (B, T, 3 H 128) projection; qo, ko: contiguous
+ * bf16 (B, T, H, 128); rows = B T H.
+ * Replaces: qkp_forward, model/kernels/qk_prologue.cu:111-118 (same signature); called by qk_forward,
+ * model/ops/qk_prologue.py:13-21. */
+void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, void *qo, void *ko, const void *cos,
+                 const void *sin, long long rows, int H, int T, void *stream);
+
+/* Fused append of n rows of the fused projection qkv (bf16 [n][row_stride]: Hq q heads, Hkv k heads, Hkv v heads
+ * of 128): q and k RMS-normed with gains q_gain, k_gain, rotated by cos/sin fp32 [rope_len][64] at pos[n]; q to
+ * q_out (bf16 [n][Hq][128]); k and v quantised per (token, kv head) into sequence seq[n]'s page. A row out of range
+ * (pos < 0 or >= rope_len or past max_blocks pages, seq outside [0, num_seqs), block outside [0, num_blocks))
+ * writes no cache byte and gets a NaN q_out row.
+ * Replaces: k_prologue + attn_prologue, model/kernels/decode.cu:476-507,550-565 (which cache bf16). */
+int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, const int32_t *pos, const int32_t *seq,
+                     const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                     int hq, int hkv, void *q_out, uint8_t *k_cache, uint8_t *v_cache, float *k_scale,
+                     float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
+                     void *stream);
+
+/* Quantise-and-store of final K and V rows (bf16 [n][row_stride], Hkv heads of 128, no norm or rotation) at
+ * (seq[n], pos[n]).
+ * Replaces: the cache write of DynamicCache.update, inference/modeling_nanochat.py:95-96 (bf16 there). */
+int nc_kv_store_fp8(const void *k, const void *v, long long row_stride, int n, const int32_t *pos,
+                    const int32_t *seq, int hkv, uint8_t *k_cache, uint8_t *v_cache, float *k_scale,
+                    float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
+                    void *stream);
+
+/* Gather of sequences 0..B-1: codes of the first ctx_len[b] positions to k_out, v_out (uint8
+ * [B][Hkv][max_ctx][128], both row-major) and scales to ks_out, vs_out (fp32 [B][Hkv][max_ctx]); later
+ * positions are zero.
+ * Replaces: the contiguous per-slot cache read of k_attn's load_run, model/kernels/decode.cu:581-591, and the
+ * prompt copies of prompt_copy, decode.cu:1053-1067. */
+int nc_kv_gather_fp8(const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale, const float *v_scale,
+                     const int32_t *block_table, int max_blocks, int num_blocks, const int32_t *ctx_len, int B,
+                     int hkv, int max_ctx, uint8_t *k_out, uint8_t *v_out, float *ks_out, float *vs_out,
+                     void *stream);
+
+/* Workspace bytes nc_decode_attn_fp8 needs for this shape (0 when no sequence is split). */
+long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx);
+
+/* Single-token decode attention: query b (bf16 q [B][Hq][128]) at position p = ctx_len[b] - 1 attends keys
+ * [max(p - window, 0), p] of sequence b (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores
+ * times sm_scale, fp32 softmax, bf16 out [B][Hq][128]. ctx_len values above max_ctx are clamped to it; a
+ * sequence with ctx_len <= 0 gets a zero row. Hq / Hkv <= 16.
+ * Replaces: k_attn, model/kernels/decode.cu:567-675 (bf16 MHA, one block per (head, slot)). */
+int nc_decode_attn_fp8(const void *q, const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,
+                       const float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks,
+                       const int32_t *ctx_len, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
+                       void *out, void *workspace, long long workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

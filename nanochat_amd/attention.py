@@ -1,0 +1,56 @@
+"""Attention over the fp8 cache: single-token decode (split-K flash-decode) and chunked prefill.
+
+decode_attention replaces the reference's k_attn (model/kernels/decode.cu:567-675): query b sits at position
+ctx_len[b] - 1 and attends the keys [max(p - window, 0), p] of its sequence in the cache (its own key appended
+first), query head h reading kv head h // (Hq / Hkv). Softmax in fp32, output bf16.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import Tensor
+
+from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
+from nanochat_amd.native import check, hip_library, pointer, stream
+
+
+def decode_workspace_bytes(batch: int, hq: int, hkv: int, max_ctx: int) -> int:
+    return int(hip_library().nc_decode_workspace_bytes(batch, hq, hkv, max_ctx))
+
+
+def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: int, window: int = -1,
+                     sm_scale: float | None = None, out: Tensor | None = None,
+                     workspace: Tensor | None = None) -> Tensor:
+    """q bf16 [B][Hq][128] (normed and rotated, e.g. Fp8KVCache.append's q_out); ctx_len int32 [B] on the GPU, each
+    at most max_ctx (an upper bound the caller knows on the host: it sizes the grid and the workspace); window: keys
+    before the query, < 0 for all. Returns bf16 [B][Hq][128]."""
+    _require(q, "q", torch.bfloat16, 3)
+    B, hq, D = q.shape
+    if D != HEAD_DIM:
+        raise ValueError(f"head dim {D} != 128")
+    _require(ctx_len, "ctx_len", torch.int32, 1)
+    if ctx_len.shape[0] != B or B > cache.num_seqs:
+        raise ValueError(f"ctx_len has {ctx_len.shape[0]} entries for batch {B} (cache holds {cache.num_seqs})")
+    if not 0 < max_ctx <= cache.capacity:
+        raise ValueError(f"max_ctx {max_ctx} outside [1, {cache.capacity}]")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out, "out", torch.bfloat16, 3)
+        if out.shape != q.shape:
+            raise ValueError("out must have q's shape")
+    need = decode_workspace_bytes(B, hq, cache.hkv, max_ctx)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
+    lib = hip_library()
+    check(lib.nc_decode_attn_fp8(pointer(q), pointer(cache.k), pointer(cache.v), pointer(cache.k_scale),
+                                 pointer(cache.v_scale), pointer(cache.block_table), cache.max_blocks,
+                                 cache.num_blocks, pointer(ctx_len), window, B, hq, cache.hkv, max_ctx, scale,
+                                 pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
+                                 stream()))
+    return out

@@ -1,0 +1,80 @@
+"""Build recipe of the HIP library: every csrc/*.hip compiled by hipcc for gfx950 into one in-tree shared object,
+libnanochat_amd.so, loaded with ctypes (the reference builds each model/kernels/<name>.cu with nvcc the same way,
+native.py:54-65).
+
+The library sits next to this file with a sidecar `<lib>.sha256` holding the digest of the command and every
+source and header, so a stale library is detected at load time (native.hip_library) and rebuilt.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import subprocess
+import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+LIBRARY = PACKAGE / "libnanochat_amd.so"
+STAMP = LIBRARY.with_suffix(".so.sha256")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere (hipcc would otherwise form them from float2 code).
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{PACKAGE.parent / 'include'}"]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def digest() -> str:
+    h = hashlib.sha256(" ".join([HIPCC, *FLAGS]).encode())
+    for f in sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(PACKAGE.parent / "include").glob("*.h")]):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def is_current() -> bool:
+    return LIBRARY.exists() and STAMP.exists() and STAMP.read_text().strip() == digest()
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every source (in parallel) and link; the library is replaced atomically."""
+    srcs = sources()
+    stamp = digest()
+    with tempfile.TemporaryDirectory(dir=PACKAGE) as tmp:
+        objs = [Path(tmp) / (s.stem + ".o") for s in srcs]
+
+        def compile_one(pair):
+            src, obj = pair
+            cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            if r.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
+            if verbose and r.stderr.strip():
+                filtered = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
+                if filtered:
+                    print("\n".join(filtered), file=sys.stderr)
+            return obj
+
+        with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+            list(pool.map(compile_one, zip(srcs, objs)))
+        out = Path(tmp) / LIBRARY.name
+        r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(out), *map(str, objs)],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stderr}")
+        out.replace(LIBRARY)
+    STAMP.write_text(stamp + "\n")
+    if verbose:
+        print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build()

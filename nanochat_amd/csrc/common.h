@@ -1,0 +1,104 @@
+/*
+ * Shared by every kernel file of the MI355X (gfx950) fp8-KV decode path: types, the HIP error policy, bf16 and
+ * OCP e4m3fn rounding, 16-byte vector access and wave64 lane exchanges.
+ *
+ * Precision rules: code that must match the CPU oracle bit for bit (the append's row math and quantisation) lives
+ * in functions that open with `#pragma clang fp contract(off)`, so no a*b+c is fused; `/` and `sqrtf` are
+ * correctly rounded (hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt). Attention code may contract.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#define NC_WAVE 64
+#define NC_HEAD_DIM 128
+#define NC_HALF 64
+
+typedef uint16_t bf16_t; /* bf16 storage: the high half of an fp32 */
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+/* A failed HIP runtime call aborts with its file and line: a launch that did not happen must never look like a
+ * result (the reference's policy, model/kernels/decode.cu:47-53). Argument errors are returned, not aborted. */
+#define NC_HIP_CHECK(call) nc_hip_check((call), #call, __FILE__, __LINE__)
+static inline void nc_hip_check(hipError_t e, const char *call, const char *file, int line) {
+    if (e == hipSuccess) return;
+    fprintf(stderr, "%s:%d: %s: %s\n", file, line, call, hipGetErrorString(e));
+    abort();
+}
+
+/* After a kernel launch: a launch error (bad configuration, no device) aborts like a failed call. */
+#define NC_LAUNCH_CHECK() NC_HIP_CHECK(hipGetLastError())
+
+/* Host-side argument errors: the message of the last failed entry point (per thread), status < 0. */
+int nc_fail(const char *fmt, ...);
+#define NC_REQUIRE(cond, ...) \
+    do {                      \
+        if (!(cond)) return nc_fail(__VA_ARGS__); \
+    } while (0)
+
+/* ------------------------------------------------------------------------------------------ bf16 */
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+/* fp32 -> bf16 bits, round to nearest even (NaN kept quiet). */
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+/* 8 bf16 (one 16-byte load) as fp32. */
+__device__ __forceinline__ void load_bf16x8(const bf16_t *p, float *v) {
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(u[i] << 16);
+        v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+}
+
+/* 8 fp32 rounded to bf16, one 16-byte store. */
+__device__ __forceinline__ void store_bf16x8(bf16_t *p, const float *v) {
+    u32x4 u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) u[i] = f32_to_bf16(v[2 * i]) | (f32_to_bf16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4 *>(p) = u;
+}
+
+/* ------------------------------------------------------------------------------------------ OCP e4m3fn */
+
+#define NC_FP8_MAX 448.0f
+
+/* fp32 -> e4m3fn code, round to nearest even, no saturation (|x| > 464, inf, NaN give 0x7f | sign): the same
+ * function as torch's float32 -> float8_e4m3fn cast. Normal results re-bias the exponent (127 -> 7) and round the
+ * mantissa to 3 bits in integer arithmetic; subnormal results count 2^-9 steps with v_rndne. */
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+#pragma clang fp contract(off)
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    uint32_t code;
+    if (a >= 0x7f800000u) {
+        code = 0x7fu;
+    } else if (a >= 0x3c800000u) { /* >= 2^-6 */
+        const uint32_t v = a - (120u << 23);
+        code = (v + 0x7ffffu + ((v >> 20) & 1u)) >> 20;
+        if (code > 0x7eu) code = 0x7fu;
+    } else {
+        code = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+    }
+    return code | sign;
+}
+
+/* ------------------------------------------------------------------------------------------ lane exchanges */
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, NC_WAVE); }

@@ -1,0 +1,49 @@
+"""Test helpers: move GPU tensors into the oracle's numpy structures, and the attention tolerance of the
+benchmark contract (max abs err <= 2e-2, mean <= 2e-3 against the fp64 oracle)."""
+
+import numpy as np
+import torch
+
+from oracle import golden as G
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor -> uint16 numpy bits."""
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def oracle_cache(cache) -> G.PagedCache:
+    c = G.PagedCache(cache.num_blocks, cache.hkv)
+    c.k[...] = cache.k.cpu().numpy()
+    c.v[...] = cache.v.cpu().numpy()
+    c.k_scale[...] = cache.k_scale.cpu().numpy()
+    c.v_scale[...] = cache.v_scale.cpu().numpy()
+    return c
+
+
+def table(cache):
+    return None if cache.block_table is None else cache.block_table.cpu().numpy()
+
+
+def assert_same_cache(gpu_cache, ref: G.PagedCache) -> None:
+    np.testing.assert_array_equal(gpu_cache.k.cpu().numpy(), ref.k)
+    np.testing.assert_array_equal(gpu_cache.v.cpu().numpy(), ref.v)
+    np.testing.assert_array_equal(gpu_cache.k_scale.cpu().numpy().view(np.uint32), ref.k_scale.view(np.uint32))
+    np.testing.assert_array_equal(gpu_cache.v_scale.cpu().numpy().view(np.uint32), ref.v_scale.view(np.uint32))
+
+
+def attention_error(got: torch.Tensor, want: np.ndarray) -> tuple[float, float]:
+    g = G.bf16_to_f32(bits(got)).astype(np.float64)
+    assert not np.isnan(g).any(), "NaN in the GPU output"
+    err = np.abs(g - want)
+    return float(err.max()), float(err.mean())
+
+
+def assert_attention_close(got: torch.Tensor, want: np.ndarray, label: str = "") -> tuple[float, float]:
+    mx, mean = attention_error(got, want)
+    print(f"{label} max abs err {mx:.3e} mean {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (label, mx, mean)
+    return mx, mean

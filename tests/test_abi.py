@@ -1,0 +1,85 @@
+"""The C-ABI library builds, loads and exports every entry point include/nanochat_amd.h declares, and its host-side
+argument checks reject bad calls before any launch (CPU only: no compute call reaches a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanochat_amd import native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nanochat_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^(?:[A-Za-z_]\w*\s+)+\**\s*(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declarations_match_the_bindings():
+    names = declared_functions()
+    assert len(names) >= 8
+    assert set(names) == set(native.SIGNATURES), set(names) ^ set(native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = native.hip_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.nc_abi_version() == 1
+
+
+def test_workspace_query_is_pure_host():
+    lib = native.hip_library()
+    assert lib.nc_decode_workspace_bytes(0, 16, 4, 8192) == 0
+    w = lib.nc_decode_workspace_bytes(64, 16, 4, 8193)
+    assert w > 0 and w % (130 * 4) == 0
+
+
+NULL = ctypes.c_void_p(0)
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its host checks first
+
+
+@pytest.mark.parametrize("kwargs, message", [
+    (dict(hq=6, hkv=4), "multiple"),
+    (dict(hq=64, hkv=2), "exceeds"),
+    (dict(max_ctx=0), "max_ctx"),
+    (dict(max_ctx=10_000), "max_ctx"),
+    (dict(workspace_bytes=0), "workspace"),
+    (dict(num_blocks=2), "contiguous"),
+])
+def test_decode_rejects_bad_arguments(kwargs, message):
+    lib = native.hip_library()
+    a = dict(hq=16, hkv=4, max_ctx=4096, workspace_bytes=1 << 30, num_blocks=1 << 16)
+    a.update(kwargs)
+    rc = lib.nc_decode_attn_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 512, a["num_blocks"], FAKE, -1, 8, a["hq"],
+                                a["hkv"], a["max_ctx"], 0.08, FAKE, FAKE, a["workspace_bytes"], NULL)
+    assert rc < 0
+    assert message in lib.nc_last_error().decode()
+
+
+def test_append_rejects_bad_arguments():
+    lib = native.hip_library()
+    base = [FAKE, 1024, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 16, 4, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 8, 64,
+            8, NULL]
+    bad_stride = list(base)
+    bad_stride[1] = 100
+    assert lib.nc_kv_append_fp8(*bad_stride) < 0 and "row_stride" in lib.nc_last_error().decode()
+    bad_heads = list(base)
+    bad_heads[10] = 6
+    assert lib.nc_kv_append_fp8(*bad_heads) < 0 and "multiple" in lib.nc_last_error().decode()
+    null_cache = list(base)
+    null_cache[13] = NULL
+    assert lib.nc_kv_append_fp8(*null_cache) < 0 and "null" in lib.nc_last_error().decode()
+    assert lib.nc_kv_store_fp8(FAKE, FAKE, 100, 4, FAKE, FAKE, 4, FAKE, FAKE, FAKE, FAKE, NULL, 8, 64, 8, NULL) < 0
+    assert lib.nc_kv_gather_fp8(FAKE, FAKE, FAKE, FAKE, NULL, 8, 64, FAKE, 8, 4, 200, FAKE, FAKE, FAKE, FAKE,
+                                NULL) < 0
+
+
+def test_stale_library_is_detected(tmp_path, monkeypatch):
+    from nanochat_amd import build
+
+    assert build.is_current()
+    monkeypatch.setattr(build, "STAMP", tmp_path / "missing.sha256")
+    assert not build.is_current()

@@ -1,0 +1,145 @@
+"""GPU parity of the cache's write side and gather against the oracle: bit-exact q rows, cache bytes and scales."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_same_cache, bits, oracle_cache, table
+from nanochat_amd.kv_cache import Fp8KVCache
+from nanochat_amd.qk_prologue import qk_forward
+from nanochat_amd.rotary import rotary_tables
+from nanochat_amd.workloads import block_table_for, seeded_normal
+from oracle import golden as G
+
+pytestmark = pytest.mark.gpu
+
+
+def random_bytes(cache: Fp8KVCache, seed: int) -> None:
+    """Fill the cache with seeded garbage so untouched bytes are checked to stay untouched."""
+    g = torch.Generator().manual_seed(seed)
+    for t in (cache.k, cache.v):
+        t.copy_(torch.randint(0, 256, t.shape, generator=g, dtype=torch.uint8))
+    for t in (cache.k_scale, cache.v_scale):
+        t.copy_(torch.rand(t.shape, generator=g))
+
+
+def make_cache(kind: str, n_seq: int, cap: int, hkv: int, dev, seed: int) -> Fp8KVCache:
+    if kind == "contiguous":
+        return Fp8KVCache.contiguous(n_seq, cap, hkv, dev)
+    tbl, nb = block_table_for(np.full(n_seq, cap), seed, dev)
+    return Fp8KVCache.paged(tbl, nb + 3, hkv)  # spare blocks nobody owns
+
+
+APPEND_CASES = [
+    # name, B sequences, rows per sequence, first position, hq, hkv, theta, layout
+    ("cfg1-decode-b1-h6", 1, 1, 1024, 6, 6, 1e6, "contiguous"),
+    ("cfg2-decode-b32-h10", 32, 1, 4096, 10, 10, 1e4, "contiguous"),
+    ("cfg3-decode-b64-gqa", 64, 1, 700, 16, 4, 1e4, "paged"),
+    ("cfg4-chunk-b8-512", 8, 512, 3584, 16, 4, 1e4, "paged"),
+    ("page-edges", 3, 33, 0, 4, 2, 1e4, "paged"),
+]
+
+
+@pytest.mark.parametrize("name, B, rows, start, hq, hkv, theta, layout", APPEND_CASES)
+def test_append_bit_exact(gpu, name, B, rows, start, hq, hkv, theta, layout):
+    print(f"append case {name}", flush=True)
+    dev = gpu
+    cap = start + rows
+    cache = make_cache(layout, B, cap, hkv, dev, seed=11)
+    random_bytes(cache, 12)
+    ref = oracle_cache(cache)
+    n = B * rows
+    qkv = seeded_normal((n, (hq + 2 * hkv) * 128), 13, dev, outliers=0.01)
+    # zero heads: a zero k row (after norm it stays zero) and a zero v row give scale 0 and codes 0
+    qkv[0, hq * 128:(hq + 1) * 128] = 0
+    qkv[-1, (hq + hkv) * 128:(hq + hkv + 1) * 128] = 0
+    pos = torch.from_numpy(np.tile(np.arange(start, start + rows), B).astype(np.int32)).to(dev)
+    seq = torch.from_numpy(np.repeat(np.arange(B), rows).astype(np.int32)).to(dev)
+    g = torch.Generator().manual_seed(14)
+    q_gain, k_gain = (0.5 + torch.rand(128, generator=g)).to(dev), (0.5 + torch.rand(128, generator=g)).to(dev)
+    cos, sin = rotary_tables(cap, theta, dev)
+    q = cache.append(qkv, pos, seq, q_gain, k_gain, cos, sin, hq)
+    torch.cuda.synchronize()
+    q_ref = G.append(ref, bits(qkv), pos.cpu().numpy(), seq.cpu().numpy(), q_gain.cpu().numpy(),
+                     k_gain.cpu().numpy(), cos.cpu().numpy(), sin.cpu().numpy(), hq, hkv, table(cache),
+                     cache.max_blocks)
+    np.testing.assert_array_equal(bits(q), q_ref)
+    assert_same_cache(cache, ref)
+
+
+def test_append_rows_out_of_range_write_nothing(gpu):
+    dev = gpu
+    hq, hkv = 4, 2
+    cache = make_cache("paged", 2, 64, hkv, dev, seed=21)
+    cache.block_table[1, 2] = -1  # a hole in the table
+    random_bytes(cache, 22)
+    before = oracle_cache(cache)
+    cos, sin = rotary_tables(64, 1e4, dev)
+    qkv = seeded_normal((5, (hq + 2 * hkv) * 128), 23, dev)
+    # pos < 0, pos >= rope_len, seq >= num_seqs, a page with no block, and one valid row
+    pos = torch.tensor([-1, 64, 3, 40, 5], dtype=torch.int32, device=dev)
+    seq = torch.tensor([0, 0, 2, 1, 1], dtype=torch.int32, device=dev)
+    ones = torch.ones(128, device=dev)
+    q = cache.append(qkv, pos, seq, ones, ones, cos, sin, hq)
+    torch.cuda.synchronize()
+    assert torch.isnan(q[:3].float()).all() and not torch.isnan(q[3:].float()).any()
+    G.append(before, bits(qkv[4:]), np.array([5]), np.array([1]), np.ones(128, np.float32),
+             np.ones(128, np.float32), cos.cpu().numpy(), sin.cpu().numpy(), hq, hkv, table(cache),
+             cache.max_blocks)
+    assert_same_cache(cache, before)
+
+
+@pytest.mark.parametrize("layout", ["contiguous", "paged"])
+def test_store_bit_exact(gpu, layout):
+    dev = gpu
+    hkv, B, L = 4, 5, 77
+    cache = make_cache(layout, B, 80, hkv, dev, seed=31)
+    random_bytes(cache, 32)
+    ref = oracle_cache(cache)
+    n = B * L
+    k = seeded_normal((n, hkv * 128), 33, dev, outliers=0.01)
+    v = seeded_normal((n, hkv * 128), 34, dev, outliers=0.01)
+    k[5] = 0
+    v[7, :128] = 0
+    pos = torch.from_numpy(np.tile(np.arange(L), B).astype(np.int32)).to(dev)
+    seq = torch.from_numpy(np.repeat(np.arange(B), L).astype(np.int32)).to(dev)
+    cache.store(k, v, pos, seq)
+    torch.cuda.synchronize()
+    kc, ks = G.quantize_rows(bits(k).reshape(n, hkv, 128))
+    vc, vs = G.quantize_rows(bits(v).reshape(n, hkv, 128))
+    blk = G.PagedCache.block_of(seq.cpu().numpy(), pos.cpu().numpy(), table(cache), cache.max_blocks)
+    t = pos.cpu().numpy() % 16
+    for h in range(hkv):
+        ref.write(blk, h, t, kc[:, h], ks[:, h], vc[:, h], vs[:, h])
+    assert_same_cache(cache, ref)
+
+
+def test_qkp_forward_bit_exact(gpu):
+    """The training-layout prologue (model/ops/qk_prologue.py:13-21 surface) against the oracle's row math."""
+    dev = gpu
+    B, T, H = 2, 96, 6
+    C = H * 128
+    qkv = seeded_normal((B, T, 3 * C), 41, dev)
+    q, k = qkv[..., :C].unflatten(-1, (H, 128)), qkv[..., C:2 * C].unflatten(-1, (H, 128))
+    g = torch.Generator().manual_seed(42)
+    gq, gk = (0.5 + torch.rand(128, generator=g)).to(dev), (0.5 + torch.rand(128, generator=g)).to(dev)
+    cos, sin = rotary_tables(T, 1e6, dev)
+    qo, ko = qk_forward(q, k, gq, gk, cos, sin)
+    torch.cuda.synchronize()
+    c, s = cos.cpu().numpy()[None, :, None, :], sin.cpu().numpy()[None, :, None, :]
+    np.testing.assert_array_equal(bits(qo), G.qk_norm_rope(bits(q), gq.cpu().numpy(), c, s))
+    np.testing.assert_array_equal(bits(ko), G.qk_norm_rope(bits(k), gk.cpu().numpy(), c, s))
+
+
+@pytest.mark.parametrize("layout", ["contiguous", "paged"])
+def test_gather_bit_exact(gpu, layout):
+    dev = gpu
+    hkv, B = 3, 4
+    cache = make_cache(layout, B, 100, hkv, dev, seed=51)
+    random_bytes(cache, 52)
+    ctx = torch.tensor([100, 0, 17, 64], dtype=torch.int32, device=dev)
+    k, v, ks, vs = cache.gather(ctx, 100)
+    torch.cuda.synchronize()
+    want = G.gather(oracle_cache(cache), table(cache), cache.max_blocks, ctx.cpu().numpy(), 100)
+    for got, w in zip((k, v, ks, vs), want):
+        np.testing.assert_array_equal(got.cpu().numpy(), w)

@@ -1,0 +1,110 @@
+"""GPU parity of decode attention (append, then split-K flash-decode over the fp8 cache) against the fp64 oracle
+over the same cache bytes, within the benchmark tolerance (max abs <= 2e-2, mean <= 2e-3)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attention_close, assert_same_cache, bits, oracle_cache, table
+from nanochat_amd.attention import decode_attention
+from nanochat_amd.kv_cache import Fp8KVCache
+from nanochat_amd.workloads import CONFIG1, CONFIG2, CONFIG3, DecodeConfig, build_decode_case, decode_step
+from oracle import golden as G
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1 / math.sqrt(128)
+
+
+def run_and_check(cfg: DecodeConfig, dev, check_append_rows: int = 0):
+    print(f"decode case {cfg.name}", flush=True)
+    case = build_decode_case(cfg, dev, steps=1)
+    ref_before = oracle_cache(case.cache) if check_append_rows else None
+    max_ctx = int(case.ctx.max()) + 1
+    q, out = decode_step(case, 0, max_ctx)
+    torch.cuda.synchronize()
+    ref = oracle_cache(case.cache)
+    if check_append_rows:
+        pos = case.positions(0).cpu().numpy()
+        q_ref = G.append(ref_before, bits(case.qkv[0]), pos, np.arange(cfg.batch), case.q_gain.cpu().numpy(),
+                         case.k_gain.cpu().numpy(), case.cos.cpu().numpy(), case.sin.cpu().numpy(), cfg.hq, cfg.hkv,
+                         table(case.cache), case.cache.max_blocks)
+        np.testing.assert_array_equal(bits(q), q_ref)
+        assert_same_cache(case.cache, ref_before)
+    want = G.decode_attention(bits(q), ref, table(case.cache), case.cache.max_blocks, case.ctx + 1, cfg.window,
+                              cfg.hq, cfg.hkv, SCALE)
+    return assert_attention_close(out, want, cfg.name)
+
+
+def test_config1_plumbing(gpu):
+    run_and_check(CONFIG1, gpu, check_append_rows=1)
+
+
+def test_config2_d20_full_size(gpu):
+    run_and_check(CONFIG2, gpu, check_append_rows=1)
+
+
+def test_config3_ragged_gqa_paged_full_size(gpu):
+    run_and_check(CONFIG3, gpu)
+
+
+@pytest.mark.parametrize("cfg", [
+    DecodeConfig("window512-gqa", 8, 16, 4, ctx_range=(100, 3000), paged=True, window=512, seed=61),
+    DecodeConfig("window-not-page-aligned", 4, 8, 2, ctx=(1000, 37, 16, 515), window=100, seed=62),
+    DecodeConfig("g16-one-kv-head", 3, 16, 1, ctx=(0, 31, 2047), paged=True, seed=63),
+    DecodeConfig("page-multiples", 6, 4, 4, ctx=(15, 16, 31, 32, 63, 64), seed=64),
+    DecodeConfig("long-single-seq", 1, 4, 1, ctx=(30000,), paged=True, outliers=0.01, seed=65),
+])
+def test_decode_edge_shapes(gpu, cfg):
+    run_and_check(cfg, gpu)
+
+
+def test_single_key_returns_the_value_exactly(gpu):
+    """One cached key: softmax weight 1, so out = code * v_scale for every code; with a power-of-two scale that is
+    exact in bf16, which checks the kernel's fp8 -> bf16 conversion over all 254 non-NaN codes and the V layout."""
+    dev = gpu
+    hkv, hq = 2, 4
+    cache = Fp8KVCache.contiguous(1, 16, hkv, dev)
+    codes = torch.tensor([c for c in range(256) if c & 0x7F != 0x7F] + [0, 0], dtype=torch.uint8)
+    v_rows = codes.view(hkv, 128)
+    cache.v[0, :, 0, :, 0] = v_rows.to(dev)  # key 0 of the page: quad 0, byte 0 of every dim's dword
+    cache.k[0, :, 0] = torch.randint(0, 0x7E, (hkv, 128), dtype=torch.uint8).to(dev)
+    cache.k_scale[0, :, 0] = 0.01
+    cache.v_scale[0, :, 0] = 0.25
+    q = torch.randn((1, hq, 128), device=dev).to(torch.bfloat16)
+    out = decode_attention(q, cache, torch.tensor([1], dtype=torch.int32, device=dev), max_ctx=16)
+    want = G.E4M3_TABLE[v_rows.numpy()] * np.float32(0.25)
+    got = G.bf16_to_f32(bits(out))
+    for h in range(hq):
+        np.testing.assert_array_equal(got[0, h], want[h // 2])
+
+
+def test_uniform_query_gives_mean_of_values(gpu):
+    """q = 0: every key weighs the same, so out is the mean of the dequantised values of the window."""
+    dev = gpu
+    cfg = DecodeConfig("q0", 2, 4, 2, ctx=(700, 130), paged=True, seed=71)
+    case = build_decode_case(cfg, dev)
+    q = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device=dev)
+    ctx = torch.tensor([700, 130], dtype=torch.int32, device=dev)
+    out = decode_attention(q, case.cache, ctx, max_ctx=701, window=200)
+    k, v, ks, vs = G.gather(oracle_cache(case.cache), table(case.cache), case.cache.max_blocks, np.array([700, 130]),
+                            701)
+    for b, c in enumerate((700, 130)):
+        lo = max(c - 1 - 200, 0)
+        for h in range(4):
+            mean = G.dequantize(v[b, h // 2, lo:c], vs[b, h // 2, lo:c]).astype(np.float64).mean(0)
+            np.testing.assert_allclose(G.bf16_to_f32(bits(out[b, h])), mean, atol=2e-3, rtol=1e-2)
+
+
+def test_split_plan_does_not_change_the_result(gpu):
+    """The same queries under different split plans (max_ctx changes the split size) agree closely."""
+    dev = gpu
+    cfg = DecodeConfig("splits", 4, 8, 2, ctx=(5000, 3000, 200, 4096), paged=True, seed=81)
+    case = build_decode_case(cfg, dev)
+    q = torch.randn((4, 8, 128), device=dev).to(torch.bfloat16)
+    ctx = torch.from_numpy(case.ctx.astype(np.int32)).to(dev)
+    a = decode_attention(q, case.cache, ctx, max_ctx=5000)
+    b = decode_attention(q, case.cache, ctx, max_ctx=case.cache.capacity)
+    torch.testing.assert_close(a.float(), b.float(), atol=4e-3, rtol=2e-2)

@@ -1,0 +1,335 @@
+"""Pins of the CPU oracle (oracle/golden.py) against library routines, closed forms and brute force. CPU only.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term, a wrong sign or index, a transposed
+operand, a wrong rounding mode) fails it; none retypes the oracle's own formula."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import golden as G
+
+
+def bits_of(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# ----------------------------------------------------------------------------------------------- rounding primitives
+
+def special_floats() -> np.ndarray:
+    vals = [0.0, -0.0, 1.0, -1.0, 448.0, -448.0, 463.99, 464.0, 464.00003, 470.0, 480.0, 1e6, np.inf, -np.inf,
+            2.0 ** -6, 2.0 ** -7, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -10, 3 * 2.0 ** -11, 2.0 ** -6 * (1 - 2 ** -24),
+            2.0 ** -100, 1e-40]
+    grid = np.array(vals, np.float32)
+    # every fp32 tie and near-tie around each e4m3 code
+    codes = G.E4M3_TABLE[np.isfinite(G.E4M3_TABLE)]
+    mids = ((codes[:-1].astype(np.float64) + codes[1:]) / 2).astype(np.float32)
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf))])
+    return np.concatenate([grid, -grid, codes, mids, near])
+
+
+def test_e4m3_encode_matches_torch_cast():
+    """Library pin: torch's float32 -> float8_e4m3fn cast (RNE, NaN beyond 464) on specials, every tie between
+    adjacent codes and 2M random bit patterns of all magnitudes."""
+    rng = np.random.default_rng(0)
+    rand = rng.integers(0, 2 ** 32, size=2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    rand = rand[np.isfinite(rand)]
+    scaled = (rng.standard_normal(1_000_000) * 100).astype(np.float32)
+    for x in (special_floats(), rand, scaled):
+        want = torch.from_numpy(x.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        got = G.e4m3_encode(x)
+        nan_want = (want & 0x7F) == 0x7F
+        np.testing.assert_array_equal(nan_want, (got & 0x7F) == 0x7F)
+        np.testing.assert_array_equal(got[~nan_want], want[~nan_want])
+
+
+def test_e4m3_decode_matches_torch_exhaustively():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = G.e4m3_decode(codes)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+    # the format's fixed points: max 448, smallest normal 2^-6, smallest subnormal 2^-9
+    assert G.E4M3_TABLE[0x7E] == 448 and G.E4M3_TABLE[0x08] == 2 ** -6 and G.E4M3_TABLE[0x01] == 2 ** -9
+
+
+def test_e4m3_round_trip_all_codes():
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+    np.testing.assert_array_equal(G.e4m3_encode(G.e4m3_decode(codes)), codes)
+
+
+def test_bf16_bits_matches_torch_cast():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.integers(0, 2 ** 32, 1_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+                        special_floats()])
+    x = x[~np.isnan(x)]
+    want = bits_of(torch.from_numpy(x.copy()).to(torch.bfloat16))
+    np.testing.assert_array_equal(G.bf16_bits(x), want)
+    np.testing.assert_array_equal(G.bf16_to_f32(want), torch.from_numpy(want.view(np.int16)).view(
+        torch.bfloat16).float().numpy())
+
+
+# ----------------------------------------------------------------------------------------------- rotary + row math
+
+def test_rotary_tables_closed_form():
+    theta = 10000.0
+    cos, sin = G.rotary_tables(4096, theta)
+    assert cos.dtype == np.float32 and cos.shape == (4096, 64)
+    np.testing.assert_array_equal(cos[0], 1.0)
+    np.testing.assert_array_equal(sin[0], 0.0)
+    for t, i in [(1, 0), (1, 63), (4095, 0), (4095, 17), (2048, 63), (37, 5)]:
+        ang = t * theta ** (-2 * i / 128)
+        assert cos[t, i] == np.float32(math.cos(ang)) and sin[t, i] == np.float32(math.sin(ang))
+    # frequency 0 rotates by exactly t radians
+    t = np.arange(4096)
+    np.testing.assert_array_equal(cos[:, 0], np.cos(t.astype(np.float64)).astype(np.float32))
+
+
+def test_sum_squares_accuracy_and_exact_cases():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((1000, 128)).astype(np.float32)
+    exact = (x.astype(np.float64) ** 2).sum(-1)
+    got = G.sum_squares(x).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= exact * 9 * 2.0 ** -24)  # tree depth 8 + product rounding
+    np.testing.assert_array_equal(G.sum_squares(np.full((3, 128), 0.5, np.float32)), np.float32(32.0))
+    one_hot = np.zeros((128, 128), np.float32)
+    one_hot[np.arange(128), np.arange(128)] = 3.0
+    np.testing.assert_array_equal(G.sum_squares(one_hot), np.float32(9.0))
+
+
+def bf16_ulp(y: np.ndarray) -> np.ndarray:
+    e = np.floor(np.log2(np.maximum(np.abs(y), 1e-30)))
+    return 2.0 ** (e - 7)
+
+
+def random_bf16(shape, seed, scale=1.0) -> np.ndarray:
+    g = torch.Generator().manual_seed(seed)
+    return bits_of((torch.randn(shape, generator=g) * scale).to(torch.bfloat16))
+
+
+def test_qk_norm_rope_identity_rotation_is_rms_norm():
+    """pos 0 (cos 1, sin 0), gain 1: y = x / sqrt(mean x² + eps), within one bf16 rounding of the fp64 value."""
+    x = random_bf16((64, 128), 3, scale=3.0)
+    y = G.bf16_to_f32(G.qk_norm_rope(x, np.ones(128, np.float32), np.ones(64, np.float32),
+                                     np.zeros(64, np.float32))).astype(np.float64)
+    xf = G.bf16_to_f32(x).astype(np.float64)
+    want = xf / np.sqrt((xf ** 2).mean(-1, keepdims=True) + float(G.EPS))
+    assert np.all(np.abs(y - want) <= bf16_ulp(want) * 0.5 + np.abs(want) * 2.0 ** -20)
+
+
+def test_qk_norm_rope_one_hot_rstd():
+    """x = c e_j: r = 1 / sqrt(c²/128 + eps) so y_j = c r exactly rounded; other dims 0."""
+    for j in (0, 5, 63, 64, 127):
+        x = np.zeros(128, np.float32)
+        x[j] = 2.0
+        y = G.bf16_to_f32(G.qk_norm_rope(G.bf16_bits(x), np.ones(128, np.float32), np.ones(64, np.float32),
+                                         np.zeros(64, np.float32)))
+        want = 2.0 / math.sqrt(4.0 / 128 + float(G.EPS))
+        assert abs(y[j] - want) <= bf16_ulp(np.array(want)) / 2
+        assert np.count_nonzero(y) == 1
+
+
+def test_qk_norm_rope_pure_pair_rotates_by_minus_theta():
+    """A row holding only the pair (i, i+64) rotates in that plane by -t θ^(-2i/128) (rotation by -θ, qk_row.cuh:3)
+    with its length kept; the gain scales the normed value per dim before the rotation."""
+    cos, sin = G.rotary_tables(512, 10000.0)
+    for t, i in [(1, 0), (7, 3), (300, 40), (511, 63)]:
+        x = np.zeros(128, np.float32)
+        x[i], x[i + 64] = 1.0, 0.5
+        g = np.ones(128, np.float32)
+        g[i + 64] = 2.0  # n = (r, 2 * 0.5 r): the gained pair is (r, r)
+        y = G.bf16_to_f32(G.qk_norm_rope(G.bf16_bits(x), g, cos[t], sin[t])).astype(np.float64)
+        r = 1 / math.sqrt((1 + 0.25) / 128 + float(G.EPS))
+        ang = t * 10000.0 ** (-2 * i / 128)
+        want1 = r * math.cos(ang) + r * math.sin(ang)
+        want2 = r * math.cos(ang) - r * math.sin(ang)
+        assert abs(y[i] - want1) <= bf16_ulp(np.array(want1)) + 1e-5
+        assert abs(y[i + 64] - want2) <= bf16_ulp(np.array(want2)) + 1e-5
+        assert np.count_nonzero(y) <= 2
+
+
+def test_qk_norm_rope_preserves_norm_and_is_row_local():
+    cos, sin = G.rotary_tables(64, 1e6)
+    x = random_bf16((8, 6, 128), 4)
+    pos = np.arange(8) * 7
+    y = G.qk_norm_rope(x, np.ones(128, np.float32), cos[pos][:, None], sin[pos][:, None])
+    yf = G.bf16_to_f32(y).astype(np.float64)
+    np.testing.assert_allclose(np.sqrt((yf ** 2).mean(-1)), 1.0, rtol=4e-3)
+    # row locality: one row alone gives the same bits as within the batch
+    np.testing.assert_array_equal(G.qk_norm_rope(x[3, 2], np.ones(128, np.float32), cos[pos[3]], sin[pos[3]]),
+                                  y[3, 2])
+
+
+# ----------------------------------------------------------------------------------------------- quantisation
+
+def test_quantize_rows_known_answers():
+    rng = np.random.default_rng(5)
+    # absmax 448 * 2^k: the scale is exactly 2^k and codes are the plain e4m3 rounding of x / 2^k
+    for k in (-3, 0, 2):
+        x = (rng.uniform(-448, 448, (4, 128)) * 2.0 ** k).astype(np.float32)
+        x[:, 7] = 448 * 2.0 ** k
+        xb = G.bf16_bits(x)
+        codes, scale = G.quantize_rows(xb)
+        np.testing.assert_array_equal(scale, np.float32(2.0 ** k))
+        want = torch.from_numpy(G.bf16_to_f32(xb) / np.float32(2.0 ** k)).to(torch.float8_e4m3fn).view(
+            torch.uint8).numpy()
+        np.testing.assert_array_equal(codes, want)
+    # zero row: scale 0, codes 0, dequantises to 0
+    codes, scale = G.quantize_rows(np.zeros((2, 128), np.uint16))
+    assert np.all(codes == 0) and np.all(scale == 0)
+    assert np.all(G.dequantize(codes, scale) == 0)
+
+
+def test_quantize_rows_absmax_maps_to_448_and_error_bound():
+    x = random_bf16((512, 128), 6)
+    x[::7, 3] = G.bf16_bits(np.float32(-8.0))  # outliers move only the scale
+    codes, scale = G.quantize_rows(x)
+    xf = G.bf16_to_f32(x)
+    amax = np.abs(xf).argmax(-1)
+    np.testing.assert_array_equal(codes[np.arange(512), amax] & 0x7F, 0x7E)
+    xq = G.dequantize(codes, scale)
+    # half an e4m3 step: 2^-4 relative for normals (plus the dequantise rounding), 2^-10 scale below 2^-6 scale
+    bound = np.maximum(np.abs(xf) * (2.0 ** -4 + 2.0 ** -23), scale[:, None] * 2.0 ** -10) * (1 + 1e-6)
+    assert np.all(np.abs(xq - xf) <= bound)
+    assert not np.any(np.isnan(xq))
+
+
+# ----------------------------------------------------------------------------------------------- cache layout
+
+def test_cache_layout_byte_offsets():
+    """V's quad-transposed page: key t, dim d at byte (t/4)*512 + d*4 + t%4 of its (block, head) 2 KiB tile."""
+    c = G.PagedCache(3, 2)
+    kc = np.arange(128, dtype=np.uint8)
+    vc = (np.arange(128) + 100).astype(np.uint8)
+    c.write(np.array([2]), 1, np.array([13]), kc[None], np.float32(0.5), vc[None], np.float32(0.25))
+    flat_k = c.k.reshape(-1)
+    flat_v = c.v.reshape(-1)
+    tile = (2 * 2 + 1) * 2048
+    np.testing.assert_array_equal(flat_k[tile + 13 * 128: tile + 14 * 128], kc)
+    for d in (0, 1, 77, 127):
+        assert flat_v[tile + (13 // 4) * 512 + d * 4 + 13 % 4] == vc[d]
+    assert c.k_scale.reshape(-1)[(2 * 2 + 1) * 16 + 13] == 0.5
+    assert np.count_nonzero(flat_v) == 128 and np.count_nonzero(flat_k) == 127
+
+
+def test_append_then_gather_paged_equals_contiguous():
+    """A random page permutation stores the same rows as the contiguous layout (brute-force comparison)."""
+    hq, hkv, n_seq, max_blocks = 4, 2, 3, 4
+    cos, sin = G.rotary_tables(64, 10000.0)
+    rng = np.random.default_rng(7)
+    pos = np.concatenate([np.arange(L) for L in (17, 64, 5)])
+    seq = np.concatenate([np.full(L, b) for b, L in enumerate((17, 64, 5))])
+    qkv = random_bf16((len(pos), (hq + 2 * hkv) * 128), 8)
+    gq, gk = rng.uniform(0.5, 1.5, 128).astype(np.float32), rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    contig = G.PagedCache(n_seq * max_blocks, hkv)
+    q1 = G.append(contig, qkv, pos, seq, gq, gk, cos, sin, hq, hkv, None, max_blocks)
+    table = rng.permutation(n_seq * max_blocks).reshape(n_seq, max_blocks).astype(np.int32)
+    paged = G.PagedCache(n_seq * max_blocks, hkv)
+    q2 = G.append(paged, qkv, pos, seq, gq, gk, cos, sin, hq, hkv, table, max_blocks)
+    np.testing.assert_array_equal(q1, q2)
+    ctx = np.array([17, 64, 5])
+    a = G.gather(contig, None, max_blocks, ctx, 64)
+    b = G.gather(paged, table, max_blocks, ctx, 64)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    # the gathered rows are the directly quantised rows (q/k norm+rope'd at their positions, v as is)
+    heads = qkv.reshape(len(pos), hq + 2 * hkv, 128)
+    k_bits = G.qk_norm_rope(heads[:, hq:hq + hkv], gk, cos[pos][:, None], sin[pos][:, None])
+    kc, ks = G.quantize_rows(k_bits)
+    vc, vs = G.quantize_rows(heads[:, hq + hkv:])
+    i = 17 + 9  # sequence 1, position 9
+    np.testing.assert_array_equal(a[0][1, :, 9], kc[i])
+    np.testing.assert_array_equal(a[1][1, :, 9], vc[i])
+    np.testing.assert_array_equal(a[2][1, :, 9], ks[i])
+    np.testing.assert_array_equal(a[3][1, :, 9], vs[i])
+    # untouched positions stay zero
+    assert np.all(a[0][2, :, 5:] == 0)
+
+
+# ----------------------------------------------------------------------------------------------- attention
+
+def make_cache(ctx, hkv, seed, table=False):
+    max_blocks = -(-max(ctx) // G.PAGE)
+    c = G.PagedCache(len(ctx) * max_blocks, hkv)
+    rng = np.random.default_rng(seed)
+    bt = rng.permutation(len(ctx) * max_blocks).reshape(len(ctx), max_blocks).astype(np.int32) if table else None
+    for b, L in enumerate(ctx):
+        t = np.arange(L)
+        blk = G.PagedCache.block_of(np.full(L, b), t, bt, max_blocks)
+        for h in range(hkv):
+            kc, ks = G.quantize_rows(random_bf16((L, 128), seed * 100 + b * 10 + h))
+            vc, vs = G.quantize_rows(random_bf16((L, 128), seed * 100 + b * 10 + h + 5))
+            c.write(blk, h, t % G.PAGE, kc, ks, vc, vs)
+    return c, bt, max_blocks
+
+
+def test_decode_attention_special_cases():
+    hq, hkv = 4, 2
+    scale = 128 ** -0.5
+    c, bt, mb = make_cache([1, 40, 40], hkv, 9)
+    q = random_bf16((3, hq, 128), 10)
+    out = G.decode_attention(q, c, bt, mb, np.array([1, 40, 40]), -1, hq, hkv, scale)
+    k, v, ks, vs = G.gather(c, bt, mb, np.array([1, 40, 40]), 40)
+    # one key: the output is that key's dequantised value, for every query head of the kv head
+    for h in range(hq):
+        np.testing.assert_allclose(out[0, h], G.dequantize(v[0, h // 2, 0], vs[0, h // 2, 0]), rtol=1e-12)
+    # q = 0: uniform weights, the mean of V over the window
+    q0 = np.zeros_like(q)
+    out0 = G.decode_attention(q0, c, bt, mb, np.array([1, 40, 40]), 9, hq, hkv, scale)
+    want = G.dequantize(v[1, 0, 30:40], vs[1, 0, 30:40]).astype(np.float64).mean(0)
+    np.testing.assert_allclose(out0[1, 0], want, rtol=1e-12, atol=1e-15)
+    # window >= context is full attention
+    full = G.decode_attention(q, c, bt, mb, np.array([1, 40, 40]), 39, hq, hkv, scale)
+    np.testing.assert_array_equal(full, out)
+
+
+def test_decode_attention_brute_force_and_gqa_mapping():
+    """Per-key Python loop (exp / sum), and GQA equals MHA over kv heads repeated G times."""
+    hq, hkv = 6, 2
+    scale = 0.1
+    ctx = np.array([23, 7])
+    c, bt, mb = make_cache(list(ctx), hkv, 11, table=True)
+    q = random_bf16((2, hq, 128), 12)
+    out = G.decode_attention(q, c, bt, mb, ctx, 5, hq, hkv, scale)
+    k, v, ks, vs = G.gather(c, bt, mb, ctx, 23)
+    qf = G.bf16_to_f32(q).astype(np.float64)
+    for b in range(2):
+        p = int(ctx[b]) - 1
+        for h in range(hq):
+            kh = h // 3
+            keys = range(max(p - 5, 0), p + 1)
+            w = [math.exp(float(qf[b, h] @ G.dequantize(k[b, kh, j], ks[b, kh, j]).astype(np.float64)) * scale)
+                 for j in keys]
+            acc = sum(wj * G.dequantize(v[b, kh, j], vs[b, kh, j]).astype(np.float64) for wj, j in zip(w, keys))
+            np.testing.assert_allclose(out[b, h], acc / sum(w), rtol=1e-10, atol=1e-12)
+    # MHA copy: kv head h of the 6-head cache is kv head h // 3 of the 2-head one
+    mha = G.PagedCache(c.num_blocks, hq)
+    for h in range(hq):
+        mha.k[:, h], mha.v[:, h] = c.k[:, h // 3], c.v[:, h // 3]
+        mha.k_scale[:, h], mha.v_scale[:, h] = c.k_scale[:, h // 3], c.v_scale[:, h // 3]
+    np.testing.assert_allclose(G.decode_attention(q, mha, bt, mb, ctx, 5, hq, hq, scale), out, rtol=1e-13)
+
+
+def test_prefill_attention_reduces_to_decode_and_is_causal():
+    hq, hkv = 4, 1
+    scale = 128 ** -0.5
+    ctx = [48, 33]
+    c, bt, mb = make_cache(ctx, hkv, 13, table=True)
+    q = random_bf16((16 + 5, hq, 128), 14)
+    cu = np.array([0, 16, 21])
+    start = np.array([32, 28])  # chunk rows are the sequences' last positions
+    out = G.prefill_attention(q, cu, start, c, bt, mb, -1, hq, hkv, scale)
+    for b, (r0, r1) in enumerate([(0, 16), (16, 21)]):
+        for i in range(r1 - r0):
+            # a batch of the one sequence b: its own block-table row
+            d = G.decode_attention(q[r0 + i][None], c, bt[b:b + 1], mb, np.array([start[b] + i + 1]), -1, hq, hkv,
+                                   scale)
+            np.testing.assert_allclose(out[r0 + i], d[0], rtol=1e-12)
+    # causality: changing keys after a row's position leaves that row unchanged
+    c.k[bt[0, 2], 0, 15] ^= 0x11  # position 47 of sequence 0
+    out2 = G.prefill_attention(q, cu, start, c, bt, mb, -1, hq, hkv, scale)
+    np.testing.assert_array_equal(out2[:15], out[:15])
+    assert not np.array_equal(out2[15], out[15])
