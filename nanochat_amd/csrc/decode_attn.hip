@@ -69,6 +69,9 @@ __device__ __forceinline__ KeyRange key_range(const DecodeArgs &a, int b) {
     return r;
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
 /* 8 fp8 codes (two dwords, byte order = element order) -> 8 bf16, exact. */
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
     const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
@@ -76,6 +79,15 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
     const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
     const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
     return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+/* 8 fp8 codes -> 8 fp16, exact (every e4m3fn value is an fp16 value). */
+__device__ __forceinline__ f16x8 fp8x8_to_f16(uint32_t w0, uint32_t w1) {
+    const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+    const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+    const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+    const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 /* One page's fragments for this lane: K row bytes, V quad bytes, the 4 keys' scales. */
@@ -109,9 +121,8 @@ __device__ __forceinline__ f32x4 page_scores(const Page &pg, const bf16x8 *qop) 
 
 __device__ __forceinline__ uint32_t v_dword(const Page &pg, int bb) { return bb < 4 ? pg.v0[bb] : pg.v1[bb - 4]; }
 
-__device__ __forceinline__ int page_block(const DecodeArgs &a, int b, int page, int last_page) {
-    return page <= last_page ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, b, page) : -1;
-}
+/* 2^e as fp32 for e in [-126, 127] (exponent bits only). */
+__device__ __forceinline__ float exp2i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
 __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -128,7 +139,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     }
     if (split >= r.n_splits) return;
     const int pg_begin = r.first_page + split * a.split_pages;
-    const int pg_end = min(pg_begin + a.split_pages, r.last_page + 1);
+    const int npg = min(a.split_pages, r.last_page + 1 - pg_begin); /* 1..64 pages */
 
     bf16x8 qop[4];
     if (n < a.group) {
@@ -140,44 +151,63 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) qop[c] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
     }
+    /* lane i holds the block of the split's page i (-1: none), read back by v_readlane */
+    const int my_blk = lane < npg ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, b, pg_begin + lane) : -1;
 
     f32x4 o[8];
 #pragma unroll
     for (int bb = 0; bb < 8; bb++) o[bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    /* running softmax max m and per-lane sum l (probability units); o is held in units of 2^(e_ref - 126),
+     * e_ref the largest v_scale exponent seen, so that p * v_scale * 2^(126 - e_ref) <= 1 fits fp16 */
     float m = -INFINITY, l = 0.f;
+    int e_ref = 0;
 
-    int blk0 = page_block(a, b, pg_begin, pg_end - 1), blk1 = page_block(a, b, pg_begin + 1, pg_end - 1);
-    Page c0, c1, n0, n1;
-    load_page(a, blk0 < 0 ? 0 : blk0, h, n, j, c0);
-    load_page(a, blk1 < 0 ? (blk0 < 0 ? 0 : blk0) : blk1, h, n, j, c1);
+    int blk0 = __builtin_amdgcn_readlane(my_blk, 0);
+    int blk1 = npg > 1 ? __builtin_amdgcn_readlane(my_blk, 1) : -1;
+    Page c0, c1;
+    load_page(a, max(blk0, 0), h, n, j, c0);
+    load_page(a, blk1 >= 0 ? blk1 : max(blk0, 0), h, n, j, c1);
 
-    for (int pg = pg_begin; pg < pg_end; pg += 2) {
-        const bool next = pg + 2 < pg_end;
-        int nb0 = -1, nb1 = -1;
-        if (next) {
-            nb0 = page_block(a, b, pg + 2, pg_end - 1);
-            nb1 = page_block(a, b, pg + 3, pg_end - 1);
-            load_page(a, nb0 < 0 ? 0 : nb0, h, n, j, n0);
-            load_page(a, nb1 < 0 ? (nb0 < 0 ? 0 : nb0) : nb1, h, n, j, n1);
-        }
+    const int steps = (npg + 1) >> 1;
+    for (int st = 0; st < steps; st++) {
+        /* the next step's pages, always loaded (the last step re-reads its own last page) so the wait before
+         * this step's math leaves exactly those loads in flight */
+        const int i0 = min(2 * st + 2, npg - 1), i1 = min(2 * st + 3, npg - 1);
+        const int nb0 = __builtin_amdgcn_readlane(my_blk, i0), nb1 = __builtin_amdgcn_readlane(my_blk, i1);
+        Page n0, n1;
+        load_page(a, max(nb0, 0), h, n, j, n0);
+        load_page(a, max(nb1, 0), h, n, j, n1);
+
         const f32x4 s0 = page_scores(c0, qop), s1 = page_scores(c1, qop);
-        float sv[8];
+        const int base = (pg_begin + 2 * st) * NC_PAGE + 4 * j; /* key of (page 0, i = 0) for this lane */
+        const int lo = r.begin - base, hi = r.p - base;         /* valid i of page 0 in [lo, hi], page 1 -16 */
+        float sv[8], vsv[8];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int k0 = pg * NC_PAGE + 4 * j + i, k1 = k0 + NC_PAGE;
-            const bool ok0 = blk0 >= 0 && k0 >= r.begin && k0 <= r.p;
-            const bool ok1 = blk1 >= 0 && k1 >= r.begin && k1 <= r.p;
+            const bool ok0 = blk0 >= 0 && i >= lo && i <= hi;
+            const bool ok1 = blk1 >= 0 && i + NC_PAGE >= lo && i + NC_PAGE <= hi;
             sv[i] = ok0 ? s0[i] * (c0.ks[i] * a.score_scale) : -INFINITY;
             sv[4 + i] = ok1 ? s1[i] * (c1.ks[i] * a.score_scale) : -INFINITY;
+            vsv[i] = ok0 ? c0.vs[i] : 0.f;
+            vsv[4 + i] = ok1 ? c1.vs[i] : 0.f;
         }
-        float mx = sv[0];
+        float mx = sv[0], vmax = vsv[0];
 #pragma unroll
-        for (int i = 1; i < 8; i++) mx = fmaxf(mx, sv[i]);
+        for (int i = 1; i < 8; i++) {
+            mx = fmaxf(mx, sv[i]);
+            vmax = fmaxf(vmax, vsv[i]);
+        }
         mx = fmaxf(mx, shfl_xor_f(mx, 16));
         mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        vmax = fmaxf(vmax, shfl_xor_f(vmax, 16));
+        vmax = fmaxf(vmax, shfl_xor_f(vmax, 32));
         const float m_new = fmaxf(m, mx);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        const int e_new = max(e_ref, (int)(__float_as_uint(vmax) >> 23));
+        const float w = exp2i(126 - e_new);                          /* p * vs * w <= 1 */
+        const float rescale = alpha * exp2i(max(e_ref - e_new, -126)); /* old units -> new units */
+        e_ref = e_new;
         float pv[8], ps = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -186,31 +216,32 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
         }
         l = l * alpha + ps;
         m = m_new;
-        const bf16x8 pop = {(__bf16)(pv[0] * c0.vs[0]), (__bf16)(pv[1] * c0.vs[1]), (__bf16)(pv[2] * c0.vs[2]),
-                            (__bf16)(pv[3] * c0.vs[3]), (__bf16)(pv[4] * c1.vs[0]), (__bf16)(pv[5] * c1.vs[1]),
-                            (__bf16)(pv[6] * c1.vs[2]), (__bf16)(pv[7] * c1.vs[3])};
+        f16x8 pop;
 #pragma unroll
-        for (int bb = 0; bb < 8; bb++) {
-            o[bb] *= alpha;
-            o[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(v_dword(c0, bb), v_dword(c1, bb)), pop,
-                                                            o[bb], 0, 0, 0);
+        for (int i = 0; i < 8; i++) pop[i] = (_Float16)(pv[i] * (vsv[i] * w));
+        if (!__all(rescale == 1.0f)) {
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) o[bb] *= rescale;
         }
-        if (next) {
-            c0 = n0;
-            c1 = n1;
-            blk0 = nb0;
-            blk1 = nb1;
-        }
+#pragma unroll
+        for (int bb = 0; bb < 8; bb++)
+            o[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16(v_dword(c0, bb), v_dword(c1, bb)), pop, o[bb],
+                                                           0, 0, 0);
+        c0 = n0;
+        c1 = n1;
+        blk0 = 2 * st + 2 < npg ? nb0 : -1;
+        blk1 = 2 * st + 3 < npg ? nb1 : -1;
     }
 
     l += shfl_xor_f(l, 16);
     l += shfl_xor_f(l, 32);
     if (n >= a.group) return;
     const int head = h * a.group + n;
+    const float unit = exp2i(e_ref - 126); /* o * unit: Σ p v in value units */
     /* lane (j, n) holds dims (4j + i) * 8 + bb of head n: 8 contiguous dims per i */
     if (r.n_splits == 1) {
         bf16_t *dst = a.out + ((size_t)b * a.hq + head) * NC_HEAD_DIM;
-        const float inv = 1.0f / l;
+        const float inv = unit / l;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float v[8];
@@ -224,9 +255,10 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     float *dst = a.ws_o + slot * NC_HEAD_DIM;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        f32x4 lo = {o[0][i], o[1][i], o[2][i], o[3][i]}, hi = {o[4][i], o[5][i], o[6][i], o[7][i]};
-        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[0] = lo;
-        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[1] = hi;
+        f32x4 lo4 = {o[0][i] * unit, o[1][i] * unit, o[2][i] * unit, o[3][i] * unit};
+        f32x4 hi4 = {o[4][i] * unit, o[5][i] * unit, o[6][i] * unit, o[7][i] * unit};
+        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[0] = lo4;
+        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[1] = hi4;
     }
     if (j == 0) {
         a.ws_ml[2 * slot] = m;
@@ -256,14 +288,25 @@ __global__ void __launch_bounds__(DEC_THREADS) k_merge(DecodeArgs a) {
     *reinterpret_cast<uint32_t *>(dst) = f32_to_bf16(acc0 * inv) | (f32_to_bf16(acc1 * inv) << 16);
 }
 
+/* Waves the split plan aims for; NC_DECODE_TARGET_WAVES overrides it (a tuning knob, read once). */
+static int target_waves() {
+    static const int waves = [] {
+        const char *e = getenv("NC_DECODE_TARGET_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : DEC_TARGET_WAVES;
+    }();
+    return waves;
+}
+
 /* The split plan, a function of the shape only so the workspace size is known before the call. */
 static void decode_plan(int B, int hkv, int max_ctx, int *split_pages, int *max_splits) {
     const int pages = (max_ctx + NC_PAGE - 1) / NC_PAGE + 1; /* +1: a window can start mid-page */
     long long units = (long long)B * hkv;
-    int per_seq = (int)((DEC_TARGET_WAVES + units - 1) / units);
+    int per_seq = (int)((target_waves() + units - 1) / units);
     if (per_seq < 1) per_seq = 1;
     int sp = (pages + per_seq - 1) / per_seq;
     sp = sp < 2 ? 2 : (sp + 1) & ~1; /* whole two-page steps */
+    if (sp > 64) sp = 64;          /* one lane per page holds the split's block ids */
     *split_pages = sp;
     *max_splits = (pages + sp - 1) / sp;
 }
@@ -292,6 +335,8 @@ extern "C" int nc_decode_attn_fp8(const void *q, const uint8_t *k_cache, const u
     NC_REQUIRE(max_ctx > 0 && max_ctx <= max_blocks * NC_PAGE, "max_ctx %d outside [1, %d]", max_ctx,
                max_blocks * NC_PAGE);
     NC_REQUIRE(q && k_cache && v_cache && k_scale && v_scale && ctx_len && out, "null argument");
+    NC_REQUIRE(((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)k_scale |
+                (uintptr_t)v_scale | (uintptr_t)workspace) % 16 == 0, "tensors must be 16-byte aligned");
     const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
     NC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "workspace %lld bytes, %lld needed",
                workspace_bytes, need);

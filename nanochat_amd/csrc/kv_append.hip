@@ -163,6 +163,7 @@ extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, co
                "row_stride %lld must hold (hq + 2 hkv) * 128 elements and keep 16-byte alignment", row_stride);
     NC_REQUIRE(rope_len > 0, "rope_len = %d", rope_len);
     NC_REQUIRE(n == 0 || (qkv && pos && seq && q_gain && k_gain && cos && sin && q_out), "null argument");
+    NC_REQUIRE(((uintptr_t)qkv | (uintptr_t)q_out) % 16 == 0, "qkv and q_out must be 16-byte aligned");
     AppendArgs a = {};
     a.qkv = (const bf16_t *)qkv; a.row_stride = row_stride; a.n = n; a.pos = pos; a.seq = seq;
     a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
@@ -184,6 +185,7 @@ extern "C" int nc_kv_store_fp8(const void *k, const void *v, long long row_strid
     NC_REQUIRE(row_stride >= (long long)hkv * NC_HEAD_DIM && row_stride % 8 == 0,
                "row_stride %lld must hold hkv * 128 elements and keep 16-byte alignment", row_stride);
     NC_REQUIRE(n == 0 || (k && v && pos && seq), "null argument");
+    NC_REQUIRE(((uintptr_t)k | (uintptr_t)v) % 16 == 0, "k and v must be 16-byte aligned");
     AppendArgs a = {};
     a.k_rows = (const bf16_t *)k; a.v_rows = (const bf16_t *)v; a.row_stride = row_stride; a.n = n;
     a.pos = pos; a.seq = seq; a.hkv = hkv;
