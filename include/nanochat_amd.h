@@ -10,10 +10,12 @@
  * Device-side, rows or keys whose position, sequence or block is out of range are skipped, never written or read
  * out of bounds.
  *
- * Cache layout (per layer), PAGE = 16 positions per block, D = 128:
- *   k_cache  uint8 [num_blocks][Hkv][16][128]   row-major keys
- *   v_cache  uint8 [num_blocks][Hkv][4][128][4] quad-transposed: key t, dim d at byte (t/4)*512 + d*4 + t%4
- *   k_scale, v_scale  fp32 [num_blocks][Hkv][16]   one absmax/448 scale per (token, kv head)
+ * Cache layout (per layer), PAGE = 16 positions per block, D = 128: one pool, uint8 [num_blocks][Hkv][4224]; the
+ * (block, kv head) tile is
+ *   [0, 2048)     K codes [16][128], row-major
+ *   [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + (t/4)*512 + d*4 + t%4
+ *   [4096, 4160)  K scales fp32 [16], one absmax/448 scale per (token, kv head)
+ *   [4160, 4224)  V scales fp32 [16]
  *   block_table int32 [num_seqs][max_blocks], or NULL: contiguous, sequence s's page i is block s*max_blocks + i
  * Codes are OCP float8 e4m3fn, rounded to nearest even from x / scale; the reference caches bf16 instead
  * (model/kernels/decode.cu:4-7, 726).
@@ -49,40 +51,40 @@ void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, v
  * Replaces: k_prologue + attn_prologue, model/kernels/decode.cu:476-507,550-565 (which cache bf16). */
 int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, const int32_t *pos, const int32_t *seq,
                      const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
-                     int hq, int hkv, void *q_out, uint8_t *k_cache, uint8_t *v_cache, float *k_scale,
-                     float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
-                     void *stream);
+                     int hq, int hkv, void *q_out, uint8_t *cache, const int32_t *block_table, int max_blocks,
+                     int num_blocks, int num_seqs, void *stream);
 
 /* Quantise-and-store of final K and V rows (bf16 [n][row_stride], Hkv heads of 128, no norm or rotation) at
  * (seq[n], pos[n]).
  * Replaces: the cache write of DynamicCache.update, inference/modeling_nanochat.py:95-96 (bf16 there). */
 int nc_kv_store_fp8(const void *k, const void *v, long long row_stride, int n, const int32_t *pos,
-                    const int32_t *seq, int hkv, uint8_t *k_cache, uint8_t *v_cache, float *k_scale,
-                    float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
-                    void *stream);
+                    const int32_t *seq, int hkv, uint8_t *cache, const int32_t *block_table, int max_blocks,
+                    int num_blocks, int num_seqs, void *stream);
 
 /* Gather of sequences 0..B-1: codes of the first ctx_len[b] positions to k_out, v_out (uint8
  * [B][Hkv][max_ctx][128], both row-major) and scales to ks_out, vs_out (fp32 [B][Hkv][max_ctx]); later
  * positions are zero.
  * Replaces: the contiguous per-slot cache read of k_attn's load_run, model/kernels/decode.cu:581-591, and the
  * prompt copies of prompt_copy, decode.cu:1053-1067. */
-int nc_kv_gather_fp8(const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale, const float *v_scale,
-                     const int32_t *block_table, int max_blocks, int num_blocks, const int32_t *ctx_len, int B,
-                     int hkv, int max_ctx, uint8_t *k_out, uint8_t *v_out, float *ks_out, float *vs_out,
-                     void *stream);
+int nc_kv_gather_fp8(const uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks,
+                     const int32_t *ctx_len, int B, int hkv, int max_ctx, uint8_t *k_out, uint8_t *v_out,
+                     float *ks_out, float *vs_out, void *stream);
 
-/* Workspace bytes nc_decode_attn_fp8 needs for this shape (0 when no sequence is split). */
+/* Workspace bytes nc_decode_attn_fp8 needs for B sequences of hq / hkv heads (independent of max_ctx and of the
+ * device): per-segment counters, then a partial-result slot per wave and per (sequence, kv head). */
 long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx);
 
 /* Single-token decode attention: query b (bf16 q [B][Hq][128]) at position p = ctx_len[b] - 1 attends keys
  * [max(p - window, 0), p] of sequence b (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores
  * times sm_scale, fp32 softmax, bf16 out [B][Hq][128]. ctx_len values above max_ctx are clamped to it; a
- * sequence with ctx_len <= 0 gets a zero row. Hq / Hkv <= 16.
+ * sequence with ctx_len <= 0 gets a zero row. Hq / Hkv <= 16. The workspace (nc_decode_workspace_bytes) holds
+ * partial results between the call's two kernels: calls in one stream may share it, calls that may overlap (two
+ * streams) need one each. The pool's code bytes must be valid e4m3fn codes (a zero-initialised pool written only
+ * by nc_kv_append_fp8 / nc_kv_store_fp8 is).
  * Replaces: k_attn, model/kernels/decode.cu:567-675 (bf16 MHA, one block per (head, slot)). */
-int nc_decode_attn_fp8(const void *q, const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,
-                       const float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks,
-                       const int32_t *ctx_len, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
-                       void *out, void *workspace, long long workspace_bytes, void *stream);
+int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int32_t *block_table, int max_blocks,
+                       int num_blocks, const int32_t *ctx_len, int window, int B, int hq, int hkv, int max_ctx,
+                       float sm_scale, void *out, void *workspace, long long workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -20,12 +20,18 @@ def decode_workspace_bytes(batch: int, hq: int, hkv: int, max_ctx: int) -> int:
     return int(hip_library().nc_decode_workspace_bytes(batch, hq, hkv, max_ctx))
 
 
+def decode_workspace(batch: int, hq: int, hkv: int, max_ctx: int, device) -> Tensor:
+    """A workspace for decode_attention: partial results between its two kernels. Calls in one stream (and graph
+    replays) may share it; calls that may overlap on two streams need one each."""
+    return torch.zeros(max(decode_workspace_bytes(batch, hq, hkv, max_ctx), 1), dtype=torch.uint8, device=device)
+
+
 def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: int, window: int = -1,
                      sm_scale: float | None = None, out: Tensor | None = None,
                      workspace: Tensor | None = None) -> Tensor:
     """q bf16 [B][Hq][128] (normed and rotated, e.g. Fp8KVCache.append's q_out); ctx_len int32 [B] on the GPU, each
-    at most max_ctx (an upper bound the caller knows on the host: it sizes the grid and the workspace); window: keys
-    before the query, < 0 for all. Returns bf16 [B][Hq][128]."""
+    at most max_ctx (larger values are clamped to it); window: keys before the query, < 0 for all. workspace: from
+    decode_workspace, allocated per call if None. Returns bf16 [B][Hq][128]."""
     _require(q, "q", torch.bfloat16, 3)
     B, hq, D = q.shape
     if D != HEAD_DIM:
@@ -44,12 +50,11 @@ def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: 
             raise ValueError("out must have q's shape")
     need = decode_workspace_bytes(B, hq, cache.hkv, max_ctx)
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        workspace = decode_workspace(B, hq, cache.hkv, max_ctx, q.device)
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
     lib = hip_library()
-    check(lib.nc_decode_attn_fp8(pointer(q), pointer(cache.k), pointer(cache.v), pointer(cache.k_scale),
-                                 pointer(cache.v_scale), pointer(cache.block_table), cache.max_blocks,
+    check(lib.nc_decode_attn_fp8(pointer(q), pointer(cache.pages), pointer(cache.block_table), cache.max_blocks,
                                  cache.num_blocks, pointer(ctx_len), window, B, hq, cache.hkv, max_ctx, scale,
                                  pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
                                  stream()))

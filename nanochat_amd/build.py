@@ -23,8 +23,11 @@ STAMP = LIBRARY.with_suffix(".so.sha256")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere (hipcc would otherwise form them from float2 code).
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs, so the softmax rescales of the decode kernel's output
+# accumulators need no AGPR <-> VGPR copies.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{PACKAGE.parent / 'include'}"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form",
+         f"-I{PACKAGE.parent / 'include'}"]
 
 
 def sources() -> list[Path]:
@@ -32,7 +35,10 @@ def sources() -> list[Path]:
 
 
 def digest() -> str:
-    h = hashlib.sha256(" ".join([HIPCC, *FLAGS]).encode())
+    """Of the command (with the repository-relative include path, so a copy of the tree elsewhere, e.g. on the GPU
+    box, sees the same digest) and of every source and header."""
+    flags = [f.replace(str(PACKAGE.parent), ".") for f in FLAGS]
+    h = hashlib.sha256(" ".join([os.path.basename(HIPCC), *flags]).encode())
     for f in sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(PACKAGE.parent / "include").glob("*.h")]):
         h.update(f.name.encode())
         h.update(f.read_bytes())

@@ -35,7 +35,8 @@ extern "C" const char *nc_last_error(void) { return nc_error; }
 
 extern "C" int nc_abi_version(void) { return 1; }
 
-/* Write this lane's 16 codes of a quantised row into the K tile (row-major) or the V tile (quad-transposed). */
+/* Write this lane's 16 codes of a quantised row into the tile's K region (row-major) or V region
+ * (quad-transposed). */
 __device__ __forceinline__ void write_codes(uint8_t *tile, int t, int g, uint64_t c1, uint64_t c2, bool is_v) {
     if (!is_v) {
         *reinterpret_cast<uint64_t *>(tile + t * NC_HEAD_DIM + 8 * g) = c1;
@@ -60,8 +61,7 @@ struct AppendArgs {
     int rope_len;
     int hq, hkv;
     bf16_t *q_out;            /* fused mode: [n][hq][128] */
-    uint8_t *k_cache, *v_cache;
-    float *k_scale, *v_scale;
+    uint8_t *cache;           /* [num_blocks][hkv][4224] tiles */
     const int32_t *block_table;
     int max_blocks, num_blocks, num_seqs;
     int fused;                /* 1: norm + rope q and k, write q_out; 0: store rows as given */
@@ -124,20 +124,21 @@ __global__ void __launch_bounds__(APPEND_THREADS) k_append(AppendArgs a) {
     uint64_t c1, c2;
     const float scale = row_quantize(x1, x2, &c1, &c2);
     const int t = p % NC_PAGE;
-    uint8_t *tile = (is_v ? a.v_cache : a.k_cache) + tile_offset(blk, h, a.hkv);
+    uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
     write_codes(tile, t, g, c1, c2, is_v);
-    if (g == 0) (is_v ? a.v_scale : a.k_scale)[scale_offset(blk, h, a.hkv) + t] = scale;
+    if (g == 0) reinterpret_cast<float *>(tile + (is_v ? NC_TILE_VS : NC_TILE_KS))[t] = scale;
 }
 
-static int check_cache_args(int n, int hkv, int max_blocks, int num_blocks, int num_seqs, const void *k_cache,
-                            const void *v_cache, const void *k_scale, const void *v_scale, const void *block_table) {
+static int check_cache_args(int n, int hkv, int max_blocks, int num_blocks, int num_seqs, const void *cache,
+                            const void *block_table) {
     NC_REQUIRE(n >= 0, "n = %d < 0", n);
     NC_REQUIRE(hkv > 0, "hkv = %d must be positive", hkv);
     NC_REQUIRE(max_blocks > 0 && num_blocks > 0 && num_seqs > 0, "max_blocks %d, num_blocks %d, num_seqs %d must "
                "be positive", max_blocks, num_blocks, num_seqs);
     NC_REQUIRE(block_table || (long long)num_seqs * max_blocks <= num_blocks,
                "contiguous cache: %d sequences x %d blocks exceed the %d blocks", num_seqs, max_blocks, num_blocks);
-    NC_REQUIRE(k_cache && v_cache && k_scale && v_scale, "null cache pointer");
+    NC_REQUIRE(cache, "null cache pointer");
+    NC_REQUIRE((uintptr_t)cache % 16 == 0, "cache must be 16-byte aligned");
     return 0;
 }
 
@@ -152,11 +153,10 @@ static void launch_append(const AppendArgs &a, hipStream_t stream) {
 
 extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, const int32_t *pos,
                                 const int32_t *seq, const float *q_gain, const float *k_gain, const float *cos,
-                                const float *sin, int rope_len, int hq, int hkv, void *q_out, uint8_t *k_cache,
-                                uint8_t *v_cache, float *k_scale, float *v_scale, const int32_t *block_table,
-                                int max_blocks, int num_blocks, int num_seqs, void *stream) {
-    int rc = check_cache_args(n, hkv, max_blocks, num_blocks, num_seqs, k_cache, v_cache, k_scale, v_scale,
-                              block_table);
+                                const float *sin, int rope_len, int hq, int hkv, void *q_out, uint8_t *cache,
+                                const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
+                                void *stream) {
+    int rc = check_cache_args(n, hkv, max_blocks, num_blocks, num_seqs, cache, block_table);
     if (rc) return rc;
     NC_REQUIRE(hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
     NC_REQUIRE(row_stride >= (long long)(hq + 2 * hkv) * NC_HEAD_DIM && row_stride % 8 == 0,
@@ -168,7 +168,7 @@ extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, co
     a.qkv = (const bf16_t *)qkv; a.row_stride = row_stride; a.n = n; a.pos = pos; a.seq = seq;
     a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
     a.hq = hq; a.hkv = hkv; a.q_out = (bf16_t *)q_out;
-    a.k_cache = k_cache; a.v_cache = v_cache; a.k_scale = k_scale; a.v_scale = v_scale;
+    a.cache = cache;
     a.block_table = block_table; a.max_blocks = max_blocks; a.num_blocks = num_blocks; a.num_seqs = num_seqs;
     a.fused = 1;
     launch_append(a, (hipStream_t)stream);
@@ -176,11 +176,9 @@ extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, co
 }
 
 extern "C" int nc_kv_store_fp8(const void *k, const void *v, long long row_stride, int n, const int32_t *pos,
-                               const int32_t *seq, int hkv, uint8_t *k_cache, uint8_t *v_cache, float *k_scale,
-                               float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks,
-                               int num_seqs, void *stream) {
-    int rc = check_cache_args(n, hkv, max_blocks, num_blocks, num_seqs, k_cache, v_cache, k_scale, v_scale,
-                              block_table);
+                               const int32_t *seq, int hkv, uint8_t *cache, const int32_t *block_table,
+                               int max_blocks, int num_blocks, int num_seqs, void *stream) {
+    int rc = check_cache_args(n, hkv, max_blocks, num_blocks, num_seqs, cache, block_table);
     if (rc) return rc;
     NC_REQUIRE(row_stride >= (long long)hkv * NC_HEAD_DIM && row_stride % 8 == 0,
                "row_stride %lld must hold hkv * 128 elements and keep 16-byte alignment", row_stride);
@@ -189,7 +187,7 @@ extern "C" int nc_kv_store_fp8(const void *k, const void *v, long long row_strid
     AppendArgs a = {};
     a.k_rows = (const bf16_t *)k; a.v_rows = (const bf16_t *)v; a.row_stride = row_stride; a.n = n;
     a.pos = pos; a.seq = seq; a.hkv = hkv;
-    a.k_cache = k_cache; a.v_cache = v_cache; a.k_scale = k_scale; a.v_scale = v_scale;
+    a.cache = cache;
     a.block_table = block_table; a.max_blocks = max_blocks; a.num_blocks = num_blocks; a.num_seqs = num_seqs;
     a.fused = 0;
     launch_append(a, (hipStream_t)stream);
@@ -244,8 +242,7 @@ extern "C" void qkp_forward(const void *q, const void *k, const void *gq, const 
 
 /* One 256-thread workgroup per (16-position tile, kv head, sequence): thread (t = tid / 16, c = tid % 16) moves
  * 8 bytes of key t's K row and V row (dims 8c..8c+7) to the canonical layout; positions past ctx_len are zeroed. */
-__global__ void __launch_bounds__(256) k_gather(const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,
-                                                const float *v_scale, const int32_t *block_table, int max_blocks,
+__global__ void __launch_bounds__(256) k_gather(const uint8_t *cache, const int32_t *block_table, int max_blocks,
                                                 int num_blocks, const int32_t *ctx_len, int hkv, int max_ctx,
                                                 uint8_t *k_out, uint8_t *v_out, float *ks_out, float *vs_out) {
     const int page = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -257,12 +254,12 @@ __global__ void __launch_bounds__(256) k_gather(const uint8_t *k_cache, const ui
     uint64_t kw = 0, vw = 0;
     float ks = 0.0f, vs = 0.0f;
     if (blk >= 0) {
-        const uint8_t *kt = k_cache + tile_offset(blk, h, hkv), *vt = v_cache + tile_offset(blk, h, hkv);
-        kw = *reinterpret_cast<const uint64_t *>(kt + t * NC_HEAD_DIM + 8 * c);
+        const uint8_t *tile = cache + tile_offset(blk, h, hkv);
+        kw = *reinterpret_cast<const uint64_t *>(tile + t * NC_HEAD_DIM + 8 * c);
 #pragma unroll
-        for (int e = 0; e < 8; e++) vw |= (uint64_t)vt[v_byte(t, 8 * c + e)] << (8 * e);
-        ks = k_scale[scale_offset(blk, h, hkv) + t];
-        vs = v_scale[scale_offset(blk, h, hkv) + t];
+        for (int e = 0; e < 8; e++) vw |= (uint64_t)tile[v_byte(t, 8 * c + e)] << (8 * e);
+        ks = reinterpret_cast<const float *>(tile + NC_TILE_KS)[t];
+        vs = reinterpret_cast<const float *>(tile + NC_TILE_VS)[t];
     }
     const size_t row = ((size_t)b * hkv + h) * max_ctx + pos;
     *reinterpret_cast<uint64_t *>(k_out + row * NC_HEAD_DIM + 8 * c) = kw;
@@ -273,20 +270,18 @@ __global__ void __launch_bounds__(256) k_gather(const uint8_t *k_cache, const ui
     }
 }
 
-extern "C" int nc_kv_gather_fp8(const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,
-                                const float *v_scale, const int32_t *block_table, int max_blocks, int num_blocks,
+extern "C" int nc_kv_gather_fp8(const uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks,
                                 const int32_t *ctx_len, int B, int hkv, int max_ctx, uint8_t *k_out, uint8_t *v_out,
                                 float *ks_out, float *vs_out, void *stream) {
-    int rc = check_cache_args(B, hkv, max_blocks, num_blocks, B > 0 ? B : 1, k_cache, v_cache, k_scale, v_scale,
-                              block_table);
+    int rc = check_cache_args(B, hkv, max_blocks, num_blocks, B > 0 ? B : 1, cache, block_table);
     if (rc) return rc;
     NC_REQUIRE(max_ctx >= 0 && max_ctx <= max_blocks * NC_PAGE, "max_ctx %d outside [0, %d]", max_ctx,
                max_blocks * NC_PAGE);
     if (B == 0 || max_ctx == 0) return 0;
     NC_REQUIRE(ctx_len && k_out && v_out && ks_out && vs_out, "null argument");
     const dim3 grid((max_ctx + NC_PAGE - 1) / NC_PAGE, hkv, B);
-    hipLaunchKernelGGL(k_gather, grid, dim3(256), 0, (hipStream_t)stream, k_cache, v_cache, k_scale, v_scale,
-                       block_table, max_blocks, num_blocks, ctx_len, hkv, max_ctx, k_out, v_out, ks_out, vs_out);
+    hipLaunchKernelGGL(k_gather, grid, dim3(256), 0, (hipStream_t)stream, cache, block_table, max_blocks,
+                       num_blocks, ctx_len, hkv, max_ctx, k_out, v_out, ks_out, vs_out);
     NC_LAUNCH_CHECK();
     return 0;
 }

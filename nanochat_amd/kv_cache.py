@@ -5,10 +5,13 @@ The reference caches K and V in bf16, contiguous per slot ([slot][layer][max_len
 (token, kv head) for K and for V, in 16-position blocks; a block table maps each sequence's pages to blocks, and a
 contiguous cache is the special case where sequence s owns blocks [s * max_blocks, (s + 1) * max_blocks).
 
-Device layout (also nanochat_amd/csrc/layout.h):
-  k        uint8 [num_blocks][Hkv][16][128]       key t of a page at row t
-  v        uint8 [num_blocks][Hkv][4][128][4]     key t, dim d at [t // 4][d][t % 4] (quad-transposed)
-  k_scale  fp32  [num_blocks][Hkv][16]            v_scale likewise
+Device layout (also nanochat_amd/csrc/layout.h): one pool `pages`, uint8 [num_blocks][Hkv][4224], and per
+(block, kv head) tile the views
+  k        [16][128]      bytes [0, 2048)      key t of a page at row t
+  v        [4][128][4]    bytes [2048, 4096)   key t, dim d at [t // 4][d][t % 4] (quad-transposed)
+  k_scale  fp32 [16]      bytes [4096, 4160)
+  v_scale  fp32 [16]      bytes [4160, 4224)
+so that one page of one kv head is a single contiguous 4224-byte read.
 """
 
 from __future__ import annotations
@@ -20,6 +23,7 @@ from nanochat_amd.native import check, hip_library, pointer, stream
 
 PAGE = 16
 HEAD_DIM = 128
+TILE_BYTES = 4224
 
 
 def _require(t: Tensor, name: str, dtype: torch.dtype, dim: int | None = None) -> None:
@@ -44,10 +48,27 @@ class Fp8KVCache:
                 raise ValueError(f"block_table {tuple(block_table.shape)} != ({num_seqs}, {max_blocks})")
         self.num_blocks, self.hkv, self.max_blocks, self.num_seqs = num_blocks, hkv, max_blocks, num_seqs
         self.block_table = block_table
-        self.k = torch.zeros((num_blocks, hkv, PAGE, HEAD_DIM), dtype=torch.uint8, device=device)
-        self.v = torch.zeros((num_blocks, hkv, PAGE // 4, HEAD_DIM, 4), dtype=torch.uint8, device=device)
-        self.k_scale = torch.zeros((num_blocks, hkv, PAGE), dtype=torch.float32, device=device)
-        self.v_scale = torch.zeros_like(self.k_scale)
+        self.pages = torch.zeros((num_blocks, hkv, TILE_BYTES), dtype=torch.uint8, device=device)
+
+    @property
+    def k(self) -> Tensor:
+        """K codes, a view [num_blocks][hkv][16][128]."""
+        return self.pages[..., :2048].unflatten(-1, (PAGE, HEAD_DIM))
+
+    @property
+    def v(self) -> Tensor:
+        """V codes, a view [num_blocks][hkv][4][128][4] (quad-transposed)."""
+        return self.pages[..., 2048:4096].unflatten(-1, (PAGE // 4, HEAD_DIM, 4))
+
+    @property
+    def k_scale(self) -> Tensor:
+        """K scales, a view fp32 [num_blocks][hkv][16]."""
+        return self.pages[..., 4096:4160].view(torch.float32)
+
+    @property
+    def v_scale(self) -> Tensor:
+        """V scales, a view fp32 [num_blocks][hkv][16]."""
+        return self.pages[..., 4160:4224].view(torch.float32)
 
     @classmethod
     def contiguous(cls, num_seqs: int, max_len: int, hkv: int, device: torch.device | str = "cuda") -> "Fp8KVCache":
@@ -64,8 +85,7 @@ class Fp8KVCache:
         return self.max_blocks * PAGE
 
     def _cache_args(self):
-        return (pointer(self.k), pointer(self.v), pointer(self.k_scale), pointer(self.v_scale),
-                pointer(self.block_table), self.max_blocks, self.num_blocks, self.num_seqs)
+        return (pointer(self.pages), pointer(self.block_table), self.max_blocks, self.num_blocks, self.num_seqs)
 
     def append(self, qkv: Tensor, pos: Tensor, seq: Tensor, q_gain: Tensor, k_gain: Tensor, cos: Tensor,
                sin: Tensor, hq: int) -> Tensor:

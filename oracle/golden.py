@@ -4,10 +4,12 @@ Every function states the rule it fixes and the reference file:line it follows. 
 (model/kernels/decode.cu:4-7); the fp8 scheme (per-token, per-kv-head absmax scale, OCP e4m3fn) is defined by the
 benchmark configuration, not by the reference, and is restated here as the build's spec.
 
-Layout spec shared with the HIP kernels (nanochat_amd/csrc/layout.h):
-  K pages   uint8 [num_blocks][Hkv][PAGE][128]      row-major: key t of a page at t*128
-  V pages   uint8 [num_blocks][Hkv][PAGE/4][128][4] quad-transposed: key t, dim d at (t/4)*512 + d*4 + t%4
-  scales    fp32  [num_blocks][Hkv][PAGE]           one per (token, kv head), separately for K and V
+Layout spec shared with the HIP kernels (nanochat_amd/csrc/layout.h): one byte pool [num_blocks][Hkv][4224]; the
+(block, kv head) tile holds
+  [0, 2048)     K codes, row-major: key t of a page at t*128
+  [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + (t/4)*512 + d*4 + t%4
+  [4096, 4160)  K scales fp32 [16], one per (token, kv head)
+  [4160, 4224)  V scales fp32 [16]
   block table int32 [B][max_blocks]; None means contiguous: sequence b's page i is block b*max_blocks + i.
 """
 
@@ -135,15 +137,22 @@ def dequantize(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
 # the paged cache
 # ---------------------------------------------------------------------------------------------------------------
 
+TILE_BYTES = 4224
+
+
 class PagedCache:
-    """The HIP kernels' cache layout (module docstring), held in numpy arrays of the same shapes and bytes."""
+    """The HIP kernels' cache layout (module docstring): the byte pool `pages` and named views of its regions
+    (k [nb][Hkv][16][128], v [nb][Hkv][4][128][4], k_scale / v_scale fp32 [nb][Hkv][16]); writes through a view
+    land in the pool."""
 
     def __init__(self, num_blocks: int, hkv: int):
         self.num_blocks, self.hkv = num_blocks, hkv
-        self.k = np.zeros((num_blocks, hkv, PAGE, HEAD_DIM), np.uint8)
-        self.v = np.zeros((num_blocks, hkv, PAGE // 4, HEAD_DIM, 4), np.uint8)
-        self.k_scale = np.zeros((num_blocks, hkv, PAGE), np.float32)
-        self.v_scale = np.zeros((num_blocks, hkv, PAGE), np.float32)
+        self.pages = np.zeros((num_blocks, hkv, TILE_BYTES), np.uint8)
+        self.k = self.pages[..., :2048].reshape(num_blocks, hkv, PAGE, HEAD_DIM)
+        self.v = self.pages[..., 2048:4096].reshape(num_blocks, hkv, PAGE // 4, HEAD_DIM, 4)
+        self.k_scale = self.pages[..., 4096:4160].view(np.float32)
+        self.v_scale = self.pages[..., 4160:4224].view(np.float32)
+        assert all(np.shares_memory(x, self.pages) for x in (self.k, self.v, self.k_scale, self.v_scale))
 
     @staticmethod
     def block_of(seq: np.ndarray, pos: np.ndarray, block_table: np.ndarray | None, max_blocks: int) -> np.ndarray:

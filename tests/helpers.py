@@ -17,10 +17,7 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 def oracle_cache(cache) -> G.PagedCache:
     c = G.PagedCache(cache.num_blocks, cache.hkv)
-    c.k[...] = cache.k.cpu().numpy()
-    c.v[...] = cache.v.cpu().numpy()
-    c.k_scale[...] = cache.k_scale.cpu().numpy()
-    c.v_scale[...] = cache.v_scale.cpu().numpy()
+    c.pages[...] = cache.pages.cpu().numpy()
     return c
 
 
@@ -29,10 +26,13 @@ def table(cache):
 
 
 def assert_same_cache(gpu_cache, ref: G.PagedCache) -> None:
-    np.testing.assert_array_equal(gpu_cache.k.cpu().numpy(), ref.k)
-    np.testing.assert_array_equal(gpu_cache.v.cpu().numpy(), ref.v)
-    np.testing.assert_array_equal(gpu_cache.k_scale.cpu().numpy().view(np.uint32), ref.k_scale.view(np.uint32))
-    np.testing.assert_array_equal(gpu_cache.v_scale.cpu().numpy().view(np.uint32), ref.v_scale.view(np.uint32))
+    """Every byte of the pool: codes and the scales' fp32 bit patterns."""
+    got = gpu_cache.pages.cpu().numpy()
+    for name in ("k", "v", "k_scale", "v_scale"):  # name the region that differs first
+        g = G.PagedCache(gpu_cache.num_blocks, gpu_cache.hkv)
+        g.pages[...] = got
+        np.testing.assert_array_equal(getattr(g, name).view(np.uint8), getattr(ref, name).view(np.uint8), name)
+    np.testing.assert_array_equal(got, ref.pages)
 
 
 def attention_error(got: torch.Tensor, want: np.ndarray) -> tuple[float, float]:

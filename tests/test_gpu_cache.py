@@ -17,8 +17,7 @@ pytestmark = pytest.mark.gpu
 def random_bytes(cache: Fp8KVCache, seed: int) -> None:
     """Fill the cache with seeded garbage so untouched bytes are checked to stay untouched."""
     g = torch.Generator().manual_seed(seed)
-    for t in (cache.k, cache.v):
-        t.copy_(torch.randint(0, 256, t.shape, generator=g, dtype=torch.uint8))
+    cache.pages.copy_(torch.randint(0, 256, cache.pages.shape, generator=g, dtype=torch.uint8))
     for t in (cache.k_scale, cache.v_scale):
         t.copy_(torch.rand(t.shape, generator=g))
 

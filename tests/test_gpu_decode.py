@@ -73,6 +73,7 @@ def test_single_key_returns_the_value_exactly(gpu):
     cache.k[0, :, 0] = torch.randint(0, 0x7E, (hkv, 128), dtype=torch.uint8).to(dev)
     cache.k_scale[0, :, 0] = 0.01
     cache.v_scale[0, :, 0] = 0.25
+    assert cache.pages[0, 1, 4160:4164].view(torch.float32).item() == 0.25  # the views write the pool
     q = torch.randn((1, hq, 128), device=dev).to(torch.bfloat16)
     out = decode_attention(q, cache, torch.tensor([1], dtype=torch.int32, device=dev), max_ctx=16)
     want = G.E4M3_TABLE[v_rows.numpy()] * np.float32(0.25)

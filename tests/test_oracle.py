@@ -200,19 +200,21 @@ def test_quantize_rows_absmax_maps_to_448_and_error_bound():
 # ----------------------------------------------------------------------------------------------- cache layout
 
 def test_cache_layout_byte_offsets():
-    """V's quad-transposed page: key t, dim d at byte (t/4)*512 + d*4 + t%4 of its (block, head) 2 KiB tile."""
+    """Tile (block, head) at byte (block * Hkv + head) * 4224 of the pool: K key t at t*128, V key t dim d at
+    2048 + (t/4)*512 + d*4 + t%4, K scale t at 4096 + 4t, V scale t at 4160 + 4t."""
     c = G.PagedCache(3, 2)
     kc = np.arange(128, dtype=np.uint8)
     vc = (np.arange(128) + 100).astype(np.uint8)
     c.write(np.array([2]), 1, np.array([13]), kc[None], np.float32(0.5), vc[None], np.float32(0.25))
-    flat_k = c.k.reshape(-1)
-    flat_v = c.v.reshape(-1)
-    tile = (2 * 2 + 1) * 2048
-    np.testing.assert_array_equal(flat_k[tile + 13 * 128: tile + 14 * 128], kc)
+    flat = c.pages.reshape(-1)
+    tile = (2 * 2 + 1) * 4224
+    np.testing.assert_array_equal(flat[tile + 13 * 128: tile + 14 * 128], kc)
     for d in (0, 1, 77, 127):
-        assert flat_v[tile + (13 // 4) * 512 + d * 4 + 13 % 4] == vc[d]
-    assert c.k_scale.reshape(-1)[(2 * 2 + 1) * 16 + 13] == 0.5
-    assert np.count_nonzero(flat_v) == 128 and np.count_nonzero(flat_k) == 127
+        assert flat[tile + 2048 + (13 // 4) * 512 + d * 4 + 13 % 4] == vc[d]
+    assert flat[tile + 4096 + 4 * 13: tile + 4096 + 4 * 14].view(np.float32)[0] == 0.5
+    assert flat[tile + 4160 + 4 * 13: tile + 4160 + 4 * 14].view(np.float32)[0] == 0.25
+    # 127 nonzero K codes, 128 V codes, and the scales' nonzero bytes: 0.5 = 0x3f000000 (1), 0.25 = 0x3e800000 (2)
+    assert np.count_nonzero(flat) == 127 + 128 + 1 + 2
 
 
 def test_append_then_gather_paged_equals_contiguous():
@@ -308,8 +310,7 @@ def test_decode_attention_brute_force_and_gqa_mapping():
     # MHA copy: kv head h of the 6-head cache is kv head h // 3 of the 2-head one
     mha = G.PagedCache(c.num_blocks, hq)
     for h in range(hq):
-        mha.k[:, h], mha.v[:, h] = c.k[:, h // 3], c.v[:, h // 3]
-        mha.k_scale[:, h], mha.v_scale[:, h] = c.k_scale[:, h // 3], c.v_scale[:, h // 3]
+        mha.pages[:, h] = c.pages[:, h // 3]
     np.testing.assert_allclose(G.decode_attention(q, mha, bt, mb, ctx, 5, hq, hq, scale), out, rtol=1e-13)
 
 
