@@ -71,7 +71,7 @@ int nc_kv_gather_fp8(const uint8_t *cache, const int32_t *block_table, int max_b
                      float *ks_out, float *vs_out, void *stream);
 
 /* Workspace bytes nc_decode_attn_fp8 needs for B sequences of hq / hkv heads (independent of max_ctx and of the
- * device): per-segment counters, then a partial-result slot per wave and per (sequence, kv head). */
+ * device): a partial-result slot (Σ p v, max, sum) per wave and per (sequence, kv head). */
 long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx);
 
 /* Single-token decode attention: query b (bf16 q [B][Hq][128]) at position p = ctx_len[b] - 1 attends keys
@@ -85,6 +85,18 @@ long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx);
 int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int32_t *block_table, int max_blocks,
                        int num_blocks, const int32_t *ctx_len, int window, int B, int hq, int hkv, int max_ctx,
                        float sm_scale, void *out, void *workspace, long long workspace_bytes, void *stream);
+
+/* Chunked-prefill attention: row r (bf16 q [n][Hq][128], normed and rotated, e.g. nc_kv_append_fp8's q_out) at
+ * position pos[r] of sequence seq[r] attends keys [max(pos - window, 0), pos] of that sequence in the cache
+ * (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores times sm_scale, fp32 softmax, bf16 out
+ * [n][Hq][128]. The rows' own keys must be in the cache already (append the whole chunk first), so each row sees
+ * the chunk's earlier rows causally. Rows with pos < 0 or seq outside [0, num_seqs) get zero rows; keys of a
+ * missing block are skipped. Rows may come in any order; a sequence's rows being consecutive is fastest.
+ * Hq / Hkv <= 16.
+ * Replaces: dec_prefill, model/kernels/decode.cu:1039-1051, whose rows each run k_attn (decode.cu:567-675). */
+int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, int n, const uint8_t *cache,
+                        const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs, int window, int hq,
+                        int hkv, float sm_scale, void *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -3,6 +3,10 @@
 decode_attention replaces the reference's k_attn (model/kernels/decode.cu:567-675): query b sits at position
 ctx_len[b] - 1 and attends the keys [max(p - window, 0), p] of its sequence in the cache (its own key appended
 first), query head h reading kv head h // (Hq / Hkv). Softmax in fp32, output bf16.
+
+prefill_attention replaces dec_prefill's rows (model/kernels/decode.cu:1039-1051, each row a k_attn block): row r
+at position pos[r] of sequence seq[r] attends keys [max(pos - window, 0), pos] after the whole chunk was appended
+(decode.cu:859-863), on MFMA tiles that share every fp8 page among the rows and heads of a kv head.
 """
 
 from __future__ import annotations
@@ -58,4 +62,31 @@ def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: 
                                  cache.num_blocks, pointer(ctx_len), window, B, hq, cache.hkv, max_ctx, scale,
                                  pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
                                  stream()))
+    return out
+
+
+def prefill_attention(q: Tensor, cache: Fp8KVCache, pos: Tensor, seq: Tensor, *, window: int = -1,
+                      sm_scale: float | None = None, out: Tensor | None = None) -> Tensor:
+    """q bf16 [n][Hq][128] (Fp8KVCache.append's q_out for the chunk); pos, seq int32 [n] on the GPU. The chunk's
+    keys must already be in the cache. Rows with pos < 0 or seq outside the cache's sequences get zero rows.
+    Fastest when each sequence's rows are consecutive. Returns bf16 [n][Hq][128]."""
+    _require(q, "q", torch.bfloat16, 3)
+    n, hq, D = q.shape
+    if D != HEAD_DIM:
+        raise ValueError(f"head dim {D} != 128")
+    _require(pos, "pos", torch.int32, 1)
+    _require(seq, "seq", torch.int32, 1)
+    if pos.shape[0] != n or seq.shape[0] != n:
+        raise ValueError(f"pos / seq have {pos.shape[0]} / {seq.shape[0]} entries for {n} rows")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out, "out", torch.bfloat16, 3)
+        if out.shape != q.shape:
+            raise ValueError("out must have q's shape")
+    lib = hip_library()
+    check(lib.nc_prefill_attn_fp8(pointer(q), pointer(pos), pointer(seq), n, pointer(cache.pages),
+                                  pointer(cache.block_table), cache.max_blocks, cache.num_blocks, cache.num_seqs, window,
+                                  hq, cache.hkv, scale, pointer(out), stream()))
     return out

@@ -1,0 +1,504 @@
+/*
+ * Chunked-prefill attention over the fp8 paged cache (reference: dec_prefill, model/kernels/decode.cu:1039-1051,
+ * whose rows each run k_attn, decode.cu:567-675, as one single-query block: no K/V reuse across rows).
+ *
+ * Rows: n query rows (bf16 q [n][Hq][128], the append's q_out), row r at position pos[r] of sequence seq[r]. As in
+ * the reference (decode.cu:859-863) every row's key and value are appended before any row attends, so row r
+ * reads keys [max(pos - window, 0), pos] of its sequence from the cache, its own and its chunk's earlier keys
+ * included. Rows may come in any order and from any sequences; the kernel is fastest when a sequence's rows are
+ * consecutive.
+ *
+ * Work: one workgroup of 4 waves per (kv head h, tile of 16 R consecutive rows), R = floor(16 / G) rows per
+ * 16-column MFMA block, G = Hq / Hkv. A wave holds 4 blocks; column n of a block is (row n / G, query head
+ * h G + n % G), so the G heads of a row share every key read. The workgroup walks the pages of the union key
+ * range of its rows in pairs; all four waves consume the same pair from LDS.
+ *
+ * Per page pair (32 keys) a wave computes, for each of its 4 blocks,
+ *   scores  Sᵀ[16 keys][16 columns] per page = K · Qᵀ, 4 v_mfma_f32_16x16x32_bf16 (fp8 -> bf16 exact, A = K with
+ *           key lane % 16 and dims 32 (lane / 16) .., B = q of column lane % 16 over the same dims);
+ *   softmax fp32 base 2, lazy reference max per column (moves only when a score exceeds it by more than 8);
+ *   values  Oᵀ[16 dims][16 columns] += Vᵀ[16 dims][32 keys] · Pᵀ, 8 v_mfma_f32_16x16x32_f16. The lane's k slots
+ *           8j..8j+7 are keys 4j..4j+3 of the first page then of the second, which is where the score MFMAs left
+ *           this lane's probabilities: Pᵀ is built in registers, no exchange. P carries v_scale and a running
+ *           power of two (as in decode): fp16 with headroom, V codes fp8 -> fp16 exact.
+ * 64 MFMAs per wave per pair for ~350 VALU instructions: MFMA-bound (the roofline is the bf16/fp16 dense peak).
+ *
+ * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
+ * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
+ * conflict-free ds_read_b128 per fragment). Each wave issues 3 of a pair's 10 DMAs (two 1 KiB fragment loads,
+ * one 64 B scale quarter), PF_RING - 1 pairs ahead; per pair: wait for its own DMAs, s_barrier, refill the slot
+ * freed by the previous pair, read, compute. Block ids are staged in LDS per chunk of PF_IDS pages.
+ */
+#include "layout.h"
+
+#ifndef PF_WAVES
+#define PF_WAVES 8         /* per workgroup, two per SIMD */
+#endif
+#define PF_THREADS (PF_WAVES * NC_WAVE)
+#ifndef PF_BLOCKS
+#define PF_BLOCKS 2        /* 16-column MFMA blocks per wave */
+#endif
+#ifndef PF_RING
+#define PF_RING 8          /* page-pair slots: 7 pairs (59 KB) in flight while one is computed */
+#endif
+#define PF_FRAGS_PER_WAVE (8 / PF_WAVES)         /* of a pair's eight 1 KiB fragment DMAs */
+#define PF_SCALE_BYTES (256 / PF_WAVES)          /* of a pair's 256 B of scales */
+#define PF_DMA_PER_PAIR (PF_FRAGS_PER_WAVE + 1)  /* per wave */
+#define PF_PAIR_BYTES (2 * NC_TILE_BYTES)
+#define PF_IDS 1024        /* block ids staged per chunk of a segment's pages */
+#define PF_LAZY 8.0f
+#define PF_M_INIT -3.0e38f
+#define PF_NO_KEY 0x40000000
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+struct PrefillArgs {
+    const bf16_t *q;        /* [n][hq][128] */
+    int n;
+    const uint8_t *cache;   /* [num_blocks][hkv][4224] tiles */
+    int max_blocks, num_blocks, num_seqs;
+    int window;             /* keys before the query; < 0: all */
+    int hq, hkv, group, rows_per_block;
+    float score_scale;      /* sm_scale * log2(e) */
+    bf16_t *out;            /* [n][hq][128] */
+    int tiles;              /* row tiles per kv head */
+    int units_per_xcd;
+};
+
+__device__ __forceinline__ bf16x8 pf_fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+/* Dword bb of the V fragments of both pages -> 8 fp16 (keys 4j..4j+3 of the first page, then of the second). */
+__device__ __forceinline__ f16x8 pf_v_operand(uint32_t wa, uint32_t wb) {
+    const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wa, 1.0f, false);
+    const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wa, 1.0f, true);
+    const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wb, 1.0f, false);
+    const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wb, 1.0f, true);
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ float pf_exp2i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+template <int N> __device__ __forceinline__ void pf_wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* This wave's DMAs of a page pair: PF_FRAGS_PER_WAVE of the pair's eight 1 KiB fragments (K bytes 0-15 and 16-31
+ * of every lane, then V bytes 0-15 and 16-31, of the first page then of the second) and a PF_SCALE_BYTES part of
+ * the pair's scales. blk < 0 (no block) loads block 0, masked later. */
+__device__ __forceinline__ void dma_pair(const PrefillArgs &a, int blk0, int blk1, int h, int wv, int lane,
+                                         unsigned char *slot) {
+    const int n = lane & 15, j = lane >> 4;
+#pragma unroll
+    for (int f = 0; f < PF_FRAGS_PER_WAVE; f++) {
+        const int fid = wv * PF_FRAGS_PER_WAVE + f, pg = fid >> 2, part = fid & 3;
+        const int blk = pg ? blk1 : blk0;
+        const uint8_t *tile = a.cache + tile_offset(blk < 0 ? 0 : blk, h, a.hkv);
+        const uint8_t *src = part < 2 ? tile + n * NC_HEAD_DIM + j * 32 : tile + NC_TILE_V + j * 512 + n * 32;
+        __builtin_amdgcn_global_load_lds(src + 16 * (part & 1), slot + pg * NC_TILE_BYTES + part * 1024, 16, 0, 0);
+    }
+    const int sb = wv * PF_SCALE_BYTES, pg = sb >> 7, off = sb & 127;
+    const int blk = pg ? blk1 : blk0;
+    const uint8_t *tile = a.cache + tile_offset(blk < 0 ? 0 : blk, h, a.hkv);
+    if (lane < PF_SCALE_BYTES / 16)
+        __builtin_amdgcn_global_load_lds(tile + NC_TILE_KS + off + 16 * lane, slot + pg * NC_TILE_BYTES + NC_TILE_KS + off,
+                                         16, 0, 0);
+}
+
+/* One page's fragments for this lane: K bytes (dims 32j.. of key n), V quad bytes (dims 8n.. of keys 4j..), and the
+ * K / V scales of keys 4j..4j+3. */
+struct PfPage {
+    u32x4 k0, k1, v0, v1, ks, vs;
+};
+
+/* Both pages of a slot, the pair's two block ids, and the two block ids of pair `next_pair` for the next
+ * refill. Inline ds_reads with their own lgkmcnt wait: as plain LDS loads the compiler would precede them
+ * with s_waitcnt vmcnt(0) (it cannot tell them from the ring's in-flight DMA writes) and drain the ring. */
+__device__ __forceinline__ void read_pair(const unsigned char *slot, const int *ids, int pair, int next_pair, int lane,
+                                          PfPage &pa, PfPage &pb, int &ida, int &idb, u32x2 &id_next) {
+    const int j = lane >> 4;
+    const uint32_t base = (uint32_t)(uintptr_t)(const lds_u8 *)slot;
+    const uint32_t mine = base + 16 * lane, sc = base + NC_TILE_KS + 16 * j;
+    const uint32_t idp = (uint32_t)(uintptr_t)(const lds_u8 *)(const unsigned char *)(ids + 2 * pair);
+    const uint32_t idn = (uint32_t)(uintptr_t)(const lds_u8 *)(const unsigned char *)(ids + 2 * next_pair);
+    u32x2 id2;
+    asm volatile(
+        "ds_read_b128 %0, %14\n"
+        "ds_read_b128 %1, %14 offset:1024\n"
+        "ds_read_b128 %2, %14 offset:2048\n"
+        "ds_read_b128 %3, %14 offset:3072\n"
+        "ds_read_b128 %4, %15\n"
+        "ds_read_b128 %5, %15 offset:64\n"
+        "ds_read_b128 %6, %14 offset:4224\n"
+        "ds_read_b128 %7, %14 offset:5248\n"
+        "ds_read_b128 %8, %14 offset:6272\n"
+        "ds_read_b128 %9, %14 offset:7296\n"
+        "ds_read_b128 %10, %15 offset:4224\n"
+        "ds_read_b128 %11, %15 offset:4288\n"
+        "ds_read_b64 %12, %16\n"
+        "ds_read_b64 %13, %17\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(pa.k0), "=&v"(pa.k1), "=&v"(pa.v0), "=&v"(pa.v1), "=&v"(pa.ks), "=&v"(pa.vs), "=&v"(pb.k0),
+          "=&v"(pb.k1), "=&v"(pb.v0), "=&v"(pb.v1), "=&v"(pb.ks), "=&v"(pb.vs), "=&v"(id2), "=&v"(id_next)
+        : "v"(mine), "v"(sc), "v"(idp), "v"(idn)
+        : "memory");
+    ida = (int)id2[0];
+    idb = (int)id2[1];
+}
+
+/* The online-softmax state of a wave's 4 blocks, lane (j, n): column n's reference max m[bl] and this lane's
+ * partial sum l[bl]; Oᵀ in o[bl][bb][i] = dim 8 (4j + i) + bb of column n, in units of 2^(e_ref - 126). */
+struct PfState {
+    f32x4 o[PF_BLOCKS][8];
+    float m[PF_BLOCKS], l[PF_BLOCKS];
+    float w, vlim;
+    int e_ref;
+};
+
+/* A wave's view of the segment being attended: per column the key range [lo, hi] (lo > hi: masked throughout),
+ * and the wave-uniform bounds under which a page pair needs no mask. */
+struct PfCols {
+    int lo[PF_BLOCKS], hi[PF_BLOCKS];
+    int max_lo, min_hi; /* over the wave's columns of the segment */
+    int seg_lo, seg_hi; /* the workgroup's union key range */
+    bool masked_always; /* a column of another sequence sits in this wave */
+    bool active;        /* the wave has a column of the segment */
+};
+
+__device__ __forceinline__ void compute_pair(const PrefillArgs &a, const PfPage &pa, const PfPage &pb, int ida, int idb,
+                                             int page0, const PfCols &c, const bf16x8 (*qop)[4], int j, PfState &st) {
+    f32x4 sa[PF_BLOCKS], sb[PF_BLOCKS];
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) sa[bl] = sb[bl] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) { /* one k step of every block per conversion: 8 converted registers live */
+        const u32x4 &fa = kk < 2 ? pa.k0 : pa.k1, &fb = kk < 2 ? pb.k0 : pb.k1;
+        const bf16x8 ka = pf_fp8x8_to_bf16(fa[2 * (kk & 1)], fa[2 * (kk & 1) + 1]);
+        const bf16x8 kb = pf_fp8x8_to_bf16(fb[2 * (kk & 1)], fb[2 * (kk & 1) + 1]);
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            sa[bl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[bl][kk], sa[bl], 0, 0, 0);
+            sb[bl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop[bl][kk], sb[bl], 0, 0, 0);
+        }
+    }
+    float x[PF_BLOCKS][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float ksa = __uint_as_float(pa.ks[i]) * a.score_scale, ksb = __uint_as_float(pb.ks[i]) * a.score_scale;
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            x[bl][i] = sa[bl][i] * ksa;
+            x[bl][4 + i] = sb[bl][i] * ksb;
+        }
+    }
+    float vs[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        vs[i] = __uint_as_float(pa.vs[i]);
+        vs[4 + i] = __uint_as_float(pb.vs[i]);
+    }
+    const int key0 = page0 * NC_PAGE + 4 * j, key1 = key0 + NC_PAGE;
+    const bool fast = ida >= 0 && idb >= 0 && !c.masked_always && page0 * NC_PAGE >= c.max_lo &&
+                      page0 * NC_PAGE + 2 * NC_PAGE - 1 <= c.min_hi;
+    if (!fast) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int key = (i < 4 ? key0 : key1 - 4) + i;
+            const bool pg_ok = i < 4 ? ida >= 0 : idb >= 0;
+            const bool in_seg = pg_ok && key >= c.seg_lo && key <= c.seg_hi;
+            vs[i] = in_seg ? vs[i] : 0.f;
+#pragma unroll
+            for (int bl = 0; bl < PF_BLOCKS; bl++)
+                x[bl][i] = (in_seg && key >= c.lo[bl] && key <= c.hi[bl]) ? x[bl][i] : -INFINITY;
+        }
+    }
+
+    float xm[PF_BLOCKS];
+    bool need = false;
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        xm[bl] = fmaxf(fmaxf(fmaxf(x[bl][0], x[bl][1]), fmaxf(x[bl][2], x[bl][3])),
+                       fmaxf(fmaxf(x[bl][4], x[bl][5]), fmaxf(x[bl][6], x[bl][7])));
+        need |= xm[bl] > st.m[bl] + PF_LAZY;
+    }
+    if (__any(need)) { /* rare: move the reference max of every block to its exact max, rescale */
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            float mx = fmaxf(xm[bl], shfl_xor_f(xm[bl], 16));
+            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            const float m_new = fmaxf(st.m[bl], mx);
+            const float alpha = __builtin_amdgcn_exp2f(st.m[bl] - m_new);
+            st.l[bl] *= alpha;
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= alpha;
+            st.m[bl] = m_new;
+        }
+    }
+    const float vm = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])), fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
+    if (__any(vm >= st.vlim)) { /* rare: a larger v_scale exponent, rescale the units of o */
+        float vx = fmaxf(vm, shfl_xor_f(vm, 16));
+        vx = fmaxf(vx, shfl_xor_f(vx, 32));
+        const int e_new = max(st.e_ref, (int)(__float_as_uint(vx) >> 23));
+        const float r = pf_exp2i(max(st.e_ref - e_new, -126));
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++)
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= r;
+        st.e_ref = e_new;
+        st.w = pf_exp2i(max(126 - e_new, -126));
+        st.vlim = pf_exp2i(min(e_new - 126, 127));
+    }
+    float vw[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) vw[i] = vs[i] * st.w;
+    f16x8 pp[PF_BLOCKS];
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(x[bl][i] - st.m[bl]);
+        st.l[bl] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+#pragma unroll
+        for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vw[i]);
+    }
+#pragma unroll
+    for (int bb = 0; bb < 8; bb++) {
+        const uint32_t wa = bb < 4 ? pa.v0[bb] : pa.v1[bb - 4];
+        const uint32_t wb = bb < 4 ? pb.v0[bb] : pb.v1[bb - 4];
+        const f16x8 va = pf_v_operand(wa, wb);
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++)
+            st.o[bl][bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pp[bl], st.o[bl][bb], 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ bool row_valid(const PrefillArgs &a, int p, int s) {
+    return p >= 0 && s >= 0 && s < a.num_seqs;
+}
+
+/* The first key of a row at position p. */
+__device__ __forceinline__ int key_lo(const PrefillArgs &a, int p) {
+    return (a.window < 0 || p <= a.window) ? 0 : p - a.window;
+}
+
+__global__ void __launch_bounds__(PF_THREADS, 1)
+    k_prefill(PrefillArgs a, const int32_t *__restrict__ pos, const int32_t *__restrict__ seq,
+              const int32_t *__restrict__ block_table) {
+    __shared__ __attribute__((aligned(16))) unsigned char ring[PF_RING * PF_PAIR_BYTES];
+    __shared__ __attribute__((aligned(16))) int ids[PF_IDS];
+
+    /* XCD-aware unit order: workgroup b runs on XCD b % 8, which takes a contiguous range of units, so the row
+     * tiles of one (sequence, kv head) -- the readers of the same pages -- share an L2 */
+    const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
+    if (unit >= a.hkv * a.tiles) return;
+    const int h = unit / a.tiles, tile = unit % a.tiles;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, n = lane & 15, j = lane >> 4;
+    const int G = a.group, R = a.rows_per_block, TR = PF_WAVES * PF_BLOCKS * R;
+    const int row0 = tile * TR;
+
+    /* this lane's q operands: column n of block bl is row row0 + (wv PF_BLOCKS + bl) R + n / G, head h G + n % G */
+    bf16x8 qop[PF_BLOCKS][4];
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
+        const bool used = n < R * G && r < a.n;
+        const bf16_t *qr = a.q + ((size_t)(used ? r : 0) * a.hq + h * G + n % G) * NC_HEAD_DIM + 32 * j;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const u32x4 u = used ? *reinterpret_cast<const u32x4 *>(qr + 8 * kk) : u32x4{0u, 0u, 0u, 0u};
+            qop[bl][kk] = __builtin_bit_cast(bf16x8, u);
+        }
+    }
+
+    PfState st;
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+#pragma unroll
+        for (int bb = 0; bb < 8; bb++) st.o[bl][bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        st.m[bl] = PF_M_INIT;
+        st.l[bl] = 0.f;
+    }
+    st.e_ref = 0;
+    st.w = pf_exp2i(126);
+    st.vlim = pf_exp2i(-126);
+
+    /* rows of the tile still to attend, 4 per lane (row0 + lane + 64 i); every wave derives the same segments */
+    unsigned pend = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int k = lane + 64 * i, r = row0 + k;
+        if (k < TR && r < a.n && row_valid(a, pos[r], seq[r])) pend |= 1u << i;
+    }
+
+    for (;;) {
+        /* a sequence with rows still to attend: its rows form the segment */
+        int s = -1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const unsigned long long bal = __ballot((pend >> i) & 1);
+            if (s < 0 && bal) {
+                const int src = __builtin_ctzll(bal);
+                s = __shfl((pend >> i) & 1 ? seq[row0 + lane + 64 * i] : -1, src, 64);
+            }
+        }
+        s = __builtin_amdgcn_readfirstlane(s);
+        if (s < 0) break;
+        int lo = PF_NO_KEY, hi = -1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + lane + 64 * i;
+            if ((pend >> i) & 1 && seq[r] == s) {
+                const int p = pos[r];
+                lo = min(lo, key_lo(a, p));
+                hi = max(hi, p);
+                pend &= ~(1u << i);
+            }
+        }
+        lo = __builtin_amdgcn_readfirstlane(wave_min_i(lo));
+        hi = __builtin_amdgcn_readfirstlane(wave_max_i(hi));
+
+        PfCols c;
+        int wmax_lo = -1, wmin_hi = PF_NO_KEY;
+        bool other = false, mine = false;
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
+            const bool used = n < R * G && r < a.n;
+            const int p = used ? pos[r] : -1, sq = used ? seq[r] : -1;
+            const bool ok = used && row_valid(a, p, sq), in_seg = ok && sq == s;
+            other |= ok && !in_seg;
+            mine |= in_seg;
+            c.lo[bl] = in_seg ? key_lo(a, p) : (ok ? PF_NO_KEY : 0);
+            c.hi[bl] = in_seg ? p : (ok ? -1 : PF_NO_KEY);
+            if (in_seg) {
+                wmax_lo = max(wmax_lo, key_lo(a, p));
+                wmin_hi = min(wmin_hi, p);
+            }
+        }
+        c.max_lo = __builtin_amdgcn_readfirstlane(wave_max_i(wmax_lo));
+        c.min_hi = __builtin_amdgcn_readfirstlane(wave_min_i(wmin_hi));
+        c.masked_always = __any(other);
+        c.active = __any(mine);
+        c.seg_lo = lo;
+        c.seg_hi = hi;
+
+        const int first = lo / NC_PAGE, npages = hi / NC_PAGE - first + 1;
+        for (int cb = 0; cb < npages; cb += PF_IDS) {
+            const int cp = min(PF_IDS, npages - cb), npairs = (cp + 1) / 2;
+            __syncthreads(); /* the previous chunk's ring and ids are no longer read */
+            for (int e = tid; e < 2 * npairs; e += PF_THREADS)
+                ids[e] = e < cp ? lookup_block(block_table, a.max_blocks, a.num_blocks, s, first + cb + e) : -1;
+            __syncthreads();
+            int pro[PF_RING - 1][2];
+#pragma unroll
+            for (int k = 0; k < PF_RING - 1; k++) {
+                pro[k][0] = ids[2 * min(k, npairs - 1)];
+                pro[k][1] = ids[2 * min(k, npairs - 1) + 1];
+            }
+            u32x2 id_next = *reinterpret_cast<const u32x2 *>(ids + 2 * min(PF_RING - 1, npairs - 1));
+#pragma unroll
+            for (int k = 0; k < PF_RING - 1; k++) {
+                __builtin_amdgcn_sched_barrier(0);
+                dma_pair(a, pro[k][0], pro[k][1], h, wv, lane, ring + k * PF_PAIR_BYTES);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            for (int k = 0; k < npairs; k++) {
+                pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 2)>(); /* this wave's DMAs of pair k have landed */
+                __builtin_amdgcn_s_barrier();                      /* everyone's have; slot k - 1 is free */
+                __builtin_amdgcn_sched_barrier(0);
+                const int kr = k + PF_RING - 1;
+                dma_pair(a, (int)id_next[0], (int)id_next[1], h, wv, lane, ring + (kr % PF_RING) * PF_PAIR_BYTES);
+                PfPage pa, pb;
+                int ida, idb;
+                read_pair(ring + (k % PF_RING) * PF_PAIR_BYTES, ids, k, min(kr + 1, npairs - 1), lane, pa, pb, ida, idb,
+                          id_next);
+                __builtin_amdgcn_sched_barrier(0);
+                if (c.active) compute_pair(a, pa, pb, ida, idb, first + cb + 2 * k, c, qop, j, st);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            pf_wait_vmcnt<0>(); /* the clamped refills past the last pair */
+        }
+    }
+
+    /* normalise and store; rows with an invalid position or sequence get zeros */
+    const float scale_unit = pf_exp2i(st.e_ref - 126);
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        float l = st.l[bl];
+        l += shfl_xor_f(l, 16);
+        l += shfl_xor_f(l, 32);
+        const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
+        if (!(n < R * G && r < a.n)) continue;
+        const bool zero = !(row_valid(a, pos[r], seq[r]) && l > 0.f); /* +0, not o * 0 (which keeps signs) */
+        const float inv = zero ? 0.f : scale_unit / l;
+        bf16_t *dst = a.out + ((size_t)r * a.hq + h * G + n % G) * NC_HEAD_DIM;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v[8];
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) v[bb] = zero ? 0.f : st.o[bl][bb][i] * inv;
+            store_bf16x8(dst + (4 * j + i) * 8, v);
+        }
+    }
+}
+
+extern "C" int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, int n,
+                                   const uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks,
+                                   int num_seqs, int window, int hq, int hkv, float sm_scale, void *out,
+                                   void *stream) {
+    NC_REQUIRE(n >= 0, "nc_prefill_attn_fp8: n = %d < 0", n);
+    NC_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0 && hq / hkv <= 16,
+               "nc_prefill_attn_fp8: need hq %% hkv == 0 and 1 <= hq / hkv <= 16 (hq %d, hkv %d)", hq, hkv);
+    NC_REQUIRE(max_blocks > 0 && num_blocks > 0 && num_seqs > 0,
+               "nc_prefill_attn_fp8: max_blocks %d, num_blocks %d, num_seqs %d must be positive", max_blocks,
+               num_blocks, num_seqs);
+    NC_REQUIRE((long long)num_blocks * hkv * NC_TILE_BYTES < (1ll << 47), "nc_prefill_attn_fp8: pool too large");
+    NC_REQUIRE(block_table || (long long)num_seqs * max_blocks <= num_blocks,
+               "nc_prefill_attn_fp8: a contiguous cache needs num_seqs * max_blocks <= num_blocks");
+    if (n == 0) return 0;
+    NC_REQUIRE(q && pos && seq && cache && out, "nc_prefill_attn_fp8: null pointer");
+    NC_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)cache & 15) == 0,
+               "nc_prefill_attn_fp8: q, out and cache must be 16-byte aligned");
+    PrefillArgs a;
+    a.q = static_cast<const bf16_t *>(q);
+    a.n = n;
+    a.cache = cache;
+    a.max_blocks = max_blocks;
+    a.num_blocks = num_blocks;
+    a.num_seqs = num_seqs;
+    a.window = window;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.group = hq / hkv;
+    a.rows_per_block = 16 / a.group;
+    a.score_scale = sm_scale * 1.4426950408889634f;
+    a.out = static_cast<bf16_t *>(out);
+    const int tr = PF_WAVES * PF_BLOCKS * a.rows_per_block;
+    a.tiles = (n + tr - 1) / tr;
+    const long long units = (long long)hkv * a.tiles;
+    NC_REQUIRE(units <= (1ll << 30), "nc_prefill_attn_fp8: too many rows");
+    a.units_per_xcd = (int)((units + 7) / 8);
+    hipLaunchKernelGGL(k_prefill, dim3(8 * a.units_per_xcd), dim3(PF_THREADS), 0, (hipStream_t)stream, a, pos, seq,
+                       block_table);
+    NC_LAUNCH_CHECK();
+    return 0;
+}

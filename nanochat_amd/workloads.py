@@ -47,6 +47,30 @@ CONFIG3 = DecodeConfig("cfg3-ragged-gqa-b64-h16/4-ctx512..8192-paged16", 64, 16,
                        paged=True, outliers=0.01, seed=3)
 
 
+@dataclass(frozen=True)
+class PrefillConfig:
+    """One chunked-prefill configuration: every sequence holds `cached` tokens and appends a `chunk`-token chunk
+    (QK-norm + RoPE + quantise), then the chunk's rows attend causally over the cache (its own keys included)."""
+    name: str
+    batch: int
+    hq: int
+    hkv: int
+    cached: tuple[int, ...]
+    chunk: tuple[int, ...]
+    paged: bool = False
+    outliers: float = 0.0
+    theta: float = 10000.0
+    window: int = -1
+    seed: int = 0
+
+    def per_seq(self, v: tuple[int, ...]) -> np.ndarray:
+        return np.array(v if len(v) == self.batch else v * self.batch, dtype=np.int64)[:self.batch]
+
+
+# BASELINE.json config 4: 8 sequences append a 512-token chunk onto 3584 cached tokens, 16 / 4 heads, θ = 1e4.
+CONFIG4 = PrefillConfig("cfg4-prefill-b8-h16/4-cache3584+chunk512", 8, 16, 4, cached=(3584,), chunk=(512,), seed=4)
+
+
 def seeded_normal(shape, seed: int, device, outliers: float = 0.0) -> torch.Tensor:
     """N(0, 1) fp32 -> bf16 (RNE), with a seeded fraction of elements replaced by ±8."""
     g = torch.Generator(device=device).manual_seed(seed)
@@ -131,6 +155,55 @@ def decode_step(case: DecodeCase, step: int, max_ctx: int, out: torch.Tensor | N
     o = decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=case.cfg.window, out=out,
                          workspace=workspace)
     return q, o
+
+
+@dataclass
+class PrefillCase:
+    cfg: PrefillConfig
+    cache: Fp8KVCache
+    cached: np.ndarray              # tokens already in the cache per sequence (host)
+    chunk: np.ndarray               # chunk length per sequence (host)
+    qkv: torch.Tensor               # [rows][(hq + 2 hkv) 128] bf16, the chunk rows sequence by sequence
+    pos: torch.Tensor               # [rows] int32
+    seq: torch.Tensor               # [rows] int32
+    q_gain: torch.Tensor
+    k_gain: torch.Tensor
+    cos: torch.Tensor
+    sin: torch.Tensor
+
+
+def build_prefill_case(cfg: PrefillConfig, device) -> PrefillCase:
+    """The cache holding each sequence's cached tokens and the chunk's projection rows, in sequence order."""
+    cached, chunk = cfg.per_seq(cfg.cached), cfg.per_seq(cfg.chunk)
+    dcfg = DecodeConfig(cfg.name, cfg.batch, cfg.hq, cfg.hkv, ctx=tuple(int(c) for c in cached), paged=cfg.paged,
+                        outliers=cfg.outliers, theta=cfg.theta, window=cfg.window, seed=cfg.seed)
+    cap = int((cached + chunk).max())
+    base = build_decode_case(dcfg, device, steps=max(cap - int(cached.min()), 1))
+    cache = base.cache
+    rows = int(chunk.sum())
+    qkv = seeded_normal((rows, (cfg.hq + 2 * cfg.hkv) * HEAD_DIM), cfg.seed * 1000 + 555, device, cfg.outliers)
+    pos = np.concatenate([np.arange(c, c + k) for c, k in zip(cached, chunk)]).astype(np.int32)
+    seq = np.repeat(np.arange(cfg.batch), chunk).astype(np.int32)
+    cos, sin = rotary_tables(cap, cfg.theta, device)
+    return PrefillCase(cfg, cache, cached, chunk, qkv, torch.from_numpy(pos).to(device),
+                       torch.from_numpy(seq).to(device), base.q_gain, base.k_gain, cos, sin)
+
+
+def prefill_step(case: PrefillCase, out: torch.Tensor | None = None):
+    """Append the whole chunk, then every chunk row attends (the reference's order, decode.cu:859-863).
+    Returns (q, out)."""
+    from nanochat_amd.attention import prefill_attention
+
+    q = case.cache.append(case.qkv, case.pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, case.cfg.hq)
+    o = prefill_attention(q, case.cache, case.pos, case.seq, window=case.cfg.window, out=out)
+    return q, o
+
+
+def prefill_flops(pos: np.ndarray, hq: int, window: int = -1) -> int:
+    """Algorithmic flops of prefill attention: per (row, query head, attended key) 2 * 128 for QK and 2 * 128
+    for PV."""
+    keys = pos + 1 if window < 0 else np.minimum(pos + 1, window + 1)
+    return int(keys.sum()) * hq * 4 * HEAD_DIM
 
 
 def decode_bytes(ctx_len: np.ndarray, hkv: int, window: int = -1) -> int:

@@ -226,20 +226,33 @@ def key_range(p: int, window: int) -> tuple[int, int]:
 
 
 def _kv_dequantized(cache: PagedCache, b: int, h: int, lo: int, hi: int, block_table, max_blocks):
+    """Dequantised K, V of keys [lo, hi) of sequence b, kv head h, and which keys have a block (a page past
+    max_blocks, or a table entry outside [0, num_blocks), has none: its keys are skipped, as by the kernels'
+    lookup_block)."""
     t = np.arange(lo, hi)
-    blk = PagedCache.block_of(np.full_like(t, b), t, block_table, max_blocks)
+    page = t // PAGE
+    present = page < max_blocks
+    if block_table is None:
+        blk = b * max_blocks + page
+    else:
+        blk = np.asarray(block_table, np.int64)[b, np.minimum(page, max_blocks - 1)]
+    present &= (blk >= 0) & (blk < cache.num_blocks)
+    blk = np.where(present, blk, 0)
     kc, vc, ks, vs = cache.read(blk, h, t % PAGE)
-    return dequantize(kc, ks).astype(np.float64), dequantize(vc, vs).astype(np.float64)
+    return dequantize(kc, ks).astype(np.float64), dequantize(vc, vs).astype(np.float64), present
 
 
 def softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, mask: np.ndarray | None = None):
-    """softmax(q kᵀ scale [+ mask]) v in fp64; q [m][128], k, v [n][128]; mask True = excluded."""
+    """softmax(q kᵀ scale [+ mask]) v in fp64; q [m][128], k, v [n][128]; mask True = excluded. A row with every
+    key excluded is zero."""
     s = (q @ k.T) * scale
     if mask is not None:
         s = np.where(mask, -np.inf, s)
-    s = s - s.max(axis=-1, keepdims=True)
-    p = np.exp(s)
-    return (p @ v) / p.sum(axis=-1, keepdims=True)
+    top = s.max(axis=-1, keepdims=True)
+    empty = ~np.isfinite(top)
+    p = np.exp(s - np.where(empty, 0.0, top))
+    den = p.sum(axis=-1, keepdims=True)
+    return np.where(empty, 0.0, (p @ v) / np.where(empty, 1.0, den))
 
 
 def decode_attention(q_bits: np.ndarray, cache: PagedCache, block_table: np.ndarray | None, max_blocks: int,
@@ -253,8 +266,8 @@ def decode_attention(q_bits: np.ndarray, cache: PagedCache, block_table: np.ndar
     for b in range(B):
         lo, hi = key_range(int(ctx_len[b]) - 1, window)
         for h in range(hkv):
-            k, v = _kv_dequantized(cache, b, h, lo, hi, block_table, max_blocks)
-            out[b, h * G:(h + 1) * G] = softmax_attend(q[b, h * G:(h + 1) * G], k, v, sm_scale)
+            k, v, present = _kv_dequantized(cache, b, h, lo, hi, block_table, max_blocks)
+            out[b, h * G:(h + 1) * G] = softmax_attend(q[b, h * G:(h + 1) * G], k, v, sm_scale, ~present[None, :])
     return out
 
 
@@ -278,7 +291,31 @@ def prefill_attention(q_bits: np.ndarray, cu_q: np.ndarray, q_start: np.ndarray,
         begin = np.array([key_range(int(x), window)[0] for x in p])
         mask = (keys[None, :] > p[:, None]) | (keys[None, :] < begin[:, None])
         for h in range(hkv):
-            k, v = _kv_dequantized(cache, b, h, lo, hi, block_table, max_blocks)
+            k, v, present = _kv_dequantized(cache, b, h, lo, hi, block_table, max_blocks)
             for g in range(G):
-                out[r0:r1, h * G + g] = softmax_attend(q[r0:r1, h * G + g], k, v, sm_scale, mask)
+                out[r0:r1, h * G + g] = softmax_attend(q[r0:r1, h * G + g], k, v, sm_scale, mask | ~present)
+    return out
+
+
+def rows_attention(q_bits: np.ndarray, pos: np.ndarray, seq: np.ndarray, cache: PagedCache,
+                   block_table: np.ndarray | None, max_blocks: int, num_seqs: int, window: int, hq: int, hkv: int,
+                   sm_scale: float) -> np.ndarray:
+    """Prefill attention over arbitrary rows (dec_prefill's rows, decode.cu:1039-1051, each a k_attn query): row r
+    at position pos[r] of sequence seq[r] attends keys [max(p - window, 0), p] of the fp8 cache; rows with
+    pos < 0 or seq outside [0, num_seqs) are zero; fp64 [n][hq][128]."""
+    G = hq // hkv
+    q = bf16_to_f32(q_bits).astype(np.float64)
+    out = np.zeros(q.shape, np.float64)
+    valid = (pos >= 0) & (seq >= 0) & (seq < num_seqs)
+    for s in np.unique(seq[valid]):
+        rows = np.nonzero(valid & (seq == s))[0]
+        p = pos[rows].astype(np.int64)
+        begin = np.array([key_range(int(x), window)[0] for x in p])
+        lo, hi = int(begin.min()), int(p.max()) + 1
+        keys = np.arange(lo, hi)
+        mask = (keys[None, :] > p[:, None]) | (keys[None, :] < begin[:, None])
+        for h in range(hkv):
+            k, v, present = _kv_dequantized(cache, int(s), h, lo, hi, block_table, max_blocks)
+            for g in range(G):
+                out[rows, h * G + g] = softmax_attend(q[rows, h * G + g], k, v, sm_scale, mask | ~present)
     return out

@@ -82,3 +82,26 @@ def test_stale_library_is_detected(tmp_path, monkeypatch):
     assert build.is_current()
     monkeypatch.setattr(build, "STAMP", tmp_path / "missing.sha256")
     assert not build.is_current()
+
+
+def test_prefill_rejects_bad_arguments():
+    lib = native.hip_library()
+    #       q     pos   seq   n   cache table max_blocks num_blocks num_seqs window hq hkv scale out   stream
+    base = [FAKE, FAKE, FAKE, 64, FAKE, NULL, 8, 64, 8, -1, 16, 4, 0.08, FAKE, NULL]
+
+    def rejects(i, value, message):
+        args = list(base)
+        args[i] = value
+        assert lib.nc_prefill_attn_fp8(*args) < 0, (i, value)
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    rejects(3, -1, "n = -1")
+    rejects(10, 6, "hq % hkv")
+    rejects(10, 68, "hq / hkv <= 16")
+    rejects(7, 63, "contiguous")
+    rejects(8, 0, "positive")
+    rejects(4, NULL, "null")
+    rejects(0, ctypes.c_void_p(0x1008), "aligned")
+    empty = list(base)
+    empty[3] = 0
+    assert lib.nc_prefill_attn_fp8(*empty) == 0  # nothing to do, nothing launched

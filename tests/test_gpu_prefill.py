@@ -1,0 +1,99 @@
+"""GPU parity of chunked prefill (append the whole chunk, then MFMA attention of every chunk row over the fp8 cache)
+against the oracle: bit-exact q rows and cache bytes for the append, and attention within the benchmark tolerance
+(max abs <= 2e-2, mean <= 2e-3) of the fp64 oracle over the same cache bytes."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attention_close, assert_same_cache, bits, oracle_cache, table
+from nanochat_amd.attention import decode_attention, prefill_attention
+from nanochat_amd.workloads import CONFIG4, PrefillConfig, build_prefill_case, prefill_step
+from oracle import golden as G
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1 / math.sqrt(128)
+
+
+def oracle_rows(case, q, pos, seq, window):
+    return G.rows_attention(bits(q), pos.cpu().numpy(), seq.cpu().numpy(), oracle_cache(case.cache),
+                            table(case.cache), case.cache.max_blocks, case.cache.num_seqs, window, case.cfg.hq,
+                            case.cfg.hkv, SCALE)
+
+
+def run_and_check(cfg: PrefillConfig, dev, check_append: bool = False):
+    print(f"prefill case {cfg.name}", flush=True)
+    case = build_prefill_case(cfg, dev)
+    before = oracle_cache(case.cache) if check_append else None
+    q, out = prefill_step(case)
+    torch.cuda.synchronize()
+    if check_append:
+        q_ref = G.append(before, bits(case.qkv), case.pos.cpu().numpy(), case.seq.cpu().numpy(),
+                         case.q_gain.cpu().numpy(), case.k_gain.cpu().numpy(), case.cos.cpu().numpy(),
+                         case.sin.cpu().numpy(), cfg.hq, cfg.hkv, table(case.cache), case.cache.max_blocks)
+        np.testing.assert_array_equal(bits(q), q_ref)
+        assert_same_cache(case.cache, before)
+    want = oracle_rows(case, q, case.pos, case.seq, cfg.window)
+    return assert_attention_close(out, want, cfg.name)
+
+
+def test_config4_full_size(gpu):
+    run_and_check(CONFIG4, gpu, check_append=True)
+
+
+@pytest.mark.parametrize("cfg", [
+    PrefillConfig("mha-g1", 2, 4, 4, cached=(100, 1000), chunk=(300, 45), paged=True, seed=41),
+    PrefillConfig("g16-one-kv-head", 2, 16, 1, cached=(0, 700), chunk=(37, 5), seed=42),
+    PrefillConfig("g3-window64", 1, 6, 2, cached=(500,), chunk=(77,), window=64, paged=True, seed=43),
+    PrefillConfig("g8-window-not-aligned", 3, 8, 1, cached=(900, 17, 250), chunk=(20, 100, 9), window=100, seed=44),
+    PrefillConfig("ragged-chunks-cross-tiles", 5, 16, 4, cached=(3, 60, 1, 300, 31), chunk=(7, 13, 3, 29, 1),
+                  paged=True, outliers=0.01, seed=45),
+    PrefillConfig("long-over-1024-pages", 1, 4, 1, cached=(17000,), chunk=(40,), paged=True, seed=46),
+])
+def test_prefill_edge_shapes(gpu, cfg):
+    run_and_check(cfg, gpu)
+
+
+def test_rows_in_any_order_and_invalid_rows(gpu):
+    """Shuffled rows (so tiles mix sequences and positions) give the oracle's per-row result; rows with pos < 0 or
+    a sequence out of range are zero and disturb no other row."""
+    dev = gpu
+    cfg = PrefillConfig("shuffled", 3, 8, 2, cached=(200, 40, 513), chunk=(50, 21, 64), paged=True, seed=51)
+    case = build_prefill_case(cfg, dev)
+    q, _ = prefill_step(case)
+    perm = torch.from_numpy(np.random.default_rng(52).permutation(q.shape[0])).to(dev)
+    qp, pos, seq = q[perm].contiguous(), case.pos[perm].contiguous(), case.seq[perm].contiguous()
+    pos[5], seq[9], seq[10] = -1, 3, -2
+    out = prefill_attention(qp, case.cache, pos, seq)
+    torch.cuda.synchronize()
+    want = oracle_rows(case, qp, pos, seq, -1)
+    assert not bits(out[[5, 9, 10]]).any()
+    assert_attention_close(out, want, "shuffled")
+
+
+def test_missing_blocks_are_skipped(gpu):
+    dev = gpu
+    cfg = PrefillConfig("holes", 2, 4, 2, cached=(300, 300), chunk=(40, 40), paged=True, seed=61)
+    case = build_prefill_case(cfg, dev)
+    q, _ = prefill_step(case)
+    case.cache.block_table[0, 3] = -1           # keys 48..63 of sequence 0
+    case.cache.block_table[1, 5] = 10 ** 6      # beyond the pool
+    out = prefill_attention(q, case.cache, case.pos, case.seq)
+    torch.cuda.synchronize()
+    assert_attention_close(out, oracle_rows(case, q, case.pos, case.seq, -1), "holes")
+
+
+def test_single_rows_agree_with_decode(gpu):
+    """One row per sequence at its last position is a decode step: the two kernels agree closely."""
+    dev = gpu
+    cfg = PrefillConfig("as-decode", 4, 16, 4, cached=(1000, 2047, 16, 5000), chunk=(1,), paged=True, seed=71)
+    case = build_prefill_case(cfg, dev)
+    q, out = prefill_step(case)
+    ctx = case.pos + 1
+    dec = decode_attention(q, case.cache, ctx, max_ctx=case.cache.capacity)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float(), dec.float(), atol=4e-3, rtol=2e-2)
+    assert_attention_close(out, oracle_rows(case, q, case.pos, case.seq, -1), "as-decode")

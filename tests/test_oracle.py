@@ -334,3 +334,52 @@ def test_prefill_attention_reduces_to_decode_and_is_causal():
     out2 = G.prefill_attention(q, cu, start, c, bt, mb, -1, hq, hkv, scale)
     np.testing.assert_array_equal(out2[:15], out[:15])
     assert not np.array_equal(out2[15], out[15])
+
+
+def test_rows_attention_matches_chunks_any_order_and_skips_invalid_rows():
+    """The per-row restatement equals the per-chunk one, is equivariant under any row order, gives zero rows for
+    invalid (pos, seq) and with a window keeps only the last window + 1 keys."""
+    hq, hkv = 6, 2
+    scale = 128 ** -0.5
+    ctx = [70, 45]
+    c, bt, mb = make_cache(ctx, hkv, 21, table=True)
+    q = random_bf16((30 + 12, hq, 128), 22)
+    cu, start = np.array([0, 30, 42]), np.array([40, 33])
+    pos = np.concatenate([start[0] + np.arange(30), start[1] + np.arange(12)])
+    seq = np.repeat([0, 1], [30, 12])
+    for window in (-1, 7):
+        want = G.prefill_attention(q, cu, start, c, bt, mb, window, hq, hkv, scale)
+        got = G.rows_attention(q, pos, seq, c, bt, mb, 2, window, hq, hkv, scale)
+        np.testing.assert_array_equal(got, want)
+        perm = np.random.default_rng(23).permutation(len(pos))
+        shuffled = G.rows_attention(q[perm], pos[perm], seq[perm], c, bt, mb, 2, window, hq, hkv, scale)
+        np.testing.assert_allclose(shuffled, want[perm], rtol=1e-13, atol=1e-15)
+    bad_pos, bad_seq = pos.copy(), seq.copy()
+    bad_pos[3], bad_seq[5], bad_seq[6] = -1, 2, -4
+    out = G.rows_attention(q, bad_pos, bad_seq, c, bt, mb, 2, -1, hq, hkv, scale)
+    assert not out[[3, 5, 6]].any()
+    keep = np.setdiff1d(np.arange(len(pos)), [3, 5, 6])
+    np.testing.assert_array_equal(out[keep], G.rows_attention(q, pos, seq, c, bt, mb, 2, -1, hq, hkv, scale)[keep])
+
+
+def test_missing_blocks_are_skipped():
+    """A hole in the block table removes that page's keys: the same as attending the remaining keys directly;
+    a row whose keys are all missing is zero."""
+    hq, hkv = 2, 1
+    scale = 128 ** -0.5
+    c, bt, mb = make_cache([64], hkv, 31, table=True)
+    q = random_bf16((1, hq, 128), 32)
+    holed = bt.copy()
+    holed[0, 1] = -1  # keys 16..31
+    out = G.decode_attention(q, c, holed, mb, np.array([64]), -1, hq, hkv, scale)
+    k, v, ks, vs = G.gather(c, bt, mb, np.array([64]), 64)
+    keep = np.r_[0:16, 32:64]
+    kd = G.dequantize(k[0, 0, keep], ks[0, 0, keep]).astype(np.float64)
+    vd = G.dequantize(v[0, 0, keep], vs[0, 0, keep]).astype(np.float64)
+    qf = G.bf16_to_f32(q).astype(np.float64)
+    for h in range(hq):
+        w = np.exp((kd @ qf[0, h]) * scale - ((kd @ qf[0, h]) * scale).max())
+        np.testing.assert_allclose(out[0, h], (w @ vd) / w.sum(), rtol=1e-12)
+    holed[0, :] = -1
+    assert not G.decode_attention(q, c, holed, mb, np.array([64]), -1, hq, hkv, scale).any()
+    assert not G.rows_attention(q, np.array([63]), np.array([0]), c, holed, mb, 1, -1, hq, hkv, scale).any()
