@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode-attn HBM GB/s (% of peak) + decode tokens/sec, bs64 ctx8K"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFS = 2500.0  # dense bf16 / fp16 MFMA, MI355X
 ATTN_REPS = 10  # decode-attention calls per timed graph replay: the replay-to-replay gap is not kernel time
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_attn_traffic.json")
 
@@ -38,6 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 2 decode and config 4 prefill lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the measurement, copy a 1 GiB buffer 3 times (the byte-counter calibration kernel)")
     return ap.parse_args()
@@ -75,6 +77,68 @@ def copy_probe(dev) -> None:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
+
+
+def time_calls(fn, calls: int, replays: int, stream) -> float:
+    """Mean GPU time (ms) of one fn() call: a graph of `calls` back-to-back calls replayed `replays` times, HIP
+    events on the replay stream."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        fn()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(calls):
+                fn()
+        graph.replay()
+    return replay_ms(graph, replays, stream) / calls
+
+
+def extra_decode_cfg2(dev, stream) -> dict:
+    """Config 2 (B 32, 10/10 heads, ctx 4096 contiguous): one decode-attention call after the step's append."""
+    from nanochat_amd.attention import decode_attention, decode_workspace
+    from nanochat_amd.workloads import CONFIG2, build_decode_case, decode_bytes
+
+    cfg = CONFIG2
+    case = build_decode_case(cfg, dev, steps=1)
+    pos = case.positions(0)
+    q = case.cache.append(case.qkv[0], pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    ctx = pos + 1
+    ws = decode_workspace(cfg.batch, cfg.hq, cfg.hkv, case.cache.capacity, dev)
+    out = torch_empty_like(q)
+    ms = time_calls(lambda: decode_attention(q, case.cache, ctx, max_ctx=case.cache.capacity, out=out, workspace=ws),
+                    ATTN_REPS, 20, stream)
+    nbytes = decode_bytes(case.ctx + 1, cfg.hkv, cfg.window)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "bytes": int(nbytes), "GB_s": round(gbs, 2),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def extra_prefill_cfg4(dev, stream) -> dict:
+    """Config 4 (B 8, 16/4 heads, 3584 cached + 512-token chunk): the chunk's append, then prefill attention; the
+    attention call timed alone (MFMA-bound: algorithmic flops over time against the dense bf16 peak)."""
+    from nanochat_amd.attention import prefill_attention
+    from nanochat_amd.workloads import CONFIG4, build_prefill_case, prefill_flops
+
+    cfg = CONFIG4
+    case = build_prefill_case(cfg, dev)
+    q = case.cache.append(case.qkv, case.pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    out = torch_empty_like(q)
+    ms = time_calls(lambda: prefill_attention(q, case.cache, case.pos, case.seq, out=out), ATTN_REPS, 10, stream)
+    append_ms = time_calls(lambda: case.cache.append(case.qkv, case.pos, case.seq, case.q_gain, case.k_gain, case.cos,
+                                                     case.sin, cfg.hq), ATTN_REPS, 10, stream)
+    flops = prefill_flops(case.pos.cpu().numpy(), cfg.hq, cfg.window)
+    tfs = flops / (ms * 1e-3) / 1e12
+    return {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "append_us": round(append_ms * 1e3, 3),
+            "flops": flops, "TFLOP_s": round(tfs, 1), "bound": "mfma", "peak_TFLOP_s": MFMA_PEAK_TFS,
+            "frac_of_mfma_peak": round(tfs / MFMA_PEAK_TFS, 4)}
+
+
+def torch_empty_like(t):
+    import torch
+
+    return torch.empty_like(t)
 
 
 def cpu_baseline(case, final_ctx: np.ndarray, q, budget_s: float) -> dict:
@@ -196,6 +260,9 @@ def main():
                                f"{ATTN_REPS} calls, HIP events on their stream",
                      "bytes_per_launch": int(attn_bytes)},
     }
+    if not args.no_extra:
+        result["decode_cfg2"] = extra_decode_cfg2(dev, stream)
+        result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream)
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:

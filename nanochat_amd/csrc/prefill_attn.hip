@@ -25,9 +25,14 @@
  *
  * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
  * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
- * conflict-free ds_read_b128 per fragment). Each wave issues 3 of a pair's 10 DMAs (two 1 KiB fragment loads,
- * one 64 B scale quarter), PF_RING - 1 pairs ahead; per pair: wait for its own DMAs, s_barrier, refill the slot
- * freed by the previous pair, read, compute. Block ids are staged in LDS per chunk of PF_IDS pages.
+ * conflict-free ds_read_b128 per fragment). Each of the 8 waves issues 2 of a pair's 10 DMAs (one 1 KiB fragment
+ * load, one 32 B part of the scales) from a scalar tile base, PF_RING - 1 pairs ahead. Block ids are staged in
+ * LDS per chunk of PF_IDS pages.
+ *
+ * Software pipeline: iteration k issues the score MFMAs of pair k + 1 and, independent of them, the softmax and
+ * the value MFMAs of pair k. A wave's VALU work does not issue under its own MFMAs on gfx950 (measured: an MFMA
+ * plus 4 independent v_mul cost their sum), but it does under the other wave's on the same SIMD; the pipeline
+ * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps.
  */
 #include "layout.h"
 
@@ -41,9 +46,7 @@
 #ifndef PF_RING
 #define PF_RING 8          /* page-pair slots: 7 pairs (59 KB) in flight while one is computed */
 #endif
-#define PF_FRAGS_PER_WAVE (8 / PF_WAVES)         /* of a pair's eight 1 KiB fragment DMAs */
-#define PF_SCALE_BYTES (256 / PF_WAVES)          /* of a pair's 256 B of scales */
-#define PF_DMA_PER_PAIR (PF_FRAGS_PER_WAVE + 1)  /* per wave */
+#define PF_DMA_PER_PAIR 2  /* per wave: one fragment, one scale part */
 #define PF_PAIR_BYTES (2 * NC_TILE_BYTES)
 #define PF_IDS 1024        /* block ids staged per chunk of a segment's pages */
 #define PF_LAZY 8.0f
@@ -102,67 +105,96 @@ template <int N> __device__ __forceinline__ void pf_wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-/* This wave's DMAs of a page pair: PF_FRAGS_PER_WAVE of the pair's eight 1 KiB fragments (K bytes 0-15 and 16-31
- * of every lane, then V bytes 0-15 and 16-31, of the first page then of the second) and a PF_SCALE_BYTES part of
- * the pair's scales. blk < 0 (no block) loads block 0, masked later. */
-__device__ __forceinline__ void dma_pair(const PrefillArgs &a, int blk0, int blk1, int h, int wv, int lane,
-                                         unsigned char *slot) {
-    const int n = lane & 15, j = lane >> 4;
-#pragma unroll
-    for (int f = 0; f < PF_FRAGS_PER_WAVE; f++) {
-        const int fid = wv * PF_FRAGS_PER_WAVE + f, pg = fid >> 2, part = fid & 3;
-        const int blk = pg ? blk1 : blk0;
-        const uint8_t *tile = a.cache + tile_offset(blk < 0 ? 0 : blk, h, a.hkv);
-        const uint8_t *src = part < 2 ? tile + n * NC_HEAD_DIM + j * 32 : tile + NC_TILE_V + j * 512 + n * 32;
-        __builtin_amdgcn_global_load_lds(src + 16 * (part & 1), slot + pg * NC_TILE_BYTES + part * 1024, 16, 0, 0);
-    }
-    const int sb = wv * PF_SCALE_BYTES, pg = sb >> 7, off = sb & 127;
-    const int blk = pg ? blk1 : blk0;
-    const uint8_t *tile = a.cache + tile_offset(blk < 0 ? 0 : blk, h, a.hkv);
-    if (lane < PF_SCALE_BYTES / 16)
-        __builtin_amdgcn_global_load_lds(tile + NC_TILE_KS + off + 16 * lane, slot + pg * NC_TILE_BYTES + NC_TILE_KS + off,
-                                         16, 0, 0);
-}
-
-/* One page's fragments for this lane: K bytes (dims 32j.. of key n), V quad bytes (dims 8n.. of keys 4j..), and the
- * K / V scales of keys 4j..4j+3. */
-struct PfPage {
-    u32x4 k0, k1, v0, v1, ks, vs;
+/* This wave's share of a pair's DMAs: fragment `part` (K bytes 0-15 / 16-31 of every lane, V bytes 0-15 / 16-31)
+ * of page `page` of the pair, and a 32 B part of that page's scales (lanes 0-1). Per-lane byte offsets within a
+ * tile are fixed for the whole loop; the tile base is wave-uniform. */
+struct PfDma {
+    uint32_t frag, scale;
+    int page, part;
 };
 
-/* Both pages of a slot, the pair's two block ids, and the two block ids of pair `next_pair` for the next
- * refill. Inline ds_reads with their own lgkmcnt wait: as plain LDS loads the compiler would precede them
- * with s_waitcnt vmcnt(0) (it cannot tell them from the ring's in-flight DMA writes) and drain the ring. */
-__device__ __forceinline__ void read_pair(const unsigned char *slot, const int *ids, int pair, int next_pair, int lane,
-                                          PfPage &pa, PfPage &pb, int &ida, int &idb, u32x2 &id_next) {
-    const int j = lane >> 4;
-    const uint32_t base = (uint32_t)(uintptr_t)(const lds_u8 *)slot;
-    const uint32_t mine = base + 16 * lane, sc = base + NC_TILE_KS + 16 * j;
-    const uint32_t idp = (uint32_t)(uintptr_t)(const lds_u8 *)(const unsigned char *)(ids + 2 * pair);
-    const uint32_t idn = (uint32_t)(uintptr_t)(const lds_u8 *)(const unsigned char *)(ids + 2 * next_pair);
-    u32x2 id2;
+__device__ __forceinline__ PfDma dma_plan(int wv, int lane) {
+    static_assert(PF_WAVES == 8, "one fragment and one scale part per wave");
+    const int n = lane & 15, j = lane >> 4;
+    PfDma d;
+    d.page = wv >> 2;
+    d.part = wv & 3;
+    d.frag = (d.part < 2 ? n * NC_HEAD_DIM + j * 32 : NC_TILE_V + j * 512 + n * 32) + 16 * (d.part & 1);
+    d.scale = NC_TILE_KS + 32 * d.part + 16 * lane;
+    return d;
+}
+
+__device__ __forceinline__ void dma_pair(const PrefillArgs &a, int blk0, int blk1, int h, const PfDma &d, int lane,
+                                         unsigned char *slot) {
+    int blk = d.page ? blk1 : blk0;
+    blk = blk < 0 ? 0 : blk; /* no block: load block 0, masked later */
+    const uint8_t *tile = a.cache + ((size_t)blk * a.hkv + h) * NC_TILE_BYTES;
+    unsigned char *dst = slot + d.page * NC_TILE_BYTES;
+    __builtin_amdgcn_global_load_lds(tile + d.frag, dst + d.part * 1024, 16, 0, 0);
+    if (lane < 2) __builtin_amdgcn_global_load_lds(tile + d.scale, dst + NC_TILE_KS + 32 * d.part, 16, 0, 0);
+}
+
+/* K fragments of a pair for the score MFMAs: dims 32j.. of key n, both pages. */
+struct PfKeys {
+    u32x4 a0, a1, b0, b1;
+};
+
+/* V quad fragments of a pair for the value MFMAs (dims 8n.. of keys 4j..4j+3, both pages), and the K and V scales
+ * of keys 4j..4j+3 of both pages. */
+struct PfVals {
+    u32x4 a0, a1, b0, b1, ks_a, ks_b, vs_a, vs_b;
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_u8 *)(const unsigned char *)p;
+}
+
+/* The keys of slot_k, the block ids of pair `pair_k` and of pair `pair_dma` (the next refill). Inline ds_reads with
+ * their own lgkmcnt wait: as plain LDS loads the compiler would precede them with s_waitcnt vmcnt(0) (it cannot
+ * tell them from the ring's in-flight DMA writes) and drain the ring. */
+__device__ __forceinline__ void read_keys(const unsigned char *slot_k, const int *ids, int pair_k, int pair_dma,
+                                          int lane, PfKeys &k, u32x2 &ids_k, u32x2 &ids_dma) {
+    const uint32_t mk = lds_addr(slot_k) + 16 * lane;
+    asm volatile(
+        "ds_read_b128 %0, %6\n"
+        "ds_read_b128 %1, %6 offset:1024\n"
+        "ds_read_b128 %2, %6 offset:4224\n"
+        "ds_read_b128 %3, %6 offset:5248\n"
+        "ds_read_b64 %4, %7\n"
+        "ds_read_b64 %5, %8\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k.a0), "=&v"(k.a1), "=&v"(k.b0), "=&v"(k.b1), "=&v"(ids_k), "=&v"(ids_dma)
+        : "v"(mk), "v"(lds_addr(ids + 2 * pair_k)), "v"(lds_addr(ids + 2 * pair_dma))
+        : "memory");
+}
+
+/* As read_keys, plus the values and both scales of slot_v (the pair whose softmax and value MFMAs run this
+ * iteration). */
+__device__ __forceinline__ void read_stage(const unsigned char *slot_v, const unsigned char *slot_k, const int *ids,
+                                           int pair_k, int pair_dma, int lane, PfVals &v, PfKeys &k, u32x2 &ids_k,
+                                           u32x2 &ids_dma) {
+    const uint32_t mv = lds_addr(slot_v) + 16 * lane, sv = lds_addr(slot_v) + NC_TILE_KS + 16 * (lane >> 4);
+    const uint32_t mk = lds_addr(slot_k) + 16 * lane;
     asm volatile(
         "ds_read_b128 %0, %14\n"
         "ds_read_b128 %1, %14 offset:1024\n"
-        "ds_read_b128 %2, %14 offset:2048\n"
-        "ds_read_b128 %3, %14 offset:3072\n"
-        "ds_read_b128 %4, %15\n"
-        "ds_read_b128 %5, %15 offset:64\n"
-        "ds_read_b128 %6, %14 offset:4224\n"
-        "ds_read_b128 %7, %14 offset:5248\n"
-        "ds_read_b128 %8, %14 offset:6272\n"
-        "ds_read_b128 %9, %14 offset:7296\n"
-        "ds_read_b128 %10, %15 offset:4224\n"
-        "ds_read_b128 %11, %15 offset:4288\n"
-        "ds_read_b64 %12, %16\n"
-        "ds_read_b64 %13, %17\n"
+        "ds_read_b128 %2, %14 offset:4224\n"
+        "ds_read_b128 %3, %14 offset:5248\n"
+        "ds_read_b64 %12, %15\n"
+        "ds_read_b64 %13, %16\n"
+        "ds_read_b128 %4, %17 offset:2048\n"
+        "ds_read_b128 %5, %17 offset:3072\n"
+        "ds_read_b128 %6, %17 offset:6272\n"
+        "ds_read_b128 %7, %17 offset:7296\n"
+        "ds_read_b128 %8, %18\n"
+        "ds_read_b128 %9, %18 offset:4224\n"
+        "ds_read_b128 %10, %18 offset:64\n"
+        "ds_read_b128 %11, %18 offset:4288\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(pa.k0), "=&v"(pa.k1), "=&v"(pa.v0), "=&v"(pa.v1), "=&v"(pa.ks), "=&v"(pa.vs), "=&v"(pb.k0),
-          "=&v"(pb.k1), "=&v"(pb.v0), "=&v"(pb.v1), "=&v"(pb.ks), "=&v"(pb.vs), "=&v"(id2), "=&v"(id_next)
-        : "v"(mine), "v"(sc), "v"(idp), "v"(idn)
+        : "=&v"(k.a0), "=&v"(k.a1), "=&v"(k.b0), "=&v"(k.b1), "=&v"(v.a0), "=&v"(v.a1), "=&v"(v.b0), "=&v"(v.b1),
+          "=&v"(v.ks_a), "=&v"(v.ks_b), "=&v"(v.vs_a), "=&v"(v.vs_b), "=&v"(ids_k), "=&v"(ids_dma)
+        : "v"(mk), "v"(lds_addr(ids + 2 * pair_k)), "v"(lds_addr(ids + 2 * pair_dma)), "v"(mv), "v"(sv)
         : "memory");
-    ida = (int)id2[0];
-    idb = (int)id2[1];
 }
 
 /* The online-softmax state of a wave's 4 blocks, lane (j, n): column n's reference max m[bl] and this lane's
@@ -184,73 +216,88 @@ struct PfCols {
     bool active;        /* the wave has a column of the segment */
 };
 
-__device__ __forceinline__ void compute_pair(const PrefillArgs &a, const PfPage &pa, const PfPage &pb, int ida, int idb,
-                                             int page0, const PfCols &c, const bf16x8 (*qop)[4], int j, PfState &st) {
-    f32x4 sa[PF_BLOCKS], sb[PF_BLOCKS];
+/* Scores of a pair for every block: s[bl][0] page A, s[bl][1] page B, lane (j, n) keys 4j..4j+3 of column n. */
+__device__ __forceinline__ void pair_scores(const PfKeys &k, const bf16x8 (*qop)[4], f32x4 (*s)[2]) {
 #pragma unroll
-    for (int bl = 0; bl < PF_BLOCKS; bl++) sa[bl] = sb[bl] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int bl = 0; bl < PF_BLOCKS; bl++) s[bl][0] = s[bl][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) { /* one k step of every block per conversion: 8 converted registers live */
-        const u32x4 &fa = kk < 2 ? pa.k0 : pa.k1, &fb = kk < 2 ? pb.k0 : pb.k1;
+        const u32x4 &fa = kk < 2 ? k.a0 : k.a1, &fb = kk < 2 ? k.b0 : k.b1;
         const bf16x8 ka = pf_fp8x8_to_bf16(fa[2 * (kk & 1)], fa[2 * (kk & 1) + 1]);
         const bf16x8 kb = pf_fp8x8_to_bf16(fb[2 * (kk & 1)], fb[2 * (kk & 1) + 1]);
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
-            sa[bl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[bl][kk], sa[bl], 0, 0, 0);
-            sb[bl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop[bl][kk], sb[bl], 0, 0, 0);
+            s[bl][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[bl][kk], s[bl][0], 0, 0, 0);
+            s[bl][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop[bl][kk], s[bl][1], 0, 0, 0);
         }
     }
-    float x[PF_BLOCKS][8];
+}
+
+/* Softmax and value MFMAs of a pair whose scores are s (keys of pages page0, page0 + 1 with blocks ida, idb) and
+ * whose values and scales are v. t = s * k_scale * score_scale - m, so p = exp2(t). */
+__device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const f32x4 (*s)[2], const PfVals &v,
+                                                    int ida, int idb, int page0, const PfCols &c, int j, PfState &st) {
+    float ksc[8], vs[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float ksa = __uint_as_float(pa.ks[i]) * a.score_scale, ksb = __uint_as_float(pb.ks[i]) * a.score_scale;
-#pragma unroll
-        for (int bl = 0; bl < PF_BLOCKS; bl++) {
-            x[bl][i] = sa[bl][i] * ksa;
-            x[bl][4 + i] = sb[bl][i] * ksb;
-        }
+        ksc[i] = __uint_as_float(v.ks_a[i]) * a.score_scale;
+        ksc[4 + i] = __uint_as_float(v.ks_b[i]) * a.score_scale;
+        vs[i] = __uint_as_float(v.vs_a[i]);
+        vs[4 + i] = __uint_as_float(v.vs_b[i]);
     }
-    float vs[8];
+    float t[PF_BLOCKS][8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        vs[i] = __uint_as_float(pa.vs[i]);
-        vs[4 + i] = __uint_as_float(pb.vs[i]);
-    }
-    const int key0 = page0 * NC_PAGE + 4 * j, key1 = key0 + NC_PAGE;
+    for (int bl = 0; bl < PF_BLOCKS; bl++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) t[bl][i] = __builtin_fmaf(s[bl][i >> 2][i & 3], ksc[i], -st.m[bl]);
+    /* masks: wave-uniform test, per-lane keys only on pairs that need it */
+    const int key0 = page0 * NC_PAGE + 4 * j;
     const bool fast = ida >= 0 && idb >= 0 && !c.masked_always && page0 * NC_PAGE >= c.max_lo &&
                       page0 * NC_PAGE + 2 * NC_PAGE - 1 <= c.min_hi;
+    unsigned ok[PF_BLOCKS];
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) ok[bl] = 0xffu;
     if (!fast) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int key = (i < 4 ? key0 : key1 - 4) + i;
+            const int key = key0 + (i < 4 ? i : NC_PAGE + i - 4);
             const bool pg_ok = i < 4 ? ida >= 0 : idb >= 0;
             const bool in_seg = pg_ok && key >= c.seg_lo && key <= c.seg_hi;
             vs[i] = in_seg ? vs[i] : 0.f;
 #pragma unroll
-            for (int bl = 0; bl < PF_BLOCKS; bl++)
-                x[bl][i] = (in_seg && key >= c.lo[bl] && key <= c.hi[bl]) ? x[bl][i] : -INFINITY;
+            for (int bl = 0; bl < PF_BLOCKS; bl++) {
+                const bool keep = in_seg && key >= c.lo[bl] && key <= c.hi[bl];
+                ok[bl] &= ~((keep ? 0u : 1u) << i);
+                t[bl][i] = keep ? t[bl][i] : -INFINITY;
+            }
         }
     }
-
-    float xm[PF_BLOCKS];
     bool need = false;
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
-        xm[bl] = fmaxf(fmaxf(fmaxf(x[bl][0], x[bl][1]), fmaxf(x[bl][2], x[bl][3])),
-                       fmaxf(fmaxf(x[bl][4], x[bl][5]), fmaxf(x[bl][6], x[bl][7])));
-        need |= xm[bl] > st.m[bl] + PF_LAZY;
+        const float tm = fmaxf(fmaxf(fmaxf(t[bl][0], t[bl][1]), fmaxf(t[bl][2], t[bl][3])),
+                               fmaxf(fmaxf(t[bl][4], t[bl][5]), fmaxf(t[bl][6], t[bl][7])));
+        need |= tm > PF_LAZY;
     }
-    if (__any(need)) { /* rare: move the reference max of every block to its exact max, rescale */
+    if (__any(need)) { /* rare: move every block's reference max to its exact max (from the unshifted scores) */
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
-            float mx = fmaxf(xm[bl], shfl_xor_f(xm[bl], 16));
-            mx = fmaxf(mx, shfl_xor_f(mx, 32));
-            const float m_new = fmaxf(st.m[bl], mx);
+            float x[8], xm = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                x[i] = (ok[bl] >> i) & 1 ? s[bl][i >> 2][i & 3] * ksc[i] : -INFINITY;
+                xm = fmaxf(xm, x[i]);
+            }
+            xm = fmaxf(xm, shfl_xor_f(xm, 16));
+            xm = fmaxf(xm, shfl_xor_f(xm, 32));
+            const float m_new = fmaxf(st.m[bl], xm);
             const float alpha = __builtin_amdgcn_exp2f(st.m[bl] - m_new);
             st.l[bl] *= alpha;
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= alpha;
             st.m[bl] = m_new;
+#pragma unroll
+            for (int i = 0; i < 8; i++) t[bl][i] = x[i] - m_new;
         }
     }
     const float vm = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])), fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
@@ -275,15 +322,15 @@ __device__ __forceinline__ void compute_pair(const PrefillArgs &a, const PfPage 
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         float p[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(x[bl][i] - st.m[bl]);
+        for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(t[bl][i]);
         st.l[bl] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 #pragma unroll
         for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vw[i]);
     }
 #pragma unroll
     for (int bb = 0; bb < 8; bb++) {
-        const uint32_t wa = bb < 4 ? pa.v0[bb] : pa.v1[bb - 4];
-        const uint32_t wb = bb < 4 ? pb.v0[bb] : pb.v1[bb - 4];
+        const uint32_t wa = bb < 4 ? v.a0[bb] : v.a1[bb - 4];
+        const uint32_t wb = bb < 4 ? v.b0[bb] : v.b1[bb - 4];
         const f16x8 va = pf_v_operand(wa, wb);
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++)
@@ -408,32 +455,55 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             for (int e = tid; e < 2 * npairs; e += PF_THREADS)
                 ids[e] = e < cp ? lookup_block(block_table, a.max_blocks, a.num_blocks, s, first + cb + e) : -1;
             __syncthreads();
+            const PfDma dp = dma_plan(wv, lane);
             int pro[PF_RING - 1][2];
 #pragma unroll
             for (int k = 0; k < PF_RING - 1; k++) {
-                pro[k][0] = ids[2 * min(k, npairs - 1)];
-                pro[k][1] = ids[2 * min(k, npairs - 1) + 1];
+                pro[k][0] = __builtin_amdgcn_readfirstlane(ids[2 * min(k, npairs - 1)]);
+                pro[k][1] = __builtin_amdgcn_readfirstlane(ids[2 * min(k, npairs - 1) + 1]);
             }
-            u32x2 id_next = *reinterpret_cast<const u32x2 *>(ids + 2 * min(PF_RING - 1, npairs - 1));
 #pragma unroll
             for (int k = 0; k < PF_RING - 1; k++) {
                 __builtin_amdgcn_sched_barrier(0);
-                dma_pair(a, pro[k][0], pro[k][1], h, wv, lane, ring + k * PF_PAIR_BYTES);
+                dma_pair(a, pro[k][0], pro[k][1], h, dp, lane, ring + k * PF_PAIR_BYTES);
             }
             __builtin_amdgcn_sched_barrier(0);
-            for (int k = 0; k < npairs; k++) {
-                pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 2)>(); /* this wave's DMAs of pair k have landed */
+            /* pipeline fill: the scores of pair 0 */
+            pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 2)>(); /* this wave's DMAs of pair 0 have landed */
+            __builtin_amdgcn_s_barrier();                      /* everyone's have */
+            __builtin_amdgcn_sched_barrier(0);
+            PfKeys kf;
+            u32x2 ids_cur, ids_dma;
+            read_keys(ring, ids, 0, min(PF_RING - 1, npairs - 1), lane, kf, ids_cur, ids_dma);
+            f32x4 s0[PF_BLOCKS][2], s1[PF_BLOCKS][2];
+            if (c.active) pair_scores(kf, qop, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            /* iteration k: the scores of pair k + 1 into one buffer while pair k's softmax and values read the other
+             * (unrolled twice so the buffers swap without copies) */
+            auto step = [&](int k, f32x4 (*s_cur)[2], f32x4 (*s_next)[2]) {
+                pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 3)>(); /* this wave's DMAs of pair k + 1 have landed */
                 __builtin_amdgcn_s_barrier();                      /* everyone's have; slot k - 1 is free */
                 __builtin_amdgcn_sched_barrier(0);
                 const int kr = k + PF_RING - 1;
-                dma_pair(a, (int)id_next[0], (int)id_next[1], h, wv, lane, ring + (kr % PF_RING) * PF_PAIR_BYTES);
-                PfPage pa, pb;
-                int ida, idb;
-                read_pair(ring + (k % PF_RING) * PF_PAIR_BYTES, ids, k, min(kr + 1, npairs - 1), lane, pa, pb, ida, idb,
-                          id_next);
+                dma_pair(a, __builtin_amdgcn_readfirstlane((int)ids_dma[0]),
+                         __builtin_amdgcn_readfirstlane((int)ids_dma[1]), h, dp, lane,
+                         ring + (kr % PF_RING) * PF_PAIR_BYTES);
+                PfVals vf;
+                u32x2 ids_next;
+                read_stage(ring + (k % PF_RING) * PF_PAIR_BYTES, ring + ((k + 1) % PF_RING) * PF_PAIR_BYTES, ids,
+                           min(k + 1, npairs - 1), min(kr + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
                 __builtin_amdgcn_sched_barrier(0);
-                if (c.active) compute_pair(a, pa, pb, ida, idb, first + cb + 2 * k, c, qop, j, st);
+                if (c.active) {
+                    pair_scores(kf, qop, s_next); /* pair k + 1 (past the end: the clamped refill, unused) */
+                    pair_softmax_values(a, s_cur, vf, __builtin_amdgcn_readfirstlane((int)ids_cur[0]),
+                                        __builtin_amdgcn_readfirstlane((int)ids_cur[1]), first + cb + 2 * k, c, j, st);
+                }
+                ids_cur = ids_next;
                 __builtin_amdgcn_sched_barrier(0);
+            };
+            for (int k = 0; k < npairs; k += 2) {
+                step(k, s0, s1);
+                if (k + 1 < npairs) step(k + 1, s1, s0);
             }
             pf_wait_vmcnt<0>(); /* the clamped refills past the last pair */
         }
