@@ -371,37 +371,52 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 
 /* One wave per segment (b, h) = blockIdx.x: combine the pieces of a segment that more than one wave touched
  * (pieces are waves floor(seg_lo / chunk) .. floor((seg_hi - 1) / chunk), slots wave + segment), weights
- * exp2(m_k - max m) as decode.cu:547-548's rescale. Lane (j, n) produces dims 32j..32j+31 of head n. */
+ * exp2(m_k - max m) as decode.cu:547-548's rescale, combined online. Lane (j, n) produces dims 32j..32j+31 of head
+ * n. The kernel is latency-bound: one pass over the context lengths gives the schedule, then the pieces' partial
+ * results are loaded 4 at a time, every load of a batch in flight together. */
 __global__ void __launch_bounds__(DEC_THREADS) k_merge(DecodeArgs a, int W) {
     const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
-    const int pages = seq_pages(a, b);
-    if (pages <= 0) return;
-    const long long total = schedule_total(a, 0, W, lane, false);
-    const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
-    long long before = 0; /* pages of sequences < b */
-    for (int base = 0; base < b; base += 64) {
+    long long total = 0, before = 0; /* pages of every sequence, of the sequences before b */
+    int pages = 0;
+    for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < b ? seq_pages(a, bb) : 0;
-        before += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
+        const int pg = bb < a.B ? seq_pages(a, bb) : 0;
+        total += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
+        before += __shfl(wave_inclusive_sum(bb < b ? pg : 0, lane), 63, 64);
+        if (b >= base && b < base + 64) pages = __shfl(pg, b - base, 64);
     }
+    if (pages <= 0) return;
+    total *= a.hkv;
+    const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
     const long long seg_lo = before * a.hkv + (long long)h * pages, seg_hi = seg_lo + pages;
     const int w_first = (int)(seg_lo / chunk), w_last = (int)((seg_hi - 1) / chunk);
     if (w_first == w_last || n >= a.group) return; /* one piece: k_decode wrote the output */
-    float mmax = DEC_M_INIT;
-    for (int k = w_first; k <= w_last; k++) mmax = fmaxf(mmax, a.ws_ml[2 * ((size_t)(k + s) * a.group + n)]);
-    float sum = 0.f, acc[32];
+    float mmax = DEC_M_INIT, sum = 0.f, acc[32];
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] = 0.f;
-    for (int k = w_first; k <= w_last; k++) {
-        const size_t slot = (size_t)(k + s) * a.group + n;
-        const float wk = __builtin_amdgcn_exp2f(a.ws_ml[2 * slot] - mmax);
-        sum += wk * a.ws_ml[2 * slot + 1];
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 32 * j);
+    for (int k0 = w_first; k0 <= w_last; k0 += 4) {
+        f32x2 ml[4];
+        f32x4 ov[4][8];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const f32x4 v = src[c];
+        for (int p = 0; p < 4; p++) {
+            const int k = min(k0 + p, w_last); /* a short batch re-reads the last piece: weight 0 below */
+            const size_t slot = (size_t)(k + s) * a.group + n;
+            ml[p] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 32 * j);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[4 * c + e] += wk * v[e];
+            for (int c = 0; c < 8; c++) ov[p][c] = src[c];
+        }
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            if (k0 + p > w_last) break;
+            const float m_new = fmaxf(mmax, ml[p][0]);
+            const float a_old = __builtin_amdgcn_exp2f(mmax - m_new), a_new = __builtin_amdgcn_exp2f(ml[p][0] - m_new);
+            sum = sum * a_old + ml[p][1] * a_new;
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[4 * c + e] = acc[4 * c + e] * a_old + ov[p][c][e] * a_new;
+            mmax = m_new;
         }
     }
     const float inv = sum > 0.f ? 1.0f / sum : 0.f;

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from helpers import assert_attention_close, assert_same_cache, bits, oracle_cache, table
-from nanochat_amd.attention import decode_attention
+from nanochat_amd.attention import decode_attention, decode_workspace
 from nanochat_amd.kv_cache import Fp8KVCache
 from nanochat_amd.workloads import CONFIG1, CONFIG2, CONFIG3, DecodeConfig, build_decode_case, decode_step
 from oracle import golden as G
@@ -109,3 +109,36 @@ def test_split_plan_does_not_change_the_result(gpu):
     a = decode_attention(q, case.cache, ctx, max_ctx=5000)
     b = decode_attention(q, case.cache, ctx, max_ctx=case.cache.capacity)
     torch.testing.assert_close(a.float(), b.float(), atol=4e-3, rtol=2e-2)
+
+
+def test_shared_workspace_across_calls_and_graph_replays(gpu):
+    """One workspace serves eager calls and several replays of a captured graph with no memset in between: every
+    result matches the oracle and the replays match the eager calls."""
+    dev = gpu
+    cfg = DecodeConfig("ws-reuse", 16, 16, 4, ctx_range=(300, 6000), paged=True, outliers=0.01, seed=91)
+    case = build_decode_case(cfg, dev, steps=1)
+    q = torch.randn((cfg.batch, cfg.hq, 128), device=dev).to(torch.bfloat16)
+    ctx = torch.from_numpy((case.ctx + 1).astype(np.int32)).to(dev)
+    max_ctx = case.cache.capacity
+    ws = decode_workspace(cfg.batch, cfg.hq, cfg.hkv, max_ctx, dev)
+    want = G.decode_attention(bits(q), oracle_cache(case.cache), table(case.cache), case.cache.max_blocks,
+                              case.ctx + 1, -1, cfg.hq, cfg.hkv, SCALE)
+    eager = []
+    for _ in range(3):
+        eager.append(decode_attention(q, case.cache, ctx, max_ctx=max_ctx, workspace=ws))
+        torch.cuda.synchronize()
+        assert_attention_close(eager[-1], want, "eager")
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        decode_attention(q, case.cache, ctx, max_ctx=max_ctx, out=out, workspace=ws)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            decode_attention(q, case.cache, ctx, max_ctx=max_ctx, out=out, workspace=ws)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.float(), eager[0].float(), atol=1e-3, rtol=1e-2)
+        assert_attention_close(out, want, "replay")
