@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the config 2 decode and config 4 prefill lines")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the measurement, copy a 1 GiB buffer 3 times (the byte-counter calibration kernel)")
     return ap.parse_args()
@@ -133,6 +134,32 @@ def extra_prefill_cfg4(dev, stream) -> dict:
     return {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "append_us": round(append_ms * 1e3, 3),
             "flops": flops, "TFLOP_s": round(tfs, 1), "bound": "mfma", "peak_TFLOP_s": MFMA_PEAK_TFS,
             "frac_of_mfma_peak": round(tfs / MFMA_PEAK_TFS, 4)}
+
+
+def extra_e2e_cfg5(dev) -> dict:
+    """Config 5: random-init 26-layer d1664 model, 128 random 2048-token prompts prefilled into the fp8 cache, then
+    512 greedy decode steps replayed from one captured graph; tokens/s and the decode steps' algorithmic HBM bytes
+    (bf16 weights once + 264 B per cached (token, head, layer))."""
+    import torch
+
+    from nanochat_amd.decoder import CONFIG5, generate
+
+    cfg = CONFIG5
+    toks, info, keep = generate(cfg, dev)
+    del keep
+    torch.cuda.empty_cache()
+    m, B, steps = cfg.model, cfg.batch, cfg.steps
+    kv = sum((cfg.prompt - 1 + i + 1) * B * m.kv_heads * 264 * m.layers for i in range(steps))
+    step_bytes = (kv + steps * info["weight_bytes"]) / steps
+    dec_s, pre_s = info["decode_ms"] * 1e-3, info["prefill_ms"] * 1e-3
+    gbs = step_bytes / (dec_s / steps) / 1e9
+    return {"workload": cfg.name, "prefill_s": round(pre_s, 4), "decode_s": round(dec_s, 4),
+            "decode_ms_per_step": round(info["decode_ms_per_step"], 4),
+            "decode_tokens_per_s": round(B * steps / dec_s, 1),
+            "e2e_tokens_per_s": round(B * steps / (pre_s + dec_s), 1),
+            "decode_step_bytes": int(step_bytes), "decode_GB_s": round(gbs, 1),
+            "decode_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "check": {"first_tokens": toks[0, :4].tolist(), "distinct_tokens": int(toks.unique().numel())}}
 
 
 def torch_empty_like(t):
@@ -263,6 +290,7 @@ def main():
     if not args.no_extra:
         result["decode_cfg2"] = extra_decode_cfg2(dev, stream)
         result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream)
+        result["e2e_cfg5"] = extra_e2e_cfg5(dev)
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:

@@ -98,6 +98,12 @@ int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, i
                         const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs, int window, int hq,
                         int hkv, float sm_scale, void *out, void *stream);
 
+/* Greedy token choice: out[r] = the column of the largest fp32 logit of row r (logits [rows][ld], cols used), the
+ * lowest column among exact ties.
+ * Replaces: the EPI_ARGMAX epilogue of the slot GEMM with its packed (score, ~row) key, model/kernels/decode.cu:90-96,
+ * 189-230 (greedy slots). */
+int nc_argmax_f32(const float *logits, int rows, int cols, long long ld, int32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

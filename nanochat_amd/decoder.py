@@ -1,0 +1,245 @@
+"""End-to-end greedy decoding of a random-init nanochat-style transformer over the fp8 KV cache.
+
+The decoder the reference drives through `dec_create` / `dec_prefill` / `dec_launch_body` / `dec_tokens`
+(model/kernels/decode.cu:950-1124; host protocol inference/decoder.py:129-222): the prompt minus its last token is
+prefilled, then every step feeds one token per sequence and appends the chosen one. Per layer
+(decode.cu:848-877, model/modeling.py:104-115):
+
+    h  = x + o_proj(attention(qk_norm_rope(qkv_proj(norm(x)))))     append + attention: this package's kernels
+    x' = h + down_proj(relu(up_proj(norm(h)))^2)
+
+with x0 = norm(embed(token)), a final norm, the untied lm_head and the greedy choice (largest fp32 logit, lowest id
+on ties, nc_argmax_f32). The weight GEMMs are plain library GEMMs (hipBLASLt through torch, bf16 in, fp32
+accumulate); the cache append, prefill and decode attention and the token choice are the HIP kernels. The decode
+step is captured once in a hipGraph and replayed.
+
+The architecture is BASELINE config 5's: RoPE, QK-norm, ReLU^2 MLP at 4x, untied embeddings, bf16 weights
+N(0, 0.02), full causal attention in every layer. The reference's training-time extras that this config does not
+name (value embeddings, per-layer residual / x0 mixing, which are identity and zero at the reference's init) are
+not part of it.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from nanochat_amd.attention import decode_attention, decode_workspace, prefill_attention
+from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
+from nanochat_amd.native import check, hip_library, pointer, stream
+from nanochat_amd.rotary import rotary_tables
+
+EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear.py:20)
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    layers: int
+    d_model: int
+    heads: int
+    vocab: int
+    mlp_mult: int = 4
+    theta: float = 10000.0
+
+    @property
+    def kv_heads(self) -> int:
+        return self.heads
+
+
+@dataclass(frozen=True)
+class E2EConfig:
+    """the model, the batch, the random prompts' length and the decode steps."""
+    name: str
+    model: ModelConfig
+    batch: int
+    prompt: int
+    steps: int
+    seed: int = 5
+
+
+CONFIG5 = E2EConfig("cfg5-e2e-l26-d1664-h13-v65536-b128-prompt2048-steps512",
+                    ModelConfig(layers=26, d_model=1664, heads=13, vocab=65536), batch=128, prompt=2048, steps=512)
+
+
+def argmax_rows(logits: Tensor, out: Tensor | None = None) -> Tensor:
+    """Greedy choice per row of fp32 logits [rows][cols]: the largest value's column, the lowest on ties."""
+    _require(logits, "logits", torch.float32, 2)
+    if logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    rows, cols = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    check(hip_library().nc_argmax_f32(pointer(logits), rows, cols, logits.stride(0), pointer(out), stream()))
+    return out
+
+
+class RandomModel:
+    """bf16 weights N(0, std) from a seeded generator (random init: no checkpoint is loaded); QK-norm gains 1.
+    wqkv rows are q heads, then k heads, then v heads (the fused projection's column blocks, decode.cu:476)."""
+
+    def __init__(self, cfg: ModelConfig, device, seed: int = 5, std: float = 0.02):
+        self.cfg = cfg
+        g = torch.Generator(device=device).manual_seed(seed)
+        d, C = cfg.d_model, cfg.heads * HEAD_DIM
+        ckv = cfg.kv_heads * HEAD_DIM
+
+        def w(*shape):
+            return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
+
+        self.wte = w(cfg.vocab, d)
+        self.layers = []
+        for _ in range(cfg.layers):
+            self.layers.append(dict(wqkv=w(C + 2 * ckv, d), wo=w(d, C), wup=w(cfg.mlp_mult * d, d),
+                                    wdown=w(d, cfg.mlp_mult * d),
+                                    q_gain=torch.ones(HEAD_DIM, device=device),
+                                    k_gain=torch.ones(HEAD_DIM, device=device)))
+        self.lm_head = w(cfg.vocab, d)
+
+    def weight_bytes(self) -> int:
+        n = self.wte.numel() + self.lm_head.numel()
+        for lw in self.layers:
+            n += sum(lw[k].numel() for k in ("wqkv", "wo", "wup", "wdown"))
+        return 2 * n
+
+
+def rms_norm(x: Tensor) -> Tensor:
+    """RMS norm with fp32 statistics, bf16 out (model/modeling.py:47-49)."""
+    return F.rms_norm(x.float(), (x.shape[-1],), eps=EPS).to(torch.bfloat16)
+
+
+class Fp8Decoder:
+    """Batch `batch` sequences of at most max_len tokens, one contiguous fp8 cache per layer."""
+
+    def __init__(self, model: RandomModel, batch: int, max_len: int, device, row_chunk: int = 16384):
+        cfg = model.cfg
+        self.model, self.cfg, self.batch, self.max_len, self.device = model, cfg, batch, max_len, device
+        self.caches = [Fp8KVCache.contiguous(batch, max_len, cfg.kv_heads, device) for _ in range(cfg.layers)]
+        self.cos, self.sin = rotary_tables(max_len, cfg.theta, device)
+        self.ws = decode_workspace(batch, cfg.heads, cfg.kv_heads, max_len, device)
+        self.seq = torch.arange(batch, dtype=torch.int32, device=device)
+        self.row_chunk = row_chunk
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    # ---------------------------------------------------------------------------------------------- layers
+    def _mlp(self, lw, x: Tensor) -> Tensor:
+        u = torch.matmul(rms_norm(x), lw["wup"].t()).float().relu_().square_().to(torch.bfloat16)
+        return x + torch.matmul(u, lw["wdown"].t())
+
+    def _qkv_append(self, l: int, x: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
+        lw = self.model.layers[l]
+        qkv = torch.matmul(rms_norm(x), lw["wqkv"].t())
+        return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
+
+    def _attn_out(self, l: int, x: Tensor, o: Tensor) -> Tensor:
+        return x + torch.matmul(o.reshape(o.shape[0], -1), self.model.layers[l]["wo"].t())
+
+    # ---------------------------------------------------------------------------------------------- prefill
+    @torch.no_grad()
+    def prefill(self, prompts: Tensor) -> None:
+        """Positions 0..T-2 of every prompt (int32 [batch][T]) into the caches (the last prompt token is the first
+        decode step's input, inference/decoder.py:211-222). Per layer every row is appended before any attends
+        (decode.cu:859-863); GEMMs and the MLP run in chunks of row_chunk rows."""
+        B, T = prompts.shape
+        if B != self.batch or T - 1 + 1 > self.max_len:
+            raise ValueError(f"prompts {tuple(prompts.shape)} do not fit batch {self.batch}, max_len {self.max_len}")
+        n = B * (T - 1)
+        if n == 0:
+            return
+        tok = prompts[:, :-1].reshape(-1)
+        pos = torch.arange(T - 1, dtype=torch.int32, device=self.device).repeat(B)
+        seq = torch.arange(B, dtype=torch.int32, device=self.device).repeat_interleave(T - 1)
+        x = rms_norm(self.model.wte[tok])
+        q = torch.empty((n, self.cfg.heads, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+        o = torch.empty_like(q)
+        chunks = [(r, min(r + self.row_chunk, n)) for r in range(0, n, self.row_chunk)]
+        for l in range(self.cfg.layers):
+            for r0, r1 in chunks:
+                q[r0:r1] = self._qkv_append(l, x[r0:r1], pos[r0:r1], seq[r0:r1])
+            prefill_attention(q, self.caches[l], pos, seq, out=o)
+            for r0, r1 in chunks:
+                xc = self._attn_out(l, x[r0:r1], o[r0:r1])
+                x[r0:r1] = self._mlp(self.model.layers[l], xc)
+
+    # ---------------------------------------------------------------------------------------------- decode
+    def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor) -> Tensor:
+        """One decode step: token tok[b] at position pos[b] of every sequence; the greedy choice into out_tok.
+        Returns the fp32 logits."""
+        x = rms_norm(self.model.wte[tok])
+        ctx = pos + 1
+        for l in range(self.cfg.layers):
+            q = self._qkv_append(l, x, pos, self.seq)
+            o = decode_attention(q, self.caches[l], ctx, max_ctx=self.max_len, workspace=self.ws)
+            x = self._mlp(self.model.layers[l], self._attn_out(l, x, o))
+        logits = torch.mm(rms_norm(x), self.model.lm_head.t(), out_dtype=torch.float32)
+        argmax_rows(logits, out_tok)
+        return logits
+
+    @torch.no_grad()
+    def start(self, last_tokens: Tensor, position: int) -> None:
+        """Decode state: every sequence's next input token (int32 [batch]) at `position`; captures the step graph
+        (positions and the token history advance on the device)."""
+        B = self.batch
+        self.tok = last_tokens.to(torch.int32).clone()
+        self.pos = torch.full((B,), position, dtype=torch.int32, device=self.device)
+        self.next = torch.empty(B, dtype=torch.int32, device=self.device)
+        self.history = torch.empty((self.max_len, B), dtype=torch.int32, device=self.device)
+        self.step_idx = torch.zeros(1, dtype=torch.int64, device=self.device)
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            # warm every launch path, then restore the state the warm-up advanced
+            self._step(self.tok, self.pos, self.next)
+            s.synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=s):
+                self._step(self.tok, self.pos, self.next)
+                self.history.index_copy_(0, self.step_idx, self.next.unsqueeze(0))
+                self.tok.copy_(self.next)
+                self.pos.add_(1)
+                self.step_idx.add_(1)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        self.stream = s
+
+    def run(self, steps: int) -> None:
+        """Replay the decode step `steps` times (asynchronous on the decoder's stream)."""
+        if self.graph is None:
+            raise RuntimeError("start() first")
+        with torch.cuda.stream(self.stream):
+            for _ in range(steps):
+                self.graph.replay()
+
+    def tokens(self, steps: int) -> Tensor:
+        """The first `steps` chosen tokens, int32 [batch][steps] (synchronises)."""
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        return self.history[:steps].t().contiguous()
+
+
+def generate(cfg: E2EConfig, device, steps: int | None = None, timing: bool = False):
+    """Random prompts (seeded), prefill, greedy decode. Returns (tokens [batch][steps], timings dict)."""
+    steps = cfg.steps if steps is None else steps
+    model = RandomModel(cfg.model, device, seed=cfg.seed)
+    g = torch.Generator(device=device).manual_seed(cfg.seed + 1)
+    prompts = torch.randint(0, cfg.model.vocab, (cfg.batch, cfg.prompt), generator=g, device=device,
+                            dtype=torch.int64).to(torch.int32)
+    dec = Fp8Decoder(model, cfg.batch, cfg.prompt - 1 + steps, device)
+    torch.cuda.synchronize(device)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    e[0].record()
+    dec.prefill(prompts)
+    e[1].record()
+    torch.cuda.synchronize(device)
+    dec.start(prompts[:, -1], cfg.prompt - 1)
+    torch.cuda.synchronize(device)
+    with torch.cuda.stream(dec.stream):
+        e[2].record(dec.stream)
+        dec.run(steps)
+        e[3].record(dec.stream)
+    e[3].synchronize()
+    toks = dec.tokens(steps)
+    prefill_ms, decode_ms = e[0].elapsed_time(e[1]), e[2].elapsed_time(e[3])
+    info = {"prefill_ms": prefill_ms, "decode_ms": decode_ms, "decode_ms_per_step": decode_ms / max(steps, 1),
+            "weight_bytes": model.weight_bytes()}
+    return toks, info, (model, dec, prompts)

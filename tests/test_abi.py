@@ -105,3 +105,11 @@ def test_prefill_rejects_bad_arguments():
     empty = list(base)
     empty[3] = 0
     assert lib.nc_prefill_attn_fp8(*empty) == 0  # nothing to do, nothing launched
+
+
+def test_argmax_rejects_bad_arguments():
+    lib = native.hip_library()
+    assert lib.nc_argmax_f32(FAKE, 4, 0, 10, FAKE, NULL) < 0 and "cols" in lib.nc_last_error().decode()
+    assert lib.nc_argmax_f32(FAKE, 4, 10, 5, FAKE, NULL) < 0
+    assert lib.nc_argmax_f32(NULL, 4, 10, 10, FAKE, NULL) < 0 and "null" in lib.nc_last_error().decode()
+    assert lib.nc_argmax_f32(FAKE, 0, 10, 10, FAKE, NULL) == 0  # nothing to do, nothing launched

@@ -1,0 +1,126 @@
+"""GPU end-to-end decoder (prefill + greedy decode over the fp8 cache) against a CPU restatement of the same model:
+torch bf16 GEMMs on the CPU and the oracle's append and fp64 attention over bit-identical cache bytes. Logits
+within tolerance at every step (the two sides feed the same tokens), the greedy choice equal wherever the CPU
+logits' top-two margin exceeds the tolerance, and the captured graph's replays equal to eager steps."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import bits
+from nanochat_amd.decoder import EPS, Fp8Decoder, ModelConfig, RandomModel, argmax_rows
+from oracle import golden as G
+
+pytestmark = pytest.mark.gpu
+
+TINY = ModelConfig(layers=2, d_model=256, heads=2, vocab=1000)
+LOGIT_ATOL = 2e-2
+
+
+def cpu_norm(x):
+    return F.rms_norm(x.float(), (x.shape[-1],), eps=EPS).to(torch.bfloat16)
+
+
+class CpuModel:
+    """The decoder's math on the CPU: bf16 tensors and torch bf16 GEMMs; the oracle's append, rows_attention and
+    decode_attention on a host copy of the cache layout."""
+
+    def __init__(self, model: RandomModel, batch: int, max_len: int):
+        cfg = model.cfg
+        self.cfg, self.batch = cfg, batch
+        self.w = [{k: v.cpu() for k, v in lw.items()} for lw in model.layers]
+        self.wte, self.lm_head = model.wte.cpu(), model.lm_head.cpu()
+        self.max_blocks = -(-max_len // G.PAGE)
+        self.caches = [G.PagedCache(batch * self.max_blocks, cfg.kv_heads) for _ in range(cfg.layers)]
+        self.cos, self.sin = G.rotary_tables(max_len, cfg.theta)
+
+    def _layer(self, l, x, pos, seq, attend):
+        lw, cfg = self.w[l], self.cfg
+        qkv = cpu_norm(x) @ lw["wqkv"].t()
+        q = G.append(self.caches[l], bits(qkv), pos, seq, lw["q_gain"].numpy(), lw["k_gain"].numpy(), self.cos,
+                     self.sin, cfg.heads, cfg.kv_heads, None, self.max_blocks)
+        o = torch.from_numpy(attend(q, self.caches[l]).astype(np.float32)).to(torch.bfloat16)
+        x = x + o.reshape(o.shape[0], -1) @ lw["wo"].t()
+        u = (cpu_norm(x) @ lw["wup"].t()).float().relu().square().to(torch.bfloat16)
+        return x + u @ lw["wdown"].t()
+
+    def prefill(self, prompts):
+        B, T = prompts.shape
+        pos = np.tile(np.arange(T - 1), B)
+        seq = np.repeat(np.arange(B), T - 1)
+        x = cpu_norm(self.wte[torch.from_numpy(prompts[:, :-1].reshape(-1).astype(np.int64))])
+        scale = 128 ** -0.5
+        for l in range(self.cfg.layers):
+            x = self._layer(l, x, pos, seq, lambda q, c: G.rows_attention(
+                q, pos, seq, c, None, self.max_blocks, B, -1, self.cfg.heads, self.cfg.kv_heads, scale))
+
+    def step(self, tok, position):
+        B = self.batch
+        pos, seq = np.full(B, position), np.arange(B)
+        x = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
+        scale = 128 ** -0.5
+        for l in range(self.cfg.layers):
+            x = self._layer(l, x, pos, seq, lambda q, c: G.decode_attention(
+                q, c, None, self.max_blocks, pos + 1, -1, self.cfg.heads, self.cfg.kv_heads, scale))
+        return (cpu_norm(x).float() @ self.lm_head.float().t()).numpy()
+
+
+def test_argmax_lowest_index_on_ties(gpu):
+    x = torch.randn((5, 3001), device=gpu)
+    x[0, 17] = x[0, 2000] = x[0].max() + 1  # a tie: the lower index wins
+    x[1] = -1.0  # all equal: index 0
+    x[2, -1] = 100.0  # the last, unaligned column
+    got = argmax_rows(x).cpu().numpy()
+    want = x.cpu().numpy().argmax(1)  # numpy: first occurrence
+    np.testing.assert_array_equal(got, want)
+    assert got[0] == 17 and got[1] == 0 and got[2] == 3000
+
+
+def test_decoder_matches_cpu_model_step_by_step(gpu):
+    dev = gpu
+    B, T, steps = 3, 40, 6
+    model = RandomModel(TINY, dev, seed=7)
+    prompts = np.random.default_rng(8).integers(0, TINY.vocab, (B, T)).astype(np.int32)
+    dec = Fp8Decoder(model, B, T - 1 + steps, dev, row_chunk=32)  # several row chunks in the prefill
+    cpu = CpuModel(model, B, T - 1 + steps)
+    dec.prefill(torch.from_numpy(prompts).to(dev))
+    cpu.prefill(prompts)
+    tok = prompts[:, -1].copy()
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    for s in range(steps):
+        p = T - 1 + s
+        logits = dec._step(torch.from_numpy(tok).to(dev), torch.full((B,), p, dtype=torch.int32, device=dev), out)
+        want = cpu.step(tok, p)
+        got = logits.cpu().numpy()
+        err = np.abs(got - want).max()
+        assert err <= LOGIT_ATOL, (s, err)
+        chosen = out.cpu().numpy()
+        top2 = np.sort(want, axis=1)[:, -2:]
+        sure = top2[:, 1] - top2[:, 0] > 2 * LOGIT_ATOL
+        np.testing.assert_array_equal(chosen[sure], want.argmax(1)[sure])
+        tok = chosen  # both sides continue from the GPU's choice
+
+
+def test_graph_replays_equal_eager_steps(gpu):
+    dev = gpu
+    B, T, steps = 4, 33, 5
+    model = RandomModel(TINY, dev, seed=9)
+    prompts = torch.from_numpy(np.random.default_rng(10).integers(0, TINY.vocab, (B, T)).astype(np.int32)).to(dev)
+    eager = Fp8Decoder(model, B, T - 1 + steps, dev)
+    eager.prefill(prompts)
+    tok, outs = prompts[:, -1].clone(), []
+    for s in range(steps):
+        nxt = torch.empty(B, dtype=torch.int32, device=dev)
+        eager._step(tok, torch.full((B,), T - 1 + s, dtype=torch.int32, device=dev), nxt)
+        outs.append(nxt.clone())
+        tok = nxt
+    want = torch.stack(outs, 1).cpu()
+    graphed = Fp8Decoder(model, B, T - 1 + steps, dev)
+    graphed.prefill(prompts)
+    graphed.start(prompts[:, -1], T - 1)
+    for _ in range(steps):  # one replay at a time, with eager work and a synchronisation in between
+        graphed.run(1)
+        torch.cuda.synchronize()
+        torch.zeros(1 << 20, device=dev).sum()
+    torch.testing.assert_close(graphed.tokens(steps).cpu(), want)
