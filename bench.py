@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
+    ap.add_argument("--only", choices=["decode2", "prefill4", "e2e5"],
+                    help="run one secondary workload alone and print its object (for profiling runs)")
+    ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the measurement, copy a 1 GiB buffer 3 times (the byte-counter calibration kernel)")
     return ap.parse_args()
@@ -136,7 +139,7 @@ def extra_prefill_cfg4(dev, stream) -> dict:
             "frac_of_mfma_peak": round(tfs / MFMA_PEAK_TFS, 4)}
 
 
-def extra_e2e_cfg5(dev) -> dict:
+def extra_e2e_cfg5(dev, steps: int | None = None) -> dict:
     """Config 5: random-init 26-layer d1664 model, 128 random 2048-token prompts prefilled into the fp8 cache, then
     512 greedy decode steps replayed from one captured graph; tokens/s and the decode steps' algorithmic HBM bytes
     (bf16 weights once + 264 B per cached (token, head, layer))."""
@@ -145,6 +148,10 @@ def extra_e2e_cfg5(dev) -> dict:
     from nanochat_amd.decoder import CONFIG5, generate
 
     cfg = CONFIG5
+    if steps is not None:
+        from dataclasses import replace
+
+        cfg = replace(cfg, steps=steps, name=cfg.name.replace(f"steps{cfg.steps}", f"steps{steps}"))
     toks, info, keep = generate(cfg, dev)
     del keep
     torch.cuda.empty_cache()
@@ -213,6 +220,12 @@ def main():
     from nanochat_amd.workloads import CONFIG3, build_decode_case, decode_bytes
 
     dev = torch.device("cuda:0")
+    if args.only:
+        s = torch.cuda.Stream(dev)
+        run = {"decode2": lambda: extra_decode_cfg2(dev, s), "prefill4": lambda: extra_prefill_cfg4(dev, s),
+               "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps)}[args.only]
+        print(json.dumps(run()), flush=True)
+        return
     cfg = CONFIG3
     steps, warmup = args.steps, args.warmup
     case = build_decode_case(cfg, dev, steps=steps + warmup + 2)
@@ -290,7 +303,7 @@ def main():
     if not args.no_extra:
         result["decode_cfg2"] = extra_decode_cfg2(dev, stream)
         result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream)
-        result["e2e_cfg5"] = extra_e2e_cfg5(dev)
+        result["e2e_cfg5"] = extra_e2e_cfg5(dev, args.e2e_steps)
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:

@@ -104,6 +104,17 @@ int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, i
  * 189-230 (greedy slots). */
 int nc_argmax_f32(const float *logits, int rows, int cols, long long ld, int32_t *out, void *stream);
 
+/* Residual add fused with the RMS norm over rows of d bf16 (contiguous, d % 8 == 0, d <= 8192): x_out = bf16(x +
+ * delta) (delta NULL: x_out = x; x_out NULL: not stored; x_out may be x), y = bf16(x_out * r), r = 1 / sqrt(Σ
+ * x_out² / d + FLT_EPSILON), Σ in fp32.
+ * Replaces: the RESID epilogue of the slot GEMM and k_rstd, model/kernels/decode.cu:107-123,179-184,447-456; norm,
+ * model/modeling.py:47-49. */
+int nc_add_rms_norm_bf16(const void *x, const void *delta, void *x_out, void *y, int rows, int d, void *stream);
+
+/* out = bf16(relu(in)^2) over n bf16 (n % 8 == 0); out may be in.
+ * Replaces: the RELU2 epilogue of the slot GEMM, model/kernels/decode.cu:174-178. */
+int nc_relu2_bf16(const void *in, void *out, long long n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

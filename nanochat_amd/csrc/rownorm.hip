@@ -1,0 +1,102 @@
+/*
+ * Row kernels of the decoder's layer body: the residual add fused with the RMS norm, and the MLP's ReLU^2.
+ * Reference: the slot GEMM's RESID epilogue (out = bf16(s + res)) with k_rstd (r = rsqrt(Σ x² / K + FLT_EPSILON)),
+ * and the RELU2 epilogue (bf16(relu(p) p)), model/kernels/decode.cu:107-123,169-184,447-456; the model's norm,
+ * model/modeling.py:47-49. Here the weight GEMMs are library GEMMs, so these run as their own bandwidth-bound
+ * passes: a (row) workgroup loads the row once into registers.
+ *
+ * add_rms_norm: x_out = bf16(x + delta) (delta NULL: x_out = x), y = bf16(x_out * r), r = 1 / sqrt(Σ x_out² / d +
+ * FLT_EPSILON) over the rounded x_out, Σ in fp32 (thread partials, then a fixed wave and workgroup tree).
+ */
+#include "common.h"
+
+#define RN_THREADS 256
+#define RN_MAX_CHUNKS 4 /* 8-element chunks per thread: d <= 8192 */
+
+/* x_out may alias x (in-place residual update): each thread reads and writes only its own chunks. */
+__global__ void __launch_bounds__(RN_THREADS) k_add_rms_norm(const bf16_t *x, const bf16_t *__restrict__ delta,
+                                                             bf16_t *x_out, bf16_t *__restrict__ y, int d) {
+    __shared__ float part[RN_THREADS / NC_WAVE];
+    const int row = blockIdx.x, tid = threadIdx.x, chunks = d / 8;
+    const size_t base = (size_t)row * d;
+    float v[RN_MAX_CHUNKS][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+        load_bf16x8(x + base + 8 * c, v[k]);
+        if (delta) {
+            float dv[8];
+            load_bf16x8(delta + base + 8 * c, dv);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[k][e] = bf16_to_f32(f32_to_bf16(v[k][e] + dv[e]));
+            if (x_out) store_bf16x8(x_out + base + 8 * c, v[k]);
+        } else if (x_out && x_out != x) {
+            store_bf16x8(x_out + base + 8 * c, v[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += v[k][e] * v[k][e];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+    if ((tid & (NC_WAVE - 1)) == 0) part[tid / NC_WAVE] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < RN_THREADS / NC_WAVE; w++) total += part[w];
+    const float r = 1.0f / sqrtf(total / (float)d + 1.1920928955078125e-07f);
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = v[k][e] * r;
+        store_bf16x8(y + base + 8 * c, o);
+    }
+}
+
+__global__ void __launch_bounds__(RN_THREADS) k_relu2(const bf16_t *in, bf16_t *out, /* may be in */
+                                                      long long n8) {
+    const long long stride = (long long)gridDim.x * RN_THREADS;
+    for (long long c = (long long)blockIdx.x * RN_THREADS + threadIdx.x; c < n8; c += stride) {
+        float v[8];
+        load_bf16x8(in + 8 * c, v);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = fmaxf(v[e], 0.f);
+            v[e] = p * p;
+        }
+        store_bf16x8(out + 8 * c, v);
+    }
+}
+
+extern "C" int nc_add_rms_norm_bf16(const void *x, const void *delta, void *x_out, void *y, int rows, int d,
+                                    void *stream) {
+    NC_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 8 * RN_THREADS * RN_MAX_CHUNKS,
+               "nc_add_rms_norm_bf16: rows %d, d %d (d a multiple of 8, at most %d)", rows, d,
+               8 * RN_THREADS * RN_MAX_CHUNKS);
+    if (rows == 0) return 0;
+    NC_REQUIRE(x && y, "nc_add_rms_norm_bf16: null pointer");
+    NC_REQUIRE(((uintptr_t)x | (uintptr_t)delta | (uintptr_t)x_out | (uintptr_t)y) % 16 == 0,
+               "nc_add_rms_norm_bf16: 16-byte alignment");
+    hipLaunchKernelGGL(k_add_rms_norm, dim3(rows), dim3(RN_THREADS), 0, (hipStream_t)stream, (const bf16_t *)x,
+                       (const bf16_t *)delta, (bf16_t *)x_out, (bf16_t *)y, d);
+    NC_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int nc_relu2_bf16(const void *in, void *out, long long n, void *stream) {
+    NC_REQUIRE(n >= 0 && n % 8 == 0, "nc_relu2_bf16: n = %lld must be a non-negative multiple of 8", n);
+    if (n == 0) return 0;
+    NC_REQUIRE(in && out, "nc_relu2_bf16: null pointer");
+    NC_REQUIRE(((uintptr_t)in | (uintptr_t)out) % 16 == 0, "nc_relu2_bf16: 16-byte alignment");
+    const long long n8 = n / 8;
+    long long blocks = (n8 + RN_THREADS - 1) / RN_THREADS;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_relu2, dim3((unsigned)blocks), dim3(RN_THREADS), 0, (hipStream_t)stream, (const bf16_t *)in,
+                       (bf16_t *)out, n8);
+    NC_LAUNCH_CHECK();
+    return 0;
+}

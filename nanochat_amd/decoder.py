@@ -106,8 +106,30 @@ class RandomModel:
 
 
 def rms_norm(x: Tensor) -> Tensor:
-    """RMS norm with fp32 statistics, bf16 out (model/modeling.py:47-49)."""
+    """RMS norm with fp32 statistics, bf16 out (model/modeling.py:47-49), in torch (the CPU-side restatement)."""
     return F.rms_norm(x.float(), (x.shape[-1],), eps=EPS).to(torch.bfloat16)
+
+
+def add_rms_norm(x: Tensor, delta: Tensor | None, x_out: Tensor | None = None) -> Tensor:
+    """nc_add_rms_norm_bf16 over rows of x (bf16 [n][d], contiguous): x_out = bf16(x + delta) (in place when x_out
+    is x), returns norm(x_out)."""
+    _require(x, "x", torch.bfloat16, 2)
+    n, d = x.shape
+    for t in (delta, x_out):
+        if t is not None and (t.shape != x.shape or t.dtype != torch.bfloat16 or not t.is_contiguous()):
+            raise ValueError("delta / x_out must be contiguous bf16 of x's shape")
+    y = torch.empty_like(x)
+    check(hip_library().nc_add_rms_norm_bf16(pointer(x), pointer(delta), pointer(x_out), pointer(y), n, d,
+                                             stream()))
+    return y
+
+
+def relu2(x: Tensor) -> Tensor:
+    """bf16(relu(x)^2) in place (nc_relu2_bf16)."""
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("relu2 needs a contiguous bf16 tensor")
+    check(hip_library().nc_relu2_bf16(pointer(x), pointer(x), x.numel(), stream()))
+    return x
 
 
 class Fp8Decoder:
@@ -124,17 +146,24 @@ class Fp8Decoder:
         self.graph: torch.cuda.CUDAGraph | None = None
 
     # ---------------------------------------------------------------------------------------------- layers
-    def _mlp(self, lw, x: Tensor) -> Tensor:
-        u = torch.matmul(rms_norm(x), lw["wup"].t()).float().relu_().square_().to(torch.bfloat16)
-        return x + torch.matmul(u, lw["wdown"].t())
-
-    def _qkv_append(self, l: int, x: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
+    def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
+        """h = norm(x); the projection, then QK-norm + RoPE + fp8 append of k, v; returns q."""
         lw = self.model.layers[l]
-        qkv = torch.matmul(rms_norm(x), lw["wqkv"].t())
+        qkv = torch.matmul(h, lw["wqkv"].t())
         return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
 
-    def _attn_out(self, l: int, x: Tensor, o: Tensor) -> Tensor:
-        return x + torch.matmul(o.reshape(o.shape[0], -1), self.model.layers[l]["wo"].t())
+    def _finish_layer(self, l: int, x: Tensor, o: Tensor) -> Tensor:
+        """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; returns norm(x), the next layer's
+        (or the final) normed input."""
+        lw = self.model.layers[l]
+        m = add_rms_norm(x, torch.matmul(o.reshape(o.shape[0], -1), lw["wo"].t()), x)
+        u = relu2(torch.matmul(m, lw["wup"].t()))
+        return add_rms_norm(x, torch.matmul(u, lw["wdown"].t()), x)
+
+    def _embed(self, tok: Tensor) -> tuple[Tensor, Tensor]:
+        """The residual stream x0 = norm(embed(tok)) and its norm, the first layer's input."""
+        x = add_rms_norm(self.model.wte[tok], None)
+        return x, add_rms_norm(x, None)
 
     # ---------------------------------------------------------------------------------------------- prefill
     @torch.no_grad()
@@ -151,29 +180,28 @@ class Fp8Decoder:
         tok = prompts[:, :-1].reshape(-1)
         pos = torch.arange(T - 1, dtype=torch.int32, device=self.device).repeat(B)
         seq = torch.arange(B, dtype=torch.int32, device=self.device).repeat_interleave(T - 1)
-        x = rms_norm(self.model.wte[tok])
+        x, h = self._embed(tok)
         q = torch.empty((n, self.cfg.heads, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
         o = torch.empty_like(q)
         chunks = [(r, min(r + self.row_chunk, n)) for r in range(0, n, self.row_chunk)]
         for l in range(self.cfg.layers):
             for r0, r1 in chunks:
-                q[r0:r1] = self._qkv_append(l, x[r0:r1], pos[r0:r1], seq[r0:r1])
+                q[r0:r1] = self._qkv_append(l, h[r0:r1], pos[r0:r1], seq[r0:r1])
             prefill_attention(q, self.caches[l], pos, seq, out=o)
             for r0, r1 in chunks:
-                xc = self._attn_out(l, x[r0:r1], o[r0:r1])
-                x[r0:r1] = self._mlp(self.model.layers[l], xc)
+                h[r0:r1] = self._finish_layer(l, x[r0:r1], o[r0:r1])
 
     # ---------------------------------------------------------------------------------------------- decode
     def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor) -> Tensor:
         """One decode step: token tok[b] at position pos[b] of every sequence; the greedy choice into out_tok.
         Returns the fp32 logits."""
-        x = rms_norm(self.model.wte[tok])
+        x, h = self._embed(tok)
         ctx = pos + 1
         for l in range(self.cfg.layers):
-            q = self._qkv_append(l, x, pos, self.seq)
+            q = self._qkv_append(l, h, pos, self.seq)
             o = decode_attention(q, self.caches[l], ctx, max_ctx=self.max_len, workspace=self.ws)
-            x = self._mlp(self.model.layers[l], self._attn_out(l, x, o))
-        logits = torch.mm(rms_norm(x), self.model.lm_head.t(), out_dtype=torch.float32)
+            h = self._finish_layer(l, x, o)
+        logits = torch.mm(h, self.model.lm_head.t(), out_dtype=torch.float32)
         argmax_rows(logits, out_tok)
         return logits
 
