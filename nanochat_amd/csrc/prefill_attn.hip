@@ -14,14 +14,18 @@
  * range of its rows in pairs; all four waves consume the same pair from LDS.
  *
  * Per page pair (32 keys) a wave computes, for each of its 4 blocks,
- *   scores  Sᵀ[16 keys][16 columns] per page = K · Qᵀ, 4 v_mfma_f32_16x16x32_bf16 (fp8 -> bf16 exact, A = K with
- *           key lane % 16 and dims 32 (lane / 16) .., B = q of column lane % 16 over the same dims);
+ *   scores  Sᵀ[16 keys][16 columns] per page = K · Qᵀ on fp8 MFMAs: v_mfma_scale_f32_16x16x128_f8f6f4 takes the
+ *           page's e4m3 K codes as they are (A: key lane % 16, dims 32 (lane / 16) .. + 31, all 128 dims in one
+ *           instruction) against q split into two e4m3 terms, q 2^e = hi + lo (hi = e4m3(q 2^e), lo = e4m3 of the
+ *           exact remainder: about 8 significant bits, bf16's precision), with e per column chosen so |q| 2^e <
+ *           256; the MFMA's E8M0 B-scale 2^-e undoes it. Two 32-cycle MFMAs per page and block, the same MFMA time
+ *           as four bf16 ones, and no K conversion;
  *   softmax fp32 base 2, lazy reference max per column (moves only when a score exceeds it by more than 8);
  *   values  Oᵀ[16 dims][16 columns] += Vᵀ[16 dims][32 keys] · Pᵀ, 8 v_mfma_f32_16x16x32_f16. The lane's k slots
  *           8j..8j+7 are keys 4j..4j+3 of the first page then of the second, which is where the score MFMAs left
  *           this lane's probabilities: Pᵀ is built in registers, no exchange. P carries v_scale and a running
  *           power of two (as in decode): fp16 with headroom, V codes fp8 -> fp16 exact.
- * 64 MFMAs per wave per pair for ~350 VALU instructions: MFMA-bound (the roofline is the bf16/fp16 dense peak).
+ * Roofline: MFMA (the dense bf16/fp16 peak; the fp8 score MFMAs run at twice that rate over twice the work).
  *
  * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
  * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
@@ -55,6 +59,8 @@
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 struct PrefillArgs {
@@ -216,20 +222,70 @@ struct PfCols {
     bool active;        /* the wave has a column of the segment */
 };
 
-/* Scores of a pair for every block: s[bl][0] page A, s[bl][1] page B, lane (j, n) keys 4j..4j+3 of column n. */
-__device__ __forceinline__ void pair_scores(const PfKeys &k, const bf16x8 (*qop)[4], f32x4 (*s)[2]) {
+/* q of one block as the fp8 score operand: q 2^e = hi + lo in e4m3, e per column; scale = the E8M0 byte of 2^-e. */
+struct PfQ8 {
+    i32x8 hi, lo;
+    int scale;
+};
+
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    const float v = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f; /* m 2^-9 */
+    return (c & 0x80u) ? -v : v;
+}
+
+/* 32 bf16 of q (this lane's dims 32j .. 32j+31 of its column) -> the two e4m3 terms; the column's exponent from
+ * its absmax over the four lanes holding it (xor 16, 32). A zero column gives zero terms. */
+__device__ PfQ8 quantize_q(const u32x4 (&u)[4]) {
+#pragma clang fp contract(off)
+    float x[32];
 #pragma unroll
-    for (int bl = 0; bl < PF_BLOCKS; bl++) s[bl][0] = s[bl][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; c++)
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) { /* one k step of every block per conversion: 8 converted registers live */
-        const u32x4 &fa = kk < 2 ? k.a0 : k.a1, &fb = kk < 2 ? k.b0 : k.b1;
-        const bf16x8 ka = pf_fp8x8_to_bf16(fa[2 * (kk & 1)], fa[2 * (kk & 1) + 1]);
-        const bf16x8 kb = pf_fp8x8_to_bf16(fb[2 * (kk & 1)], fb[2 * (kk & 1) + 1]);
-#pragma unroll
-        for (int bl = 0; bl < PF_BLOCKS; bl++) {
-            s[bl][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[bl][kk], s[bl][0], 0, 0, 0);
-            s[bl][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop[bl][kk], s[bl][1], 0, 0, 0);
+        for (int i = 0; i < 4; i++) {
+            x[8 * c + 2 * i] = __uint_as_float(u[c][i] << 16);
+            x[8 * c + 2 * i + 1] = __uint_as_float(u[c][i] & 0xffff0000u);
         }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
+    amax = fmaxf(amax, shfl_xor_f(amax, 16));
+    amax = fmaxf(amax, shfl_xor_f(amax, 32));
+    /* amax in [2^ea, 2^(ea+1)): with e = 7 - ea, |q| 2^e < 2^8 <= 448 */
+    const int ea = amax > 0.f ? (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127 : 0;
+    const int e = max(min(7 - ea, 127), -126);
+    const float up = __uint_as_float((uint32_t)(e + 127) << 23);
+    PfQ8 q;
+    q.scale = max(min(127 - e, 254), 0);
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        uint32_t hi = 0, lo = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float v = x[4 * w + b] * up; /* exact: a power of two */
+            const uint32_t ch = f32_to_e4m3(v);
+            hi |= ch << (8 * b);
+            lo |= f32_to_e4m3(v - e4m3_value(ch)) << (8 * b); /* the remainder is exact in fp32 */
+        }
+        q.hi[w] = (int)hi;
+        q.lo[w] = (int)lo;
+    }
+    return q;
+}
+
+/* Scores of a pair for every block: s[bl][0] page A, s[bl][1] page B, lane (j, n) keys 4j..4j+3 of column n. */
+__device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32x4 (*s)[2]) {
+    const i32x8 ka = __builtin_bit_cast(i32x8, u32x8{k.a0[0], k.a0[1], k.a0[2], k.a0[3], k.a1[0], k.a1[1], k.a1[2],
+                                                     k.a1[3]});
+    const i32x8 kb = __builtin_bit_cast(i32x8, u32x8{k.b0[0], k.b0[1], k.b0[2], k.b0[3], k.b1[0], k.b1[1], k.b1[2],
+                                                     k.b1[3]});
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        f32x4 sa = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, q8[bl].hi, z, 0, 0, 0, 127, 0, q8[bl].scale);
+        f32x4 sb = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kb, q8[bl].hi, z, 0, 0, 0, 127, 0, q8[bl].scale);
+        s[bl][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, q8[bl].lo, sa, 0, 0, 0, 127, 0, q8[bl].scale);
+        s[bl][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kb, q8[bl].lo, sb, 0, 0, 0, 127, 0, q8[bl].scale);
     }
 }
 
@@ -358,22 +414,24 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
     if (unit >= a.hkv * a.tiles) return;
     const int h = unit / a.tiles, tile = unit % a.tiles;
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, n = lane & 15, j = lane >> 4;
+    /* the wave index is wave-uniform: readfirstlane lets the compiler keep what derives from it in scalars */
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, n = lane & 15,
+              j = lane >> 4;
     const int G = a.group, R = a.rows_per_block, TR = PF_WAVES * PF_BLOCKS * R;
     const int row0 = tile * TR;
 
     /* this lane's q operands: column n of block bl is row row0 + (wv PF_BLOCKS + bl) R + n / G, head h G + n % G */
-    bf16x8 qop[PF_BLOCKS][4];
+    PfQ8 q8[PF_BLOCKS];
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
         const bool used = n < R * G && r < a.n;
         const bf16_t *qr = a.q + ((size_t)(used ? r : 0) * a.hq + h * G + n % G) * NC_HEAD_DIM + 32 * j;
+        u32x4 u[4];
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const u32x4 u = used ? *reinterpret_cast<const u32x4 *>(qr + 8 * kk) : u32x4{0u, 0u, 0u, 0u};
-            qop[bl][kk] = __builtin_bit_cast(bf16x8, u);
-        }
+        for (int kk = 0; kk < 4; kk++)
+            u[kk] = used ? *reinterpret_cast<const u32x4 *>(qr + 8 * kk) : u32x4{0u, 0u, 0u, 0u};
+        q8[bl] = quantize_q(u);
     }
 
     PfState st;
@@ -476,7 +534,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             u32x2 ids_cur, ids_dma;
             read_keys(ring, ids, 0, min(PF_RING - 1, npairs - 1), lane, kf, ids_cur, ids_dma);
             f32x4 s0[PF_BLOCKS][2], s1[PF_BLOCKS][2];
-            if (c.active) pair_scores(kf, qop, s0);
+            if (c.active) pair_scores(kf, q8, s0);
             __builtin_amdgcn_sched_barrier(0);
             /* iteration k: the scores of pair k + 1 into one buffer while pair k's softmax and values read the other
              * (unrolled twice so the buffers swap without copies) */
@@ -494,7 +552,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                            min(k + 1, npairs - 1), min(kr + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
                 __builtin_amdgcn_sched_barrier(0);
                 if (c.active) {
-                    pair_scores(kf, qop, s_next); /* pair k + 1 (past the end: the clamped refill, unused) */
+                    pair_scores(kf, q8, s_next); /* pair k + 1 (past the end: the clamped refill, unused) */
                     pair_softmax_values(a, s_cur, vf, __builtin_amdgcn_readfirstlane((int)ids_cur[0]),
                                         __builtin_amdgcn_readfirstlane((int)ids_cur[1]), first + cb + 2 * k, c, j, st);
                 }
