@@ -25,7 +25,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere (hipcc would otherwise form them from float2 code).
 # -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs, so the softmax rescales of the decode kernel's output
 # accumulators need no AGPR <-> VGPR copies.
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wshadow", "-Wno-unused-function",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form",
          f"-I{PACKAGE.parent / 'include'}"]
 
