@@ -115,6 +115,25 @@ int nc_add_rms_norm_bf16(const void *x, const void *delta, void *x_out, void *y,
  * Replaces: the RELU2 epilogue of the slot GEMM, model/kernels/decode.cu:174-178. */
 int nc_relu2_bf16(const void *in, void *out, long long n, void *stream);
 
+/* Epilogues of nc_slot_gemm_bf16 (s = Σ_k w[r][k] x[b][k] in fp32, rn = 1 / sqrt(Σ_k x[b][k]² / k + FLT_EPSILON)). */
+enum {
+    NC_GEMM_STORE = 0,      /* out bf16 = s */
+    NC_GEMM_NORM_STORE = 1, /* out bf16 = s rn: the GEMM of the RMS-normed rows */
+    NC_GEMM_RESID = 2,      /* out bf16 = bf16(s + res), one rounding; res may be out (in place) */
+    NC_GEMM_RELU2_NORM = 3, /* out bf16 = relu(p) p, p = s rn */
+    NC_GEMM_NORM_F32 = 4    /* out fp32 = s rn: logits */
+};
+
+/* The decode step's skinny weight GEMM: out[b][r] = epilogue(w[r] . x[b]) for b < m, r < n; w bf16 [n][k]
+ * (nn.Linear layout), x bf16 [m][k], out [m][n] (bf16, fp32 for NORM_F32), all contiguous and 16-byte aligned;
+ * n % 32 == 0, k % 64 == 0. Deterministic (fixed summation order). tile_n x tile_m picks the work tile (32 x 32,
+ * 64 x 32, 32 x 64, 64 x 64, 32 x 128, 64 x 128, 128 x 64 or 128 x 128; n a multiple of tile_n); 0 x 0 chooses one
+ * from the shape.
+ * Replaces: the slot GEMM k_wgmma with its STORE / RESID / RELU2 epilogues and the rstd it applies (k_rstd),
+ * model/kernels/decode.cu:107-123,169-184,292-338,447-456, launched per layer at :848-877. */
+int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out, const void *res,
+                      int tile_n, int tile_m, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,364 @@
+/*
+ * The decode step's weight GEMMs (the reference's slot GEMM, model/kernels/decode.cu:107-123,169-184,292-338):
+ * out[b][r] = epilogue(Σ_k W[r][k] x[b][k]) for the M rows x of a decode batch (M is the batch, 1..a few hundred)
+ * against a weight matrix W [N][K] in nn.Linear layout, bf16 operands, fp32 accumulation.
+ *
+ * At decode batch sizes the GEMM is a stream of W through the chip: W is read once from HBM and every byte meets all
+ * M rows of x, which stay L2-resident. The work unit is an output tile of NT weight rows x MT batch rows over the full
+ * K, so the epilogue sees complete sums and the result is deterministic (no split-K atomics):
+ *
+ *   - a workgroup of 4 waves splits K into 4 contiguous ranges of 64-column chunks; each wave multiplies its range with
+ *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles), loading its fragments straight from global
+ *     memory with buffer loads (16 bytes per lane, the 4 lanes of a row covering 64 contiguous bytes of it), 2 to 7 chunks
+ *     in flight in a register ring;
+ *   - the 4 partial tiles meet in LDS and are summed in a fixed order, then the epilogue stores 4 adjacent outputs
+ *     per lane;
+ *   - the RMS norm of the input rows is fused: the same x fragments feed one more MFMA per 16 rows, x·xᵀ, whose
+ *     diagonal is Σ x² of each row, so r = 1 / sqrt(Σ x² / K + FLT_EPSILON) (model/modeling.py:47-49, decode.cu:448-456)
+ *     scales the sums in the epilogue instead of a separate normalised copy of x (the reference's RELU2 epilogue,
+ *     p = s r, decode.cu:171-175);
+ *   - units are ordered so the MT-row slices of one weight tile run on one XCD (workgroup b on XCD b % 8 takes a
+ *     contiguous range), so W is fetched from HBM once and re-read from that XCD's L2.
+ *
+ * Epilogues (decode.cu:169-184): STORE bf16(s); NORM_STORE bf16(s r); RESID bf16(s + res) (one rounding, res may be
+ * out: an in-place residual update); RELU2_NORM bf16(relu(p) p) with p = s r; NORM_F32 fp32 s r (the lm_head's
+ * logits for nc_argmax_f32).
+ */
+#include "common.h"
+
+#define SG_THREADS 256
+#define SG_WAVES 4
+#define SG_CHUNK 64                 /* K columns per ring slot: 128 bytes of every row */
+#define SG_LDS_BUDGET (128 * 1024) /* ring bytes per workgroup */
+
+enum { SG_STORE = 0, SG_NORM_STORE = 1, SG_RESID = 2, SG_RELU2_NORM = 3, SG_NORM_F32 = 4 };
+
+typedef __attribute__((address_space(3))) unsigned char sg_lds_u8;
+
+struct SlotGemmArgs {
+    const bf16_t *w;   /* [n][k] */
+    const bf16_t *x;   /* [m][k] */
+    void *out;         /* [m][n] bf16 (fp32 for NORM_F32) */
+    const bf16_t *res; /* [m][n] RESID's addend, may equal out */
+    int n, k, m;
+    int n_tiles, m_slices, units_per_xcd;
+};
+
+/* The 4 waves as WN (over W rows) x 4/WN (over batch rows): the split that reads the fewest fragments per wave
+ * (per chunk a wave reads its NT/WN W rows and MT/(4/WN) x rows from LDS); ties to the larger WN. */
+__host__ __device__ constexpr int sg_reads(int nt, int mt, int wn) {
+    return (nt / 16) % wn || (mt / 16) % (4 / wn) ? 1 << 20 : nt / 16 / wn + mt / 16 / (4 / wn);
+}
+__host__ __device__ constexpr int sg_waves_n(int nt, int mt) {
+    return sg_reads(nt, mt, 4) <= sg_reads(nt, mt, 2) && sg_reads(nt, mt, 4) <= sg_reads(nt, mt, 1)
+               ? 4
+               : (sg_reads(nt, mt, 2) <= sg_reads(nt, mt, 1) ? 2 : 1);
+}
+
+/* Ring geometry of an NT x MT tile: a slot holds the chunk's NT W rows then MT x rows, 128 bytes each. */
+__host__ __device__ constexpr int sg_slot_bytes(int nt, int mt) { return (nt + mt) * 128; }
+__host__ __device__ constexpr int sg_depth(int nt, int mt) {
+    return SG_LDS_BUDGET / sg_slot_bytes(nt, mt) > 8 ? 8 : SG_LDS_BUDGET / sg_slot_bytes(nt, mt);
+}
+
+template <int N> __device__ __forceinline__ void sg_wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+__device__ __forceinline__ uint32_t sg_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const sg_lds_u8 *)(const unsigned char *)p;
+}
+
+/* 16 bytes of LDS; completion is waited for by sg_ds_wait (the compiler does not see the read in flight). */
+__device__ __forceinline__ bf16x8 sg_ds_read(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ void sg_ds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+/* Orders every use of v after the preceding sg_ds_wait. */
+__device__ __forceinline__ void sg_after_wait(bf16x8 &v) { asm volatile("" : "+v"(v)); }
+
+/* This wave's DMA instructions of a chunk: instruction wv + SG_WAVES d lands at dst + 1024 (wv + SG_WAVES d). (A
+ * function, not a lambda: clang drops the host stub of a kernel template whose lambda calls this builtin.) */
+template <int DPW>
+__device__ __forceinline__ void sg_dma(const unsigned char *const *src, size_t off, unsigned char *dst, int wv) {
+#pragma unroll
+    for (int d = 0; d < DPW; d++)
+        __builtin_amdgcn_global_load_lds(src[d] + off, dst + 1024 * (wv + SG_WAVES * d), 16, 0, 0);
+}
+
+/*
+ * LDS layout of a slot: row r (W rows 0..NT-1, then x rows) at 128 r; its 16-byte piece p (k columns 8p..8p+7 of
+ * the chunk) at position p ^ (r & 7), so the fragment reads below are bank-conflict free. DMA instruction i of a
+ * chunk moves rows 8i..8i+7: lane l lands at slot + 1024 i + 16 l (row 8i + l/8, position l % 8) and therefore
+ * fetches piece (l % 8) ^ (row & 7) of its row -- every instruction reads 8 whole 128-byte row segments.
+ */
+template <int NT, int MT, int EPI>
+__global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
+    constexpr int ROWS = NT + MT, DMAS = ROWS / 8, DPW = DMAS / SG_WAVES; /* DMA instructions per chunk, per wave */
+    constexpr int SLOT = sg_slot_bytes(NT, MT), D = sg_depth(NT, MT);
+    constexpr int WN = sg_waves_n(NT, MT), WM = SG_WAVES / WN; /* waves over W rows x batch rows */
+    constexpr int TNW = NT / 16 / WN, TMW = MT / 16 / WM;     /* 16x16 tiles per wave */
+    constexpr int TSQ = (TMW + WN - 1) / WN; /* batch tiles whose Σ x² this wave computes (shared with its row) */
+    constexpr bool NORM = EPI == SG_NORM_STORE || EPI == SG_RELU2_NORM || EPI == SG_NORM_F32;
+    static_assert(DMAS % SG_WAVES == 0 && NT % (16 * WN) == 0 && MT % (16 * WM) == 0, "tile shape");
+    static_assert(D >= 3, "ring depth");
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[D * SLOT];
+
+    const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
+    if (unit >= a.n_tiles * a.m_slices) return;
+    const int nt = unit / a.m_slices, ms = unit % a.m_slices;
+    const int row0 = nt * NT, m0 = ms * MT;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int j = lane >> 4, n = lane & 15;
+    const int wn = wv % WN, wm = wv / WN;
+    const int chunks = a.k / SG_CHUNK;
+    const size_t ld = (size_t)a.k;
+
+    /* this wave's DMA sources: instruction i = wv + SG_WAVES d of every chunk; x rows past m repeat row m - 1 */
+    const unsigned char *src[DPW];
+#pragma unroll
+    for (int d = 0; d < DPW; d++) {
+        const int r = 8 * (wv + SG_WAVES * d) + (lane >> 3);
+        const int piece = (lane & 7) ^ (r & 7);
+        const bf16_t *row = r < NT ? a.w + (size_t)(row0 + r) * ld : a.x + (size_t)min(m0 + r - NT, a.m - 1) * ld;
+        src[d] = reinterpret_cast<const unsigned char *>(row) + 16 * piece;
+    }
+    /* chunk c (clamped to the last) into ring slot `slot` */
+    auto dma = [&](int c, int slot) {
+        sg_dma<DPW>(src, (size_t)min(c, chunks - 1) * (SG_CHUNK * 2), ring + slot * SLOT, wv);
+    };
+
+    /* this wave's fragment addresses within a slot: W row tile t, x row tile u, k half h: piece 4h + j of row n */
+    uint32_t fw[TNW][2], fx[TMW][2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int t = 0; t < TNW; t++) {
+            const int r = 16 * (wn * TNW + t) + n;
+            fw[t][h] = sg_lds_addr(ring) + 128 * r + 16 * ((4 * h + j) ^ (r & 7));
+        }
+#pragma unroll
+        for (int u = 0; u < TMW; u++) {
+            const int r = NT + 16 * (wm * TMW + u) + n;
+            fx[u][h] = sg_lds_addr(ring) + 128 * r + 16 * ((4 * h + j) ^ (r & 7));
+        }
+    }
+
+    f32x4 acc[TNW][TMW];
+    f32x4 sq[TSQ];
+#pragma unroll
+    for (int t = 0; t < TNW; t++)
+#pragma unroll
+        for (int u = 0; u < TMW; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < TSQ; q++) sq[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    /* fragment reads of a chunk's slot (completed by the next sg_ds_wait) */
+    auto read = [&](int c, bf16x8 (&wf)[TNW][2], bf16x8 (&xf)[TMW][2]) {
+        const uint32_t so = (uint32_t)((c % D) * SLOT);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int t = 0; t < TNW; t++) wf[t][h] = sg_ds_read(fw[t][h] + so);
+#pragma unroll
+            for (int u = 0; u < TMW; u++) xf[u][h] = sg_ds_read(fx[u][h] + so);
+        }
+    };
+    auto settle = [&](bf16x8 (&wf)[TNW][2], bf16x8 (&xf)[TMW][2]) {
+        sg_ds_wait();
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int t = 0; t < TNW; t++) sg_after_wait(wf[t][h]);
+#pragma unroll
+            for (int u = 0; u < TMW; u++) sg_after_wait(xf[u][h]);
+        }
+    };
+    auto multiply = [&](const bf16x8 (&wf)[TNW][2], const bf16x8 (&xf)[TMW][2]) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int t = 0; t < TNW; t++)
+#pragma unroll
+                for (int u = 0; u < TMW; u++)
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[t][h], xf[u][h], acc[t][u], 0, 0, 0);
+            if constexpr (NORM) {
+                /* this wave's batch tiles u = q WN + wn, picked by selects (no dynamic register indexing, no branch);
+                 * past TMW the product is computed and ignored */
+#pragma unroll
+                for (int q = 0; q < TSQ; q++) {
+                    bf16x8 v = xf[q * WN < TMW ? q * WN : TMW - 1][h];
+#pragma unroll
+                    for (int w = 1; w < WN; w++)
+                        if (q * WN + w < TMW) v = wn == w ? xf[q * WN + w][h] : v;
+                    sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, v, sq[q], 0, 0, 0);
+                }
+            }
+        }
+    };
+    /* one iteration, straight-line code (fragments in flight never cross a branch, where the compiler could copy
+     * their registers before the data lands): once every wave has settled chunk c's fragments (the barrier), slot
+     * c % D takes chunk c + D; chunk c + 1's fragments are read while chunk c's MFMAs run, then settle. Past the
+     * end the chunk indices clamp to the last chunk, which the refill then rewrites with the same bytes. */
+    auto step = [&](int c, const bf16x8 (&wf)[TNW][2], const bf16x8 (&xf)[TMW][2], bf16x8 (&wn_)[TNW][2],
+                    bf16x8 (&xn_)[TMW][2]) {
+        sg_wait_vmcnt<DPW * (D - 2)>(); /* this wave's DMAs of chunk c + 1 have landed */
+        __builtin_amdgcn_s_barrier();   /* everyone's have, and everyone has settled chunk c's reads */
+        __builtin_amdgcn_sched_barrier(0);
+        dma(c + D, c % D);
+        read(min(c + 1, chunks - 1), wn_, xn_);
+        multiply(wf, xf);
+        settle(wn_, xn_);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+#pragma unroll
+    for (int c = 0; c < D; c++) dma(c, c); /* chunks 0..D-1 in flight (the slot of chunk D is that of chunk 0) */
+    sg_wait_vmcnt<DPW * (D - 1)>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 wa[TNW][2], xa[TMW][2], wb[TNW][2], xb[TMW][2];
+    read(0, wa, xa);
+    settle(wa, xa);
+    for (int c = 0; c < chunks; c += 2) {
+        step(c, wa, xa, wb, xb);
+        if (c + 1 < chunks) step(c + 1, wb, xb, wa, xa);
+    }
+    sg_wait_vmcnt<0>(); /* the clamped refills past the last chunk land before the ring is reused or released */
+
+    /* the rows' Σ x², each computed by one wave of its batch slice: x·xᵀ's diagonal, row n's in lane (n / 4, n),
+     * element n % 4; exchanged through LDS (the ring is free: every wave is past its last read) */
+    float rstd[TMW];
+    if constexpr (NORM) {
+        float *ss = reinterpret_cast<float *>(ring);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < TSQ; q++) {
+            const int u = q * WN + wn;
+            if (u < TMW && j == (n >> 2)) ss[16 * (wm * TMW + u) + n] = sq[q][n & 3];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TMW; u++)
+            rstd[u] = 1.0f / sqrtf(ss[16 * (wm * TMW + u) + n] / (float)a.k + 1.1920928955078125e-07f);
+    } else {
+#pragma unroll
+        for (int u = 0; u < TMW; u++) rstd[u] = 1.f;
+    }
+
+    const int N = a.n;
+#pragma unroll
+    for (int u = 0; u < TMW; u++) {
+        const int b = m0 + 16 * (wm * TMW + u) + n;
+        const float r = rstd[u];
+        if (b >= a.m) continue;
+#pragma unroll
+        for (int t = 0; t < TNW; t++) {
+            const f32x4 s = acc[t][u];
+            const int col = row0 + 16 * (wn * TNW + t) + 4 * j;
+            const size_t at = (size_t)b * N + col;
+            if constexpr (EPI == SG_NORM_F32) {
+                *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + at) = s * r;
+            } else {
+                float v[4];
+                if constexpr (EPI == SG_RESID) {
+                    const u32x2 rr = *reinterpret_cast<const u32x2 *>(a.res + at);
+                    v[0] = s[0] + bf16_to_f32(rr[0] & 0xffffu);
+                    v[1] = s[1] + bf16_to_f32(rr[0] >> 16);
+                    v[2] = s[2] + bf16_to_f32(rr[1] & 0xffffu);
+                    v[3] = s[3] + bf16_to_f32(rr[1] >> 16);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float p = s[i] * r;
+                        v[i] = EPI == SG_RELU2_NORM ? fmaxf(p, 0.f) * p : p;
+                    }
+                }
+                const u32x2 o = {f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
+                                 f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
+                *reinterpret_cast<u32x2 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------ host side */
+
+typedef void (*SgKernel)(SlotGemmArgs);
+
+template <int NT, int MT> static SgKernel sg_pick_epi(int epi) {
+    switch (epi) {
+    case SG_STORE: return k_slot_gemm<NT, MT, SG_STORE>;
+    case SG_NORM_STORE: return k_slot_gemm<NT, MT, SG_NORM_STORE>;
+    case SG_RESID: return k_slot_gemm<NT, MT, SG_RESID>;
+    case SG_RELU2_NORM: return k_slot_gemm<NT, MT, SG_RELU2_NORM>;
+    default: return k_slot_gemm<NT, MT, SG_NORM_F32>;
+    }
+}
+
+/* The tiles built: NT W rows x MT batch rows per workgroup (NT + MT a multiple of 32, so the 4 waves share a
+ * chunk's DMAs evenly). */
+static const int SG_TILES[][2] = {{32, 32}, {64, 32}, {32, 64}, {64, 64}, {32, 128}, {64, 128}, {128, 64}, {128, 128}};
+
+static SgKernel sg_pick(int nt, int mt, int epi) {
+    if (nt == 32 && mt == 32) return sg_pick_epi<32, 32>(epi);
+    if (nt == 64 && mt == 32) return sg_pick_epi<64, 32>(epi);
+    if (nt == 32 && mt == 64) return sg_pick_epi<32, 64>(epi);
+    if (nt == 64 && mt == 64) return sg_pick_epi<64, 64>(epi);
+    if (nt == 32 && mt == 128) return sg_pick_epi<32, 128>(epi);
+    if (nt == 64 && mt == 128) return sg_pick_epi<64, 128>(epi);
+    if (nt == 128 && mt == 64) return sg_pick_epi<128, 64>(epi);
+    if (nt == 128 && mt == 128) return sg_pick_epi<128, 128>(epi);
+    return nullptr;
+}
+
+/* The automatic tile: a workgroup moves (NT + MT) rows of K into its CU, and a CU fills at a roughly fixed rate, so
+ * the time is about (units per CU) x (NT + MT); among the tiles dividing n, the least of ceil(units / 256) x
+ * (NT + MT), ties to the larger tile (less re-reading of W and x through L2). */
+static void sg_auto_tile(int n, int m, int &nt, int &mt) {
+    long long best = -1;
+    nt = mt = 0;
+    for (const auto &t : SG_TILES) {
+        if (n % t[0] || (t[1] > 32 && t[1] / 2 >= m)) continue;
+        const long long units = (long long)(n / t[0]) * ((m + t[1] - 1) / t[1]);
+        const long long cost = ((units + 255) / 256) * (t[0] + t[1]);
+        if (best < 0 || cost < best || (cost == best && t[0] * t[1] > nt * mt)) {
+            best = cost;
+            nt = t[0];
+            mt = t[1];
+        }
+    }
+}
+
+extern "C" int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out,
+                                 const void *res, int nt, int mt, void *stream) {
+    NC_REQUIRE(n > 0 && k > 0 && m >= 0, "nc_slot_gemm_bf16: n %d, k %d, m %d", n, k, m);
+    NC_REQUIRE(n % 32 == 0 && k % SG_CHUNK == 0, "nc_slot_gemm_bf16: n = %d must be a multiple of 32 and k = %d of %d",
+               n, k, SG_CHUNK);
+    NC_REQUIRE(epi >= SG_STORE && epi <= SG_NORM_F32, "nc_slot_gemm_bf16: unknown epilogue %d", epi);
+    NC_REQUIRE((long long)n * k * 2 < (1LL << 31) && (long long)m * k * 2 < (1LL << 31),
+               "nc_slot_gemm_bf16: W (%d x %d) and x (%d x %d) must each stay under 2 GiB", n, k, m, k);
+    if (m == 0) return 0;
+    NC_REQUIRE(w && x && out, "nc_slot_gemm_bf16: null pointer");
+    NC_REQUIRE(epi != SG_RESID || res, "nc_slot_gemm_bf16: RESID needs res");
+    NC_REQUIRE(((uintptr_t)w | (uintptr_t)x | (uintptr_t)out | (uintptr_t)res) % 16 == 0,
+               "nc_slot_gemm_bf16: 16-byte alignment");
+    if (nt == 0 && mt == 0) sg_auto_tile(n, m, nt, mt);
+    const SgKernel kern = sg_pick(nt, mt, epi);
+    NC_REQUIRE(kern && n % nt == 0, "nc_slot_gemm_bf16: tile %d x %d is not available for n = %d", nt, mt, n);
+    SlotGemmArgs a;
+    a.w = (const bf16_t *)w;
+    a.x = (const bf16_t *)x;
+    a.out = out;
+    a.res = (const bf16_t *)res;
+    a.n = n;
+    a.k = k;
+    a.m = m;
+    a.n_tiles = n / nt;
+    a.m_slices = (m + mt - 1) / mt;
+    const long long units = (long long)a.n_tiles * a.m_slices;
+    a.units_per_xcd = (int)((units + 7) / 8);
+    hipLaunchKernelGGL(kern, dim3(8 * a.units_per_xcd), dim3(SG_THREADS), 0, (hipStream_t)stream, a);
+    NC_LAUNCH_CHECK();
+    return 0;
+}

@@ -9,9 +9,12 @@ prefilled, then every step feeds one token per sequence and appends the chosen o
     x' = h + down_proj(relu(up_proj(norm(h)))^2)
 
 with x0 = norm(embed(token)), a final norm, the untied lm_head and the greedy choice (largest fp32 logit, lowest id
-on ties, nc_argmax_f32). The weight GEMMs are plain library GEMMs (hipBLASLt through torch, bf16 in, fp32
-accumulate); the cache append, prefill and decode attention and the token choice are the HIP kernels. The decode
-step is captured once in a hipGraph and replayed.
+on ties, nc_argmax_f32). The decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the
+reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
+per-row rstd, ReLU^2 into the up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
+through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
+attention and the token choice are HIP kernels throughout; the decode step is captured once in a hipGraph and
+replayed.
 
 The architecture is BASELINE config 5's: RoPE, QK-norm, ReLU^2 MLP at 4x, untied embeddings, bf16 weights
 N(0, 0.02), full causal attention in every layer. The reference's training-time extras that this config does not
@@ -31,6 +34,7 @@ from nanochat_amd.attention import decode_attention, decode_workspace, prefill_a
 from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
 from nanochat_amd.native import check, hip_library, pointer, stream
 from nanochat_amd.rotary import rotary_tables
+from nanochat_amd.slot_gemm import NORM_F32, NORM_STORE, RELU2_NORM, RESID, slot_gemm
 
 EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear.py:20)
 
@@ -65,9 +69,11 @@ CONFIG5 = E2EConfig("cfg5-e2e-l26-d1664-h13-v65536-b128-prompt2048-steps512",
 
 
 def argmax_rows(logits: Tensor, out: Tensor | None = None) -> Tensor:
-    """Greedy choice per row of fp32 logits [rows][cols]: the largest value's column, the lowest on ties."""
-    _require(logits, "logits", torch.float32, 2)
-    if logits.stride(1) != 1:
+    """Greedy choice per row of fp32 logits [rows][cols] (rows contiguous, any row stride): the largest value's
+    column, the lowest on ties."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.dim() != 2:
+        raise ValueError("logits must be a 2-d fp32 tensor on the GPU")
+    if logits.stride(1) != 1 or logits.stride(0) < logits.shape[1]:
         raise ValueError("logits rows must be contiguous")
     rows, cols = logits.shape
     if out is None:
@@ -144,6 +150,13 @@ class Fp8Decoder:
         self.seq = torch.arange(batch, dtype=torch.int32, device=device)
         self.row_chunk = row_chunk
         self.graph: torch.cuda.CUDAGraph | None = None
+        # the slot GEMM takes weight rows in multiples of 32: the lm_head gets zero rows past the vocabulary, whose
+        # logits the choice skips
+        vp = -(-cfg.vocab // 32) * 32
+        self.lm_head = model.lm_head
+        if vp != cfg.vocab:
+            self.lm_head = torch.zeros((vp, cfg.d_model), dtype=torch.bfloat16, device=device)
+            self.lm_head[:cfg.vocab] = model.lm_head
 
     # ---------------------------------------------------------------------------------------------- layers
     def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
@@ -194,16 +207,22 @@ class Fp8Decoder:
     # ---------------------------------------------------------------------------------------------- decode
     def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor) -> Tensor:
         """One decode step: token tok[b] at position pos[b] of every sequence; the greedy choice into out_tok.
-        Returns the fp32 logits."""
-        x, h = self._embed(tok)
+        Returns the fp32 logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and
+        attention; x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
+        x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
         ctx = pos + 1
         for l in range(self.cfg.layers):
-            q = self._qkv_append(l, h, pos, self.seq)
+            lw = self.model.layers[l]
+            qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
+            q = self.caches[l].append(qkv, pos, self.seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin,
+                                      self.cfg.heads)
             o = decode_attention(q, self.caches[l], ctx, max_ctx=self.max_len, workspace=self.ws)
-            h = self._finish_layer(l, x, o)
-        logits = torch.mm(h, self.model.lm_head.t(), out_dtype=torch.float32)
-        argmax_rows(logits, out_tok)
-        return logits
+            slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
+            u = slot_gemm(x, lw["wup"], RELU2_NORM)
+            slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
+        logits = slot_gemm(x, self.lm_head, NORM_F32)
+        argmax_rows(logits[:, :self.cfg.vocab], out_tok)
+        return logits[:, :self.cfg.vocab]
 
     @torch.no_grad()
     def start(self, last_tokens: Tensor, position: int) -> None:

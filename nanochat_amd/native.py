@@ -32,6 +32,7 @@ SIGNATURES: dict[str, tuple] = {
     "nc_argmax_f32": (I32, [P, I32, I32, I64, P, P]),
     "nc_add_rms_norm_bf16": (I32, [P, P, P, P, I32, I32, P]),
     "nc_relu2_bf16": (I32, [P, P, I64, P]),
+    "nc_slot_gemm_bf16": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P]),
 }
 
 

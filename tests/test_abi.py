@@ -113,3 +113,22 @@ def test_argmax_rejects_bad_arguments():
     assert lib.nc_argmax_f32(FAKE, 4, 10, 5, FAKE, NULL) < 0
     assert lib.nc_argmax_f32(NULL, 4, 10, 10, FAKE, NULL) < 0 and "null" in lib.nc_last_error().decode()
     assert lib.nc_argmax_f32(FAKE, 0, 10, 10, FAKE, NULL) == 0  # nothing to do, nothing launched
+
+
+def test_slot_gemm_rejects_bad_arguments():
+    lib = native.hip_library()
+
+    def rejects(n, k, m, epi, res, tile, message):
+        rc = lib.nc_slot_gemm_bf16(FAKE, n, k, FAKE, m, epi, FAKE, res, tile[0], tile[1], NULL)
+        assert rc < 0
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error().decode()
+
+    rejects(48, 64, 8, 0, NULL, (0, 0), "multiple of 32")
+    rejects(32, 96, 8, 0, NULL, (0, 0), "multiple of 32")  # k % 64
+    rejects(32, 64, 8, 5, NULL, (0, 0), "epilogue")
+    rejects(32, 64, 8, 2, NULL, (0, 0), "RESID needs res")
+    rejects(32, 64, 8, 0, NULL, (16, 16), "tile")
+    rejects(32, 64, 8, 0, NULL, (48, 16), "tile")
+    rejects(96, 64, 8, 0, NULL, (64, 32), "tile")  # n not a multiple of the tile
+    rejects(1 << 20, 1 << 10, 8, 0, NULL, (0, 0), "2 GiB")
+    assert lib.nc_slot_gemm_bf16(FAKE, 32, 64, FAKE, 0, 0, FAKE, NULL, 0, 0, NULL) == 0  # m = 0: nothing launched
