@@ -3,8 +3,9 @@ decode tokens/s, bs64 ctx8K).
 
 Workload (config 3): batch 64, 16 query / 4 kv heads, head dim 128, prior context per sequence U[512, 8192]
 (seeded), fp8 e4m3 K/V in 16-token pages under a random block permutation, values N(0,1) with 1 % outliers at
-8σ. A step appends one token to every sequence (QK-norm + RoPE + quantise) and runs decode attention over the
-fp8 cache; the step is captured once in a HIP graph (positions advance on the device) and replayed.
+8σ. A step appends one token to every sequence (QK-norm + RoPE + quantise; the append also writes the next
+positions, pos + 1, which are this step's context lengths) and runs decode attention over the fp8 cache; two steps
+(positions ping-ponging between two tensors) are captured in a HIP graph and replayed.
 
 Output: one JSON line. value = algorithmic attention bytes per step / measured step time (GB/s, inputs resident in
 HBM); roofline = the decode-attention call (k_decode, then k_merge) timed over graph replays of 10 back-to-back
@@ -231,43 +232,61 @@ def main():
     case = build_decode_case(cfg, dev, steps=steps + warmup + 2)
     B = cfg.batch
     max_ctx = case.cache.capacity
-    # positions and context lengths in one tensor, so a single add advances both
-    pos_ctx = torch.stack([case.positions(0), case.positions(0) + 1]).contiguous()
-    pos, ctx_len = pos_ctx[0], pos_ctx[1]
+    # positions ping-pong between two tensors: a step appends at pos and its append writes pos + 1 into the other
+    # tensor, which is the decode's context length and the next step's positions (no position-advance kernel)
+    p0 = case.positions(0).contiguous()
+    p1 = torch.empty_like(p0)
     qkv = case.qkv[0].contiguous()
     ws = decode_workspace(B, cfg.hq, cfg.hkv, max_ctx, dev)
     out = torch.empty((B, cfg.hq, 128), dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
 
+    def step(pos, ctx):
+        q = case.cache.append(qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq, ctx_out=ctx)
+        decode_attention(q, case.cache, ctx, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+        return q
+
     stream = torch.cuda.Stream(dev)
-    step_graph, attn_graph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    graph_ab, graph_a, attn_graph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        # eager warm-up of every launch path before capture
-        q = case.cache.append(qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
-        decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+        # eager warm-up of every launch path before capture: two steps, positions back in p0
+        step(p0, p1)
+        step(p1, p0)
         stream.synchronize()
-        with torch.cuda.graph(step_graph, stream=stream):
-            q = case.cache.append(qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
-            decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
-            pos_ctx.add_(1)
+        with torch.cuda.graph(graph_ab, stream=stream):
+            step(p0, p1)
+            q_b = step(p1, p0)
+        with torch.cuda.graph(graph_a, stream=stream):
+            q_a = step(p0, p1)
+    done = 2
+    for _ in range(warmup // 2):
+        graph_ab.replay()
+        done += 2
+    stream.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(steps // 2):
+            graph_ab.replay()
+        if steps % 2:
+            graph_a.replay()
+        e1.record(stream)
+    e1.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    wall = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    base = case.ctx + done  # keys before the timed steps (prior context + the appended tokens)
+    final_ctx = base + steps  # the keys of the last step
+    q, ctx_len = (q_a, p1) if steps % 2 else (q_b, p0)  # the last step's queries and context lengths
+    with torch.cuda.stream(stream):
         with torch.cuda.graph(attn_graph, stream=stream):
             for _ in range(ATTN_REPS):
                 decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
-    # the eager warm-up appended at pos (same bytes the first replay rewrites); positions now start at ctx
-    for _ in range(warmup):
-        step_graph.replay()
-    stream.synchronize()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    step_ms = replay_ms(step_graph, steps, stream)
-    wall = time.perf_counter() - t0
-    torch.cuda.synchronize()
-    final_ctx = case.ctx + warmup + steps  # the keys of the last step (prior + appended tokens)
-    ctx_len.sub_(1)  # the step's add ran ahead to the next token: attend over the last step's keys again
-    torch.cuda.synchronize()
     attn_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
 
-    step_bytes = np.mean([decode_bytes(case.ctx + warmup + i + 1, cfg.hkv, cfg.window) for i in range(steps)])
+    step_bytes = np.mean([decode_bytes(base + i + 1, cfg.hkv, cfg.window) for i in range(steps)])
     attn_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
     value = step_bytes / (step_ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -286,9 +305,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": cfg.name, "batch": B, "hq": cfg.hq, "hkv": cfg.hkv, "head_dim": 128,
                    "ctx_prior": "U[512,8192] seed 3", "page": 16, "outliers": "1% at 8 sigma",
-                   "mean_keys_per_seq": round(float(np.mean(case.ctx + warmup + steps / 2 + 1)), 1),
-                   "step": "append 1 token/seq (qk-norm+rope+fp8 quantise) + split-K decode attention + position "
-                           "advance, one attention layer, one hipGraph replay per step"},
+                   "mean_keys_per_seq": round(float(np.mean(base + steps / 2 + 1)), 1),
+                   "step": "append 1 token/seq (qk-norm+rope+fp8 quantise, emitting the next positions) + split-K "
+                           "decode attention, one attention layer, graph replays of two steps"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_one_layer": round(B / (step_ms * 1e-3), 1),
         "attn_us": round(attn_ms * 1e3, 3),

@@ -47,12 +47,14 @@ void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, v
  * of 128): q and k RMS-normed with gains q_gain, k_gain, rotated by cos/sin fp32 [rope_len][64] at pos[n]; q to
  * q_out (bf16 [n][Hq][128]); k and v quantised per (token, kv head) into sequence seq[n]'s page. A row out of range
  * (pos < 0 or >= rope_len or past max_blocks pages, seq outside [0, num_seqs), block outside [0, num_blocks))
- * writes no cache byte and gets a NaN q_out row.
+ * writes no cache byte and gets a NaN q_out row. ctx_out (optional, int32 [n], must not overlap pos) receives
+ * pos + 1 for every row: the context lengths the following decode attends with, and the next step's positions
+ * (the position advance the reference's k_commit makes, decode.cu:1107-1124, without a kernel of its own).
  * Replaces: k_prologue + attn_prologue, model/kernels/decode.cu:476-507,550-565 (which cache bf16). */
 int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, const int32_t *pos, const int32_t *seq,
                      const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
                      int hq, int hkv, void *q_out, uint8_t *cache, const int32_t *block_table, int max_blocks,
-                     int num_blocks, int num_seqs, void *stream);
+                     int num_blocks, int num_seqs, int32_t *ctx_out, void *stream);
 
 /* Quantise-and-store of final K and V rows (bf16 [n][row_stride], Hkv heads of 128, no norm or rotation) at
  * (seq[n], pos[n]).

@@ -61,6 +61,7 @@ struct AppendArgs {
     int rope_len;
     int hq, hkv;
     bf16_t *q_out;            /* fused mode: [n][hq][128] */
+    int32_t *ctx_out;         /* fused mode, optional: [n] pos + 1, the context length after the append */
     uint8_t *cache;           /* [num_blocks][hkv][4224] tiles */
     const int32_t *block_table;
     int max_blocks, num_blocks, num_seqs;
@@ -76,6 +77,7 @@ __global__ void __launch_bounds__(APPEND_THREADS) k_append(AppendArgs a) {
     const int g = threadIdx.x % NC_ROW_LANES;
     const int row = (int)(item / heads), head = (int)(item % heads);
     const int p = a.pos[row], s = a.seq[row];
+    if (a.ctx_out && head == 0 && g == 0) a.ctx_out[row] = p + 1; /* never aliases pos (host check) */
     bool ok = p >= 0 && s >= 0 && s < a.num_seqs;
     if (a.fused) ok = ok && p < a.rope_len;
     const int blk = ok ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, s, p / NC_PAGE) : -1;
@@ -155,7 +157,7 @@ extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, co
                                 const int32_t *seq, const float *q_gain, const float *k_gain, const float *cos,
                                 const float *sin, int rope_len, int hq, int hkv, void *q_out, uint8_t *cache,
                                 const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs,
-                                void *stream) {
+                                int32_t *ctx_out, void *stream) {
     int rc = check_cache_args(n, hkv, max_blocks, num_blocks, num_seqs, cache, block_table);
     if (rc) return rc;
     NC_REQUIRE(hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
@@ -164,10 +166,11 @@ extern "C" int nc_kv_append_fp8(const void *qkv, long long row_stride, int n, co
     NC_REQUIRE(rope_len > 0, "rope_len = %d", rope_len);
     NC_REQUIRE(n == 0 || (qkv && pos && seq && q_gain && k_gain && cos && sin && q_out), "null argument");
     NC_REQUIRE(((uintptr_t)qkv | (uintptr_t)q_out) % 16 == 0, "qkv and q_out must be 16-byte aligned");
+    NC_REQUIRE(!ctx_out || ctx_out + n <= pos || pos + n <= ctx_out, "ctx_out must not overlap pos");
     AppendArgs a = {};
     a.qkv = (const bf16_t *)qkv; a.row_stride = row_stride; a.n = n; a.pos = pos; a.seq = seq;
     a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
-    a.hq = hq; a.hkv = hkv; a.q_out = (bf16_t *)q_out;
+    a.hq = hq; a.hkv = hkv; a.q_out = (bf16_t *)q_out; a.ctx_out = ctx_out;
     a.cache = cache;
     a.block_table = block_table; a.max_blocks = max_blocks; a.num_blocks = num_blocks; a.num_seqs = num_seqs;
     a.fused = 1;

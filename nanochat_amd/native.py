@@ -23,7 +23,7 @@ SIGNATURES: dict[str, tuple] = {
     "nc_abi_version": (I32, []),
     "nc_last_error": (ctypes.c_char_p, []),
     "qkp_forward": (None, [P, P, P, P, P, P, P, P, I64, I32, I32, P]),
-    "nc_kv_append_fp8": (I32, [P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P, P, P, I32, I32, I32, P]),
+    "nc_kv_append_fp8": (I32, [P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P, P, P, I32, I32, I32, P, P]),
     "nc_kv_store_fp8": (I32, [P, P, I64, I32, P, P, I32, P, P, I32, I32, I32, P]),
     "nc_kv_gather_fp8": (I32, [P, P, I32, I32, P, I32, I32, I32, P, P, P, P, P]),
     "nc_decode_workspace_bytes": (I64, [I32, I32, I32, I32]),

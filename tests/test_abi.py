@@ -62,7 +62,7 @@ def test_decode_rejects_bad_arguments(kwargs, message):
 
 def test_append_rejects_bad_arguments():
     lib = native.hip_library()
-    base = [FAKE, 1024, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 16, 4, FAKE, FAKE, NULL, 8, 64, 8, NULL]
+    base = [FAKE, 1024, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 16, 4, FAKE, FAKE, NULL, 8, 64, 8, NULL, NULL]
     bad_stride = list(base)
     bad_stride[1] = 100
     assert lib.nc_kv_append_fp8(*bad_stride) < 0 and "row_stride" in lib.nc_last_error().decode()
@@ -72,6 +72,10 @@ def test_append_rejects_bad_arguments():
     null_cache = list(base)
     null_cache[13] = NULL
     assert lib.nc_kv_append_fp8(*null_cache) < 0 and "null" in lib.nc_last_error().decode()
+    ctx_on_pos = list(base)
+    ctx_on_pos[1] = (16 + 2 * 4) * 128
+    ctx_on_pos[3] = ctx_on_pos[18] = ctypes.c_void_p(0x2000)  # ctx_out overlapping pos
+    assert lib.nc_kv_append_fp8(*ctx_on_pos) < 0 and "overlap" in lib.nc_last_error().decode()
     assert lib.nc_kv_store_fp8(FAKE, FAKE, 100, 4, FAKE, FAKE, 4, FAKE, NULL, 8, 64, 8, NULL) < 0
     assert lib.nc_kv_gather_fp8(FAKE, NULL, 8, 64, FAKE, 8, 4, 200, FAKE, FAKE, FAKE, FAKE, NULL) < 0
 

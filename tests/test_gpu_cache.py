@@ -79,9 +79,11 @@ def test_append_rows_out_of_range_write_nothing(gpu):
     pos = torch.tensor([-1, 64, 3, 40, 5], dtype=torch.int32, device=dev)
     seq = torch.tensor([0, 0, 2, 1, 1], dtype=torch.int32, device=dev)
     ones = torch.ones(128, device=dev)
-    q = cache.append(qkv, pos, seq, ones, ones, cos, sin, hq)
+    ctx = torch.full_like(pos, -7)
+    q = cache.append(qkv, pos, seq, ones, ones, cos, sin, hq, ctx_out=ctx)
     torch.cuda.synchronize()
     assert torch.isnan(q[:3].float()).all() and not torch.isnan(q[3:].float()).any()
+    assert ctx.tolist() == (pos + 1).tolist()  # every row, in range or not, gets pos + 1
     G.append(before, bits(qkv[4:]), np.array([5]), np.array([1]), np.ones(128, np.float32),
              np.ones(128, np.float32), cos.cpu().numpy(), sin.cpu().numpy(), hq, hkv, table(cache),
              cache.max_blocks)
