@@ -3,13 +3,15 @@ decode tokens/s, bs64 ctx8K).
 
 Workload (config 3): batch 64, 16 query / 4 kv heads, head dim 128, prior context per sequence U[512, 8192]
 (seeded), fp8 e4m3 K/V in 16-token pages under a random block permutation, values N(0,1) with 1 % outliers at
-8σ. A step appends one token to every sequence (QK-norm + RoPE + quantise; the append also writes the next
-positions, pos + 1, which are this step's context lengths) and runs decode attention over the fp8 cache; two steps
+8σ. A step appends one token to every sequence (QK-norm + RoPE + quantise) and runs decode attention over the fp8
+cache, new keys included: one nc_decode_step_fp8 call (the append fused into the attention kernel; --unfused: an
+nc_kv_append_fp8 call, then nc_decode_attn_fp8). Each step also writes the next positions, pos + 1; two steps
 (positions ping-ponging between two tensors) are captured in a HIP graph and replayed.
 
 Output: one JSON line. value = algorithmic attention bytes per step / measured step time (GB/s, inputs resident in
-HBM); roofline = the decode-attention call (k_decode, then k_merge) timed over graph replays of 10 back-to-back
-calls with HIP events on their stream;
+HBM); roofline = the step's attention call (k_decode, then k_merge): the timed steps themselves (one
+nc_decode_step_fp8 call each), or with --unfused the attention call alone at the last step's context, timed over
+graph replays of 10 back-to-back calls, with HIP events on their stream;
 cpu_baseline = the numpy oracle over a bounded sample of the same sequences on this host's cores.
 """
 
@@ -45,6 +47,9 @@ def parse():
     ap.add_argument("--only", choices=["decode2", "prefill4", "e2e5"],
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="time the step as two calls (nc_kv_append_fp8, then nc_decode_attn_fp8) instead of the "
+                         "fused nc_decode_step_fp8")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the measurement, copy a 1 GiB buffer 3 times (the byte-counter calibration kernel)")
     return ap.parse_args()
@@ -217,7 +222,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from nanochat_amd.attention import decode_attention, decode_workspace
+    from nanochat_amd.attention import decode_attention, decode_step, decode_workspace
     from nanochat_amd.workloads import CONFIG3, build_decode_case, decode_bytes
 
     dev = torch.device("cuda:0")
@@ -232,8 +237,8 @@ def main():
     case = build_decode_case(cfg, dev, steps=steps + warmup + 2)
     B = cfg.batch
     max_ctx = case.cache.capacity
-    # positions ping-pong between two tensors: a step appends at pos and its append writes pos + 1 into the other
-    # tensor, which is the decode's context length and the next step's positions (no position-advance kernel)
+    # positions ping-pong between two tensors: a step appends at pos and writes pos + 1 into the other tensor, the
+    # next step's positions (no position-advance kernel)
     p0 = case.positions(0).contiguous()
     p1 = torch.empty_like(p0)
     qkv = case.qkv[0].contiguous()
@@ -241,10 +246,15 @@ def main():
     out = torch.empty((B, cfg.hq, 128), dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
 
-    def step(pos, ctx):
+    def fused(pos, nxt):
+        decode_step(qkv, case.cache, pos, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq, max_ctx=max_ctx,
+                    window=cfg.window, out=out, workspace=ws, pos_out=nxt)
+
+    def unfused(pos, ctx):
         q = case.cache.append(qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq, ctx_out=ctx)
         decode_attention(q, case.cache, ctx, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
-        return q
+
+    step = unfused if args.unfused else fused
 
     stream = torch.cuda.Stream(dev)
     graph_ab, graph_a, attn_graph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
@@ -255,9 +265,9 @@ def main():
         stream.synchronize()
         with torch.cuda.graph(graph_ab, stream=stream):
             step(p0, p1)
-            q_b = step(p1, p0)
+            step(p1, p0)
         with torch.cuda.graph(graph_a, stream=stream):
-            q_a = step(p0, p1)
+            step(p0, p1)
     done = 2
     for _ in range(warmup // 2):
         graph_ab.replay()
@@ -279,17 +289,29 @@ def main():
     torch.cuda.synchronize()
     base = case.ctx + done  # keys before the timed steps (prior context + the appended tokens)
     final_ctx = base + steps  # the keys of the last step
-    q, ctx_len = (q_a, p1) if steps % 2 else (q_b, p0)  # the last step's queries and context lengths
+    ctx_len = p1 if steps % 2 else p0  # the last step's context lengths: its positions + 1
     with torch.cuda.stream(stream):
-        with torch.cuda.graph(attn_graph, stream=stream):
-            for _ in range(ATTN_REPS):
-                decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
-    attn_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
-
+        # the last step's queries (cpu_baseline); appending its tokens again rewrites the same cache bytes
+        q = case.cache.append(qkv, ctx_len - 1, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
     step_bytes = np.mean([decode_bytes(base + i + 1, cfg.hkv, cfg.window) for i in range(steps)])
-    attn_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
     value = step_bytes / (step_ms * 1e-3) / 1e9
-    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    if args.unfused:
+        # roofline of the attention call alone: ATTN_REPS calls at the last step's context in one graph
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(attn_graph, stream=stream):
+                for _ in range(ATTN_REPS):
+                    decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out,
+                                     workspace=ws)
+        call_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
+        call_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
+        call_kernel = (f"nc_decode_attn_fp8 = k_decode<false> + k_merge, a graph of {ATTN_REPS} calls at the last "
+                       "step's context, HIP events on their stream")
+    else:
+        # the step is one nc_decode_step_fp8 call: the timed region is the roofline measurement itself
+        call_ms, call_bytes = step_ms, step_bytes
+        call_kernel = ("nc_decode_step_fp8 = k_decode<true> + k_merge, one call per timed step, HIP events on their "
+                       "stream")
+    achieved = call_bytes / (call_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -306,18 +328,18 @@ def main():
         "config": {"workload": cfg.name, "batch": B, "hq": cfg.hq, "hkv": cfg.hkv, "head_dim": 128,
                    "ctx_prior": "U[512,8192] seed 3", "page": 16, "outliers": "1% at 8 sigma",
                    "mean_keys_per_seq": round(float(np.mean(base + steps / 2 + 1)), 1),
-                   "step": "append 1 token/seq (qk-norm+rope+fp8 quantise, emitting the next positions) + split-K "
+                   "step": ("nc_kv_append_fp8 + nc_decode_attn_fp8" if args.unfused else
+                            "nc_decode_step_fp8 (append fused into the attention kernel)") +
+                           ": append 1 token/seq (qk-norm+rope+fp8 quantise, emitting the next positions) + split-K "
                            "decode attention, one attention layer, graph replays of two steps"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_one_layer": round(B / (step_ms * 1e-3), 1),
-        "attn_us": round(attn_ms * 1e3, 3),
+        "call_us": round(call_ms * 1e3, 3),
         "step_us": round(step_ms * 1e3, 3),
         "wall_s_timed": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
-                     "kernel": "nc_decode_attn_fp8 = k_decode + k_merge, back to back in a graph of "
-                               f"{ATTN_REPS} calls, HIP events on their stream",
-                     "bytes_per_launch": int(attn_bytes)},
+                     "kernel": call_kernel, "bytes_per_launch": int(call_bytes)},
     }
     if not args.no_extra:
         result["decode_cfg2"] = extra_decode_cfg2(dev, stream)

@@ -88,6 +88,24 @@ int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int32_t *block
                        int num_blocks, const int32_t *ctx_len, int window, int B, int hq, int hkv, int max_ctx,
                        float sm_scale, void *out, void *workspace, long long workspace_bytes, void *stream);
 
+/* A whole decode step's attention in two launches: the append of nc_kv_append_fp8 fused into
+ * nc_decode_attn_fp8. Row b of the projection qkv (bf16 [B][row_stride]: Hq q heads, Hkv k heads, Hkv v heads)
+ * is token pos[b] of sequence b: its q heads are QK-normed, gained (q_gain [128]) and rotated (cos / sin
+ * [rope_len][64]) as nc_kv_append_fp8 does, its key (k_gain) and value are quantised into sequence b's page, and
+ * q attends keys [max(pos - window, 0), pos], the new key included. Cache bytes, scales and out are bit-identical
+ * to nc_kv_append_fp8 (seq[b] = b) followed by nc_decode_attn_fp8 with ctx_len = pos + 1, for every row with
+ * 0 <= pos < min(max_ctx, rope_len). A row with pos < 0 writes nothing and gets a zero row; a row with pos at or
+ * past max_ctx or rope_len writes nothing and gets a NaN row. pos_out (optional, int32 [B], not overlapping pos)
+ * receives pos + 1, the next step's positions. out must not overlap qkv. Workspace and other arguments as
+ * nc_decode_attn_fp8.
+ * Replaces: the decode body's k_prologue append (model/kernels/decode.cu:550-565) and k_attn (decode.cu:567-675),
+ * launched back to back by the reference. */
+int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                       const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                       uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks, int window, int B,
+                       int hq, int hkv, int max_ctx, float sm_scale, void *out, void *workspace,
+                       long long workspace_bytes, void *stream);
+
 /* Chunked-prefill attention: row r (bf16 q [n][Hq][128], normed and rotated, e.g. nc_kv_append_fp8's q_out) at
  * position pos[r] of sequence seq[r] attends keys [max(pos - window, 0), pos] of that sequence in the cache
  * (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores times sm_scale, fp32 softmax, bf16 out

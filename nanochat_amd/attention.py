@@ -65,6 +65,48 @@ def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: 
     return out
 
 
+def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_gain: Tensor, cos: Tensor,
+                sin: Tensor, hq: int, *, max_ctx: int, window: int = -1, sm_scale: float | None = None,
+                out: Tensor | None = None, workspace: Tensor | None = None, pos_out: Tensor | None = None) -> Tensor:
+    """Fp8KVCache.append (row b into sequence b at pos[b]) and decode_attention (ctx_len = pos + 1) in one call of
+    two launches, with bit-identical cache bytes and output: the reference's decode-body append (decode.cu:550-565)
+    and k_attn. qkv bf16 [B][>= (hq + 2 hkv) 128] row-major; pos int32 [B]. A row with pos < 0 gets a zero row, a
+    row with pos at or past max_ctx or len(cos) a NaN row; neither writes the cache. pos_out (int32 [B], another
+    tensor than pos) receives pos + 1. Returns bf16 [B][hq][128]."""
+    if qkv.dim() != 2 or qkv.dtype != torch.bfloat16 or not qkv.is_cuda or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a row-major bf16 [B][width] GPU tensor")
+    B = qkv.shape[0]
+    _require(pos, "pos", torch.int32, 1)
+    if pos.shape[0] != B or B > cache.num_seqs:
+        raise ValueError(f"pos has {pos.shape[0]} entries for batch {B} (cache holds {cache.num_seqs})")
+    for t, name in ((q_gain, "q_gain"), (k_gain, "k_gain"), (cos, "cos"), (sin, "sin")):
+        _require(t, name, torch.float32)
+    if pos_out is not None:
+        _require(pos_out, "pos_out", torch.int32, 1)
+        if pos_out.shape[0] != B:
+            raise ValueError(f"pos_out has {pos_out.shape[0]} entries for batch {B}")
+    if not 0 < max_ctx <= cache.capacity:
+        raise ValueError(f"max_ctx {max_ctx} outside [1, {cache.capacity}]")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    if out is None:
+        out = torch.empty((B, hq, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    else:
+        _require(out, "out", torch.bfloat16, 3)
+        if tuple(out.shape) != (B, hq, HEAD_DIM):
+            raise ValueError(f"out must be [{B}][{hq}][{HEAD_DIM}]")
+    need = decode_workspace_bytes(B, hq, cache.hkv, max_ctx)
+    if workspace is None:
+        workspace = decode_workspace(B, hq, cache.hkv, max_ctx, qkv.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
+    check(hip_library().nc_decode_step_fp8(
+        pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos), pointer(sin),
+        cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks, cache.num_blocks, window, B,
+        hq, cache.hkv, max_ctx, scale, pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
+        stream()))
+    return out
+
+
 def prefill_attention(q: Tensor, cache: Fp8KVCache, pos: Tensor, seq: Tensor, *, window: int = -1,
                       sm_scale: float | None = None, out: Tensor | None = None) -> Tensor:
     """q bf16 [n][Hq][128] (Fp8KVCache.append's q_out for the chunk); pos, seq int32 [n] on the GPU. The chunk's

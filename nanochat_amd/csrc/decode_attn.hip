@@ -32,9 +32,17 @@
  * coherent with each other, so an in-kernel "last wave merges" handshake needs agent-scope fences, which on
  * gfx950 write back and invalidate the whole L2 (buffer_wbl2 / buffer_inv) and cost more than a launch.
  *
+ * The fused step (nc_decode_step_fp8) is the append and the attention of a decode step in these two launches
+ * instead of three (reference: k_prologue's append, decode.cu:550-565, then k_attn). Every piece builds its q
+ * rows from the projection (QK-norm, gain, RoPE, the row math of k_append, so bit-identical), and the piece that
+ * ends a segment also quantises the new key and value, patches them into its registers for the last page and
+ * stores them in the cache after its pages: that page is read by no other wave, so the new key needs no ordering
+ * between waves.
+ *
  * Roofline: HBM. Per (token, kv head) the kernel reads 128 B of K, 128 B of V and two fp32 scales: 264 B.
  */
 #include "layout.h"
+#include "qk_row.h"
 
 
 #define DEC_THREADS 64
@@ -46,6 +54,16 @@
 #ifndef DEC_DEPTH
 #define DEC_DEPTH 4         /* page buffers per wave: 3 pages (12.4 KiB) in flight while one is computed */
 #endif
+/* Schedule units (page equivalents, measured on config 3 with NC_DECODE_UNITS sweeps) of a piece start (the
+ * segment's context length and block ids: two dependent round trips) and of a segment's end (the fused step's q
+ * rows and the append's quantisation; the same in both entry points, so that they split the work alike and give
+ * bit-identical outputs). */
+#ifndef DEC_UNITS_START
+#define DEC_UNITS_START 3
+#endif
+#ifndef DEC_UNITS_END
+#define DEC_UNITS_END 6
+#endif
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 1 /* one wave per SIMD: no older/younger wave competing for issue on a SIMD */
 #endif
@@ -55,10 +73,17 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 struct DecodeArgs {
     const bf16_t *q;          /* [B][hq][128] */
-    const uint8_t *cache;     /* [num_blocks][hkv][4224] tiles */
+    uint8_t *cache;           /* [num_blocks][hkv][4224] tiles; written only by the fused step's append */
     const int32_t *block_table;
     int max_blocks, num_blocks;
-    const int32_t *ctx_len;   /* [B] */
+    const int32_t *ctx_len;   /* [B]; the fused step: the positions */
+    /* the fused step: q and the new key/value come from the projection rows (null: q is given) */
+    const bf16_t *qkv;        /* [B][row_stride]: hq q heads, hkv k heads, hkv v heads */
+    long long row_stride;
+    const float *q_gain, *k_gain; /* [128] */
+    const float *cos, *sin;   /* [rope_len][64] */
+    int rope_len;
+    int32_t *pos_out;         /* optional [B]: pos + 1, the next step's positions (never aliases the positions) */
     int window;               /* keys before the query; < 0: all */
     int B, hq, hkv, group;
     float score_scale;        /* sm_scale * log2(e) */
@@ -66,6 +91,7 @@ struct DecodeArgs {
     float *ws_o;              /* [DEC_MAX_WAVES + S][group][128]: the pieces' Σ p v, slot wave + segment */
     float *ws_ml;             /* [DEC_MAX_WAVES + S][group][2] */
     int max_ctx;              /* ctx_len is clamped to it */
+    int unit_start, unit_end; /* schedule units a non-empty segment costs before its first and after its last page */
 };
 
 /* The key range of sequence b: pages [first, last] (none if last < first), keys [begin, p]. */
@@ -73,9 +99,18 @@ struct SeqRange {
     int first, last, begin, p;
 };
 
+/* The context length of sequence b: ctx_len[b] clamped to [0, max_ctx]. The fused step reads a position p and
+ * gives p + 1, 0 for p < 0, and -1 (no append, a NaN output row) for p at or past max_ctx or rope_len. */
+__device__ __forceinline__ int seq_ctx(const DecodeArgs &a, int b) {
+    const int v = a.ctx_len[b];
+    if (!a.qkv) return max(min(v, a.max_ctx), 0);
+    if (v < 0) return 0;
+    return (v >= a.max_ctx || v >= a.rope_len) ? -1 : v + 1;
+}
+
 __device__ __forceinline__ SeqRange seq_range(const DecodeArgs &a, int b) {
     SeqRange r;
-    const int ctx = min(a.ctx_len[b], a.max_ctx);
+    const int ctx = seq_ctx(a, b);
     if (ctx <= 0) {
         r.first = 0, r.last = -1, r.begin = 0, r.p = -1;
         return r;
@@ -90,6 +125,14 @@ __device__ __forceinline__ SeqRange seq_range(const DecodeArgs &a, int b) {
 __device__ __forceinline__ int seq_pages(const DecodeArgs &a, int b) {
     const SeqRange r = seq_range(a, b);
     return r.last - r.first + 1;
+}
+
+/* Schedule units of one segment of sequence b: its pages plus the fixed costs of starting a piece there and of
+ * ending the segment (the fused step's append), in page equivalents, so that the waves that carry them get fewer
+ * pages; an empty sequence costs nothing. */
+__device__ __forceinline__ int seq_units(const DecodeArgs &a, int b) {
+    const int pg = seq_pages(a, b);
+    return pg > 0 ? pg + a.unit_start + a.unit_end : 0;
 }
 
 __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
@@ -159,9 +202,44 @@ __device__ __forceinline__ void state_init(State &st) {
     st.vlim = exp2i(-126);
 }
 
+/* The fused step's new key and value (codes and scales in LDS, key t = p % 16 of the last page): t >= 0 when
+ * the piece appends. */
+struct StepLds {
+    bf16_t q[DEC_MAX_G][NC_HEAD_DIM];
+    uint8_t codes[2][NC_HEAD_DIM]; /* new key, new value */
+    float scale[2];
+    int blk;                       /* their block, -1: none */
+};
+
+/* Put the new key and value into a page loaded before they were stored: lane (j, n) holds K row n, dims 32 j..,
+ * and the V codes of dims 8 n.. for keys 4 j..4 j + 3. */
+__device__ __forceinline__ void apply_patch(Page &pg, const StepLds &sm, int t, int n, int j) {
+    if (n == t) {
+        pg.k0 = *reinterpret_cast<const u32x4 *>(&sm.codes[0][32 * j]);
+        pg.k1 = *reinterpret_cast<const u32x4 *>(&sm.codes[0][32 * j + 16]);
+    }
+    if (j == (t >> 2)) {
+        const u32x2 v = *reinterpret_cast<const u32x2 *>(&sm.codes[1][8 * n]);
+        const int sh = 8 * (t & 3);
+        const uint32_t keep = ~(0xffu << sh);
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            pg.v0[bb] = (pg.v0[bb] & keep) | (((v[0] >> (8 * bb)) & 0xffu) << sh);
+            pg.v1[bb] = (pg.v1[bb] & keep) | (((v[1] >> (8 * bb)) & 0xffu) << sh);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pg.ks[i] = i == (t & 3) ? sm.scale[0] : pg.ks[i];
+            pg.vs[i] = i == (t & 3) ? sm.scale[1] : pg.vs[i];
+        }
+    }
+}
+
 /* Attend one page: pg its page number in the sequence. */
-__device__ __forceinline__ void attend_page(const DecodeArgs &a, const Page &pg, int page, const SeqRange &sr,
-                                            const bf16x8 *qop, int j, State &st) {
+__device__ __forceinline__ void attend_page(const DecodeArgs &a, Page pg, int page, const SeqRange &sr,
+                                            const bf16x8 *qop, int lane, int patch_t, const StepLds &sm, State &st) {
+    const int j = lane >> 4;
+    if (patch_t >= 0 && page == sr.last) apply_patch(pg, sm, patch_t, lane & 15, j);
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(pg.k0[0], pg.k0[1]), qop[0], s, 0, 0, 0);
     s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(pg.k0[2], pg.k0[3]), qop[1], s, 0, 0, 0);
@@ -221,14 +299,146 @@ __device__ __forceinline__ void attend_page(const DecodeArgs &a, const Page &pg,
     }
 }
 
-/* The pages [pg_lo, pg_lo + npg) of segment (b, h), DEC_DEPTH buffers in rotation: DEC_DEPTH - 1 pages are in
- * flight while one is computed. */
-__device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
-                                           const bf16x8 *qop, int lane, State &st) {
+/* ------------------------------------------------------------------------------------------ fused step rows */
+
+#define DEC_ROW_PASSES ((DEC_MAX_G + 2 + 7) / 8) /* 8-lane rows per wave pass: G q heads, the k and v heads */
+
+/* A piece's projection rows in the 8-lane row layout of qk_row.h (lane g = lane % 8 holds dims [8g, 8g + 8) and
+ * [64 + 8g, 64 + 8g + 8)): row ri = 8 pass + lane / 8 is q head h G + ri for ri < G, then the k head and the v
+ * head of kv head h when the piece appends. Loaded before the first pages, used once they are in flight. */
+struct Rows {
+    u32x4 lo[DEC_ROW_PASSES], hi[DEC_ROW_PASSES];
+    f32x4 qg[4], kg[4], cs[2], sn[2];
+    int blk; /* the new key's block (table entry, unchecked) */
+};
+
+__device__ __forceinline__ void load_rows(const DecodeArgs &a, int b, int h, int p, bool app, int lane, Rows &rw) {
+    const int g = lane & 7, G = a.group, rows = G + (app ? 2 : 0);
+    const bf16_t *row = a.qkv + (size_t)b * a.row_stride;
+#pragma unroll
+    for (int ps = 0; ps < DEC_ROW_PASSES; ps++) {
+        const int ri = 8 * ps + (lane >> 3);
+        int head = ri < G ? h * G + ri : (ri == G ? a.hq + h : a.hq + a.hkv + h);
+        if (ri >= rows) head = h * G; /* unused rows read a valid one */
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(row + (size_t)head * NC_HEAD_DIM);
+        rw.lo[ps] = src[g];
+        rw.hi[ps] = src[8 + g];
+    }
+    const f32x4 *qg = reinterpret_cast<const f32x4 *>(a.q_gain), *kg = reinterpret_cast<const f32x4 *>(a.k_gain);
+    const f32x4 *cp = reinterpret_cast<const f32x4 *>(a.cos + (size_t)p * NC_HALF);
+    const f32x4 *sp = reinterpret_cast<const f32x4 *>(a.sin + (size_t)p * NC_HALF);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        rw.qg[i] = qg[2 * g + i];
+        rw.qg[2 + i] = qg[16 + 2 * g + i];
+        rw.kg[i] = kg[2 * g + i];
+        rw.kg[2 + i] = kg[16 + 2 * g + i];
+        rw.cs[i] = cp[2 * g + i];
+        rw.sn[i] = sp[2 * g + i];
+    }
+    /* the new key's block: the table entry is loaded without a branch (from ctx_len when there is no table) so
+     * that its wait lands in build_rows, after the first pages' loads; p < max_ctx keeps the page in the table */
+    const size_t at = (size_t)b * a.max_blocks + p / NC_PAGE;
+    rw.blk = *(a.block_table ? a.block_table + at : a.ctx_len); /* no table: replaced by `at` in build_rows */
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const u32x4 u, float *v) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(u[i] << 16);
+        v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+}
+
+/* Norm, gain and rotate the piece's q rows (k_append's row math, so bit-identical to its q_out) into this lane's
+ * MFMA operand (head n, dims 32 j..) through LDS. A piece that appends also quantises the new key and value
+ * into LDS, for its last page and for store_new_kv. */
+__device__ __forceinline__ void build_rows(const DecodeArgs &a, int b, int h, int p, bool app, const Rows &rw, int lane,
+                                           bf16x8 *qop, StepLds &sm) {
+    const int g = lane & 7, G = a.group, rows = G + (app ? 2 : 0);
+    float c[8], s[8], qg1[8], qg2[8], kg1[8], kg2[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        c[e] = rw.cs[e / 4][e % 4];
+        s[e] = rw.sn[e / 4][e % 4];
+        qg1[e] = rw.qg[e / 4][e % 4];
+        qg2[e] = rw.qg[2 + e / 4][e % 4];
+        kg1[e] = rw.kg[e / 4][e % 4];
+        kg2[e] = rw.kg[2 + e / 4][e % 4];
+    }
+    __syncthreads(); /* the previous piece's reads of sm are done */
+#pragma unroll
+    for (int ps = 0; ps < DEC_ROW_PASSES; ps++) {
+        if (8 * ps >= rows) break;
+        const int ri = 8 * ps + (lane >> 3);
+        if (ri >= rows) continue; /* whole 8-lane rows: the row reductions stay inside active lanes */
+        float x1[8], x2[8];
+        unpack_bf16x8(rw.lo[ps], x1);
+        unpack_bf16x8(rw.hi[ps], x2);
+        if (ri <= G) {
+            float g1[8], g2[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                g1[e] = ri < G ? qg1[e] : kg1[e];
+                g2[e] = ri < G ? qg2[e] : kg2[e];
+            }
+            row_norm_rope(x1, x2, g1, g2, c, s);
+        }
+        if (ri < G) {
+            store_bf16x8(&sm.q[ri][8 * g], x1);
+            store_bf16x8(&sm.q[ri][NC_HALF + 8 * g], x2);
+            continue;
+        }
+        const int is_v = ri > G;
+        uint64_t c1, c2;
+        const float scale = row_quantize(x1, x2, &c1, &c2);
+        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][8 * g]) = c1;
+        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][NC_HALF + 8 * g]) = c2;
+        if (g == 0) sm.scale[is_v] = scale;
+        if (g == 0 && !is_v) {
+            const int blk = a.block_table ? rw.blk : b * a.max_blocks + p / NC_PAGE;
+            sm.blk = (blk >= 0 && blk < a.num_blocks) ? blk : -1;
+        }
+    }
+    __syncthreads();
     const int n = lane & 15, j = lane >> 4;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++)
+        qop[cc] = n < G ? *reinterpret_cast<const bf16x8 *>(&sm.q[n][32 * j + 8 * cc])
+                        : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+}
+
+/* The fused step's cache write of the new key and value (codes and scales from LDS, the bytes k_append writes),
+ * after the piece: nothing in this kernel reads them from memory (the piece used them from LDS), and stores
+ * issued before page loads would hold up those loads' waits (the memory counter completes in order). Lane l
+ * writes dims 2l and 2l + 1. */
+__device__ __forceinline__ void store_new_kv(const DecodeArgs &a, int h, int p, int lane, const StepLds &sm) {
+    const int blk = sm.blk, t = p % NC_PAGE;
+    if (blk < 0) return;
+    uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
+    const int d = 2 * lane;
+    *reinterpret_cast<uint16_t *>(tile + t * NC_HEAD_DIM + d) = *reinterpret_cast<const uint16_t *>(&sm.codes[0][d]);
+    tile[v_byte(t, d)] = sm.codes[1][d];
+    tile[v_byte(t, d + 1)] = sm.codes[1][d + 1];
+    if (lane < 2) reinterpret_cast<float *>(tile + (lane ? NC_TILE_VS : NC_TILE_KS))[t] = sm.scale[lane];
+}
+
+/* The pages [pg_lo, pg_lo + npg) of segment (b, h), DEC_DEPTH buffers in rotation: DEC_DEPTH - 1 pages are in
+ * flight while one is computed. The fused step builds q (and the append) while the first pages are in flight. */
+template <bool FUSED>
+__device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
+                                           bool app, bf16x8 *qop, int lane, StepLds &sm, State &st) {
+    const int n = lane & 15, j = lane >> 4;
+    const int patch_t = FUSED && app ? sr.p % NC_PAGE : -1;
     for (int win = 0; win < npg; win += 64) {
         const int nw = min(64, npg - win);
         const int base = pg_lo + win;
+        /* the fused step's rows first: they arrive with the block ids, and are used while the first pages load */
+        Rows rw;
+        if (FUSED && win == 0) {
+            load_rows(a, b, h, sr.p, app, lane, rw);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         /* lane i holds the block of page base + i */
         const int ids = lane < nw ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, b, base + lane) : -1;
         const int last = __builtin_amdgcn_readfirstlane(nw - 1);
@@ -239,6 +449,10 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
             load_page(a, __builtin_amdgcn_readlane(ids, min(i, last)), h, n, j, r[i]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (FUSED && win == 0) {
+            build_rows(a, b, h, sr.p, app, rw, lane, qop, sm);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         /* sched_barrier keeps each reload after the math that frees its buffer: with the live ranges apart the
          * buffers keep their registers across iterations (no copies of in-flight loads, no vmcnt(0)). Loads are
          * unconditional (clamped to the last page) so the counted waits stay exact. */
@@ -248,7 +462,7 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
                 load_page(a, __builtin_amdgcn_readlane(ids, min(k + u + DEC_DEPTH - 1, last)), h, n, j,
                           r[(u + DEC_DEPTH - 1) % DEC_DEPTH]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (u == 0 || k + u < nw) attend_page(a, r[u], base + k + u, sr, qop, j, st);
+                if (u == 0 || k + u < nw) attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -294,14 +508,17 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, bool whol
 }
 
 /* Pages per wave of the balanced schedule: every wave of k_decode and k_merge derives the same value from the
- * live context lengths. Writes the empty sequences' zero rows when zero_rows (sequence b by wave b % W). */
+ * live context lengths. When zero_rows (k_decode), wave b % W writes sequence b's row if it is empty (zeros, or
+ * NaN for the fused step's positions out of range) and its next position to pos_out. */
 __device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane, bool zero_rows) {
     long long total = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int b = base + lane;
-        const int pg = b < a.B ? seq_pages(a, b) : 0;
+        const int pg = b < a.B ? seq_units(a, b) : 0;
+        if (zero_rows && a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
         if (zero_rows && b < a.B && pg == 0 && b % W == w) {
-            const u32x4 z = {0u, 0u, 0u, 0u};
+            const uint32_t f = seq_ctx(a, b) < 0 ? 0x7fc07fc0u : 0u;
+            const u32x4 z = {f, f, f, f};
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
                 reinterpret_cast<u32x4 *>(a.out + (size_t)b * a.hq * NC_HEAD_DIM)[r] = z;
         }
@@ -310,7 +527,9 @@ __device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane,
     return total * a.hkv;
 }
 
+template <bool FUSED>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
+    __shared__ StepLds sm;
     const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
 
     const long long total = schedule_total(a, w, W, lane, true);
@@ -319,46 +538,53 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     if (start >= total) return;
     long long remaining = min(chunk, total - start);
 
-    /* the segment holding `start`: sequence b0, then kv head and page offset */
+    /* the segment holding `start`: sequence b0, then kv head and unit offset */
     long long carry = 0;
-    int b = -1, pages_b = 0;
+    int b = -1, units_b = 0;
     for (int base = 0; base < a.B && b < 0; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < a.B ? seq_pages(a, bb) : 0;
+        const int pg = bb < a.B ? seq_units(a, bb) : 0;
         const int incl = wave_inclusive_sum(pg, lane);
         const unsigned long long hit = __ballot(bb < a.B && carry + (long long)incl * a.hkv > start);
         if (hit) {
             const int first = __builtin_ctzll(hit);
             b = base + first;
-            pages_b = __shfl(pg, first, 64);
+            units_b = __shfl(pg, first, 64);
             carry += (long long)__shfl(incl - pg, first, 64) * a.hkv;
         } else {
             carry += (long long)__shfl(incl, 63, 64) * a.hkv;
         }
     }
     const long long into = start - carry; /* flattened offset inside sequence b */
-    int h = (int)(into / pages_b), off = (int)(into % pages_b);
+    int h = (int)(into / units_b), off = (int)(into % units_b);
 
     while (remaining > 0) {
         const SeqRange sr = seq_range(a, b);
         const int seg_pages = sr.last - sr.first + 1;
-        const int len = (int)min((long long)(seg_pages - off), remaining);
-        bf16x8 qop[4];
-        if (n < a.group) {
-            const u32x4 *qp = reinterpret_cast<const u32x4 *>(a.q + ((size_t)b * a.hq + h * a.group + n) *
-                                                             NC_HEAD_DIM + j * 32);
-#pragma unroll
-            for (int c = 0; c < 4; c++) qop[c] = __builtin_bit_cast(bf16x8, qp[c]);
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++) qop[c] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-        }
-        State st;
-        state_init(st);
-        attend_run(a, b, h, sr.first + off, len, sr, qop, lane, st);
-        finish_piece(a, b, h, w, off == 0 && len == seg_pages, lane, st);
-        remaining -= len;
+        /* this slice takes units [off, off + take) of the segment; its pages are [lo, hi) */
+        const int take = (int)min((long long)(seg_pages + a.unit_start + a.unit_end - off), remaining);
+        const int lo = max(off - a.unit_start, 0), hi = min(off + take - a.unit_start, seg_pages);
+        remaining -= take;
         off = 0;
+        if (hi > lo) {
+            bf16x8 qop[4]; /* the fused step builds it in attend_run */
+            if constexpr (!FUSED) {
+                if (n < a.group) {
+                    const u32x4 *qp = reinterpret_cast<const u32x4 *>(
+                        a.q + ((size_t)b * a.hq + h * a.group + n) * NC_HEAD_DIM + j * 32);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) qop[c] = __builtin_bit_cast(bf16x8, qp[c]);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) qop[c] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+                }
+            }
+            State st;
+            state_init(st);
+            attend_run<FUSED>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
+            finish_piece(a, b, h, w, lo == 0 && hi == seg_pages, lane, st);
+            if (FUSED && hi == seg_pages) store_new_kv(a, h, sr.p, lane, sm);
+        }
         if (++h == a.hkv) {
             h = 0;
             do {
@@ -376,19 +602,21 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
  * results are loaded 4 at a time, every load of a batch in flight together. */
 __global__ void __launch_bounds__(DEC_THREADS) k_merge(DecodeArgs a, int W) {
     const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
-    long long total = 0, before = 0; /* pages of every sequence, of the sequences before b */
-    int pages = 0;
+    long long total = 0, before = 0; /* units of every sequence, of the sequences before b */
+    int units = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < a.B ? seq_pages(a, bb) : 0;
+        const int pg = bb < a.B ? seq_units(a, bb) : 0;
         total += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
         before += __shfl(wave_inclusive_sum(bb < b ? pg : 0, lane), 63, 64);
-        if (b >= base && b < base + 64) pages = __shfl(pg, b - base, 64);
+        if (b >= base && b < base + 64) units = __shfl(pg, b - base, 64);
     }
-    if (pages <= 0) return;
+    if (units <= 0) return;
     total *= a.hkv;
     const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
-    const long long seg_lo = before * a.hkv + (long long)h * pages, seg_hi = seg_lo + pages;
+    /* the segment's pages in schedule units */
+    const long long seg_lo = before * a.hkv + (long long)h * units + a.unit_start;
+    const long long seg_hi = seg_lo + units - a.unit_start - a.unit_end;
     const int w_first = (int)(seg_lo / chunk), w_last = (int)((seg_hi - 1) / chunk);
     if (w_first == w_last || n >= a.group) return; /* one piece: k_decode wrote the output */
     float mmax = DEC_M_INIT, sum = 0.f, acc[32];
@@ -438,7 +666,10 @@ static int decode_waves() {
     if (dev < 0 || dev >= 64) dev = 0;
     if (!cached[dev]) {
         int per_cu = 0, cus = 0;
-        NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode, DEC_THREADS, 0));
+        int per_cu_fused = 0;
+        NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<false>, DEC_THREADS, 0));
+        NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_fused, k_decode<true>, DEC_THREADS, 0));
+        if (per_cu_fused < per_cu) per_cu = per_cu_fused; /* one grid size for both: the same schedule */
         NC_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         /* CDNA: 4 SIMDs per CU. Resident waves beyond DEC_WAVES_PER_SIMD per SIMD are not used: a second wave on
          * a SIMD loses issue arbitration to the older one and finishes its equal share last. */
@@ -453,10 +684,61 @@ static int decode_waves() {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+/* Schedule units (page equivalents) a segment costs besides its pages: starting a piece there, and ending it.
+ * NC_DECODE_UNITS="start,end" overrides them (a tuning knob, read once per process). */
+static void schedule_units(int *start, int *end) {
+    static int s = -1, e = 0;
+    if (s < 0) {
+        int v[2] = {DEC_UNITS_START, DEC_UNITS_END};
+        const char *env = getenv("NC_DECODE_UNITS");
+        if (env) sscanf(env, "%d,%d", &v[0], &v[1]);
+        e = v[1] < 0 ? 0 : v[1];
+        s = v[0] < 0 ? 0 : v[0];
+    }
+    *start = s;
+    *end = e;
+}
+
 extern "C" long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx) {
     if (B <= 0 || hq <= 0 || hkv <= 0 || max_ctx <= 0 || hq % hkv) return 0;
     const size_t S = (size_t)B * hkv, G = hq / hkv, slots = DEC_MAX_WAVES + S;
     return (long long)(align256(slots * G * NC_HEAD_DIM * sizeof(float)) + slots * G * 2 * sizeof(float));
+}
+
+/* Checks shared by both entry points, then the launch of k_decode<FUSED> and k_merge. */
+static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void *workspace, long long workspace_bytes,
+                         int max_ctx, float sm_scale, void *stream) {
+    const int B = a.B, hq = a.hq, hkv = a.hkv;
+    NC_REQUIRE(hkv > 0 && hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
+    NC_REQUIRE(hq / hkv <= DEC_MAX_G, "hq / hkv = %d exceeds %d query heads per kv head", hq / hkv, DEC_MAX_G);
+    NC_REQUIRE(a.max_blocks > 0 && a.num_blocks > 0, "max_blocks %d, num_blocks %d must be positive", a.max_blocks,
+               a.num_blocks);
+    NC_REQUIRE(a.block_table || (long long)B * a.max_blocks <= a.num_blocks,
+               "contiguous cache: %d sequences x %d blocks exceed the %d blocks", B, a.max_blocks, a.num_blocks);
+    NC_REQUIRE(max_ctx > 0 && max_ctx <= a.max_blocks * NC_PAGE, "max_ctx %d outside [1, %d]", max_ctx,
+               a.max_blocks * NC_PAGE);
+    NC_REQUIRE(a.cache && a.ctx_len && out && workspace, "null argument");
+    NC_REQUIRE(((uintptr_t)out | (uintptr_t)a.cache | (uintptr_t)workspace) % 16 == 0,
+               "tensors must be 16-byte aligned");
+    const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
+    NC_REQUIRE(workspace_bytes >= need, "workspace %lld bytes, %lld needed", workspace_bytes, need);
+    a.group = hq / hkv;
+    a.score_scale = sm_scale * 1.4426950408889634f;
+    a.out = (bf16_t *)out;
+    a.max_ctx = max_ctx;
+    const size_t S = (size_t)B * hkv, slots = DEC_MAX_WAVES + S;
+    a.ws_o = (float *)workspace;
+    a.ws_ml = (float *)((unsigned char *)workspace + align256(slots * a.group * NC_HEAD_DIM * sizeof(float)));
+    schedule_units(&a.unit_start, &a.unit_end);
+    const int W = decode_waves();
+    if (fused)
+        hipLaunchKernelGGL(k_decode<true>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(k_decode<false>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
+    NC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(DEC_THREADS), 0, (hipStream_t)stream, a, W);
+    NC_LAUNCH_CHECK();
+    return 0;
 }
 
 extern "C" int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int32_t *block_table, int max_blocks,
@@ -465,33 +747,39 @@ extern "C" int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int
                                   void *stream) {
     NC_REQUIRE(B >= 0, "B = %d < 0", B);
     if (B == 0) return 0;
-    NC_REQUIRE(hkv > 0 && hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
-    NC_REQUIRE(hq / hkv <= DEC_MAX_G, "hq / hkv = %d exceeds %d query heads per kv head", hq / hkv, DEC_MAX_G);
-    NC_REQUIRE(max_blocks > 0 && num_blocks > 0, "max_blocks %d, num_blocks %d must be positive", max_blocks,
-               num_blocks);
-    NC_REQUIRE(block_table || (long long)B * max_blocks <= num_blocks,
-               "contiguous cache: %d sequences x %d blocks exceed the %d blocks", B, max_blocks, num_blocks);
-    NC_REQUIRE(max_ctx > 0 && max_ctx <= max_blocks * NC_PAGE, "max_ctx %d outside [1, %d]", max_ctx,
-               max_blocks * NC_PAGE);
-    NC_REQUIRE(q && cache && ctx_len && out && workspace, "null argument");
-    NC_REQUIRE(((uintptr_t)q | (uintptr_t)out | (uintptr_t)cache | (uintptr_t)workspace) % 16 == 0,
-               "tensors must be 16-byte aligned");
-    const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
-    NC_REQUIRE(workspace_bytes >= need, "workspace %lld bytes, %lld needed", workspace_bytes, need);
+    NC_REQUIRE(q && (uintptr_t)q % 16 == 0, "q must be a 16-byte aligned pointer");
     DecodeArgs a = {};
-    a.q = (const bf16_t *)q; a.cache = cache;
+    a.q = (const bf16_t *)q; a.cache = const_cast<uint8_t *>(cache); /* not written without qkv */
     a.block_table = block_table; a.max_blocks = max_blocks; a.num_blocks = num_blocks; a.ctx_len = ctx_len;
-    a.window = window; a.B = B; a.hq = hq; a.hkv = hkv; a.group = hq / hkv;
-    a.score_scale = sm_scale * 1.4426950408889634f;
-    a.out = (bf16_t *)out;
-    a.max_ctx = max_ctx;
-    const size_t S = (size_t)B * hkv, slots = DEC_MAX_WAVES + S;
-    a.ws_o = (float *)workspace;
-    a.ws_ml = (float *)((unsigned char *)workspace + align256(slots * a.group * NC_HEAD_DIM * sizeof(float)));
-    const int W = decode_waves();
-    hipLaunchKernelGGL(k_decode, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
-    NC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(DEC_THREADS), 0, (hipStream_t)stream, a, W);
-    NC_LAUNCH_CHECK();
-    return 0;
+    a.window = window; a.B = B; a.hq = hq; a.hkv = hkv;
+    return decode_launch(a, false, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
+}
+
+extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                                  const float *q_gain,
+                                  const float *k_gain, const float *cos, const float *sin, int rope_len,
+                                  uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks,
+                                  int window, int B, int hq, int hkv, int max_ctx, float sm_scale, void *out,
+                                  void *workspace, long long workspace_bytes, void *stream) {
+    NC_REQUIRE(B >= 0, "B = %d < 0", B);
+    if (B == 0) return 0;
+    NC_REQUIRE(hkv > 0 && hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
+    NC_REQUIRE(row_stride >= (long long)(hq + 2 * hkv) * NC_HEAD_DIM && row_stride % 8 == 0,
+               "row_stride %lld must hold (hq + 2 hkv) * 128 elements and keep 16-byte alignment", row_stride);
+    NC_REQUIRE(rope_len > 0, "rope_len = %d", rope_len);
+    NC_REQUIRE(qkv && pos && q_gain && k_gain && cos && sin, "null argument");
+    NC_REQUIRE(((uintptr_t)qkv | (uintptr_t)q_gain | (uintptr_t)k_gain | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0,
+               "qkv, gains and rotary tables must be 16-byte aligned");
+    const char *o = (const char *)out, *x = (const char *)qkv;
+    NC_REQUIRE(!out || o + (size_t)B * hq * NC_HEAD_DIM * 2 <= x || x + (size_t)B * row_stride * 2 <= o,
+               "out must not overlap qkv");
+    NC_REQUIRE(!pos_out || pos_out + B <= pos || pos + B <= pos_out, "pos_out must not overlap pos");
+    DecodeArgs a = {};
+    a.cache = cache;
+    a.block_table = block_table; a.max_blocks = max_blocks; a.num_blocks = num_blocks; a.ctx_len = pos;
+    a.pos_out = pos_out;
+    a.qkv = (const bf16_t *)qkv; a.row_stride = row_stride; a.q_gain = q_gain; a.k_gain = k_gain;
+    a.cos = cos; a.sin = sin; a.rope_len = rope_len;
+    a.window = window; a.B = B; a.hq = hq; a.hkv = hkv;
+    return decode_launch(a, true, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
 }

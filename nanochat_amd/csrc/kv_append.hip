@@ -35,21 +35,6 @@ extern "C" const char *nc_last_error(void) { return nc_error; }
 
 extern "C" int nc_abi_version(void) { return 1; }
 
-/* Write this lane's 16 codes of a quantised row into the tile's K region (row-major) or V region
- * (quad-transposed). */
-__device__ __forceinline__ void write_codes(uint8_t *tile, int t, int g, uint64_t c1, uint64_t c2, bool is_v) {
-    if (!is_v) {
-        *reinterpret_cast<uint64_t *>(tile + t * NC_HEAD_DIM + 8 * g) = c1;
-        *reinterpret_cast<uint64_t *>(tile + t * NC_HEAD_DIM + NC_HALF + 8 * g) = c2;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            tile[v_byte(t, 8 * g + e)] = (uint8_t)(c1 >> (8 * e));
-            tile[v_byte(t, NC_HALF + 8 * g + e)] = (uint8_t)(c2 >> (8 * e));
-        }
-    }
-}
-
 struct AppendArgs {
     const bf16_t *qkv;        /* fused mode: [n][row_stride], q heads then k heads then v heads */
     const bf16_t *k_rows;     /* store mode: [n][row_stride] kv heads */

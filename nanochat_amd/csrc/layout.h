@@ -42,3 +42,18 @@ __device__ __forceinline__ int lookup_block(const int32_t *block_table, int max_
     const int blk = block_table ? block_table[(size_t)seq * max_blocks + page] : seq * max_blocks + page;
     return (blk >= 0 && blk < num_blocks) ? blk : -1;
 }
+
+/* Write this lane's 16 codes of a quantised row into the tile's K region (row-major) or V region
+ * (quad-transposed). */
+__device__ __forceinline__ void write_codes(uint8_t *tile, int t, int g, uint64_t c1, uint64_t c2, bool is_v) {
+    if (!is_v) {
+        *reinterpret_cast<uint64_t *>(tile + t * NC_HEAD_DIM + 8 * g) = c1;
+        *reinterpret_cast<uint64_t *>(tile + t * NC_HEAD_DIM + NC_HALF + 8 * g) = c2;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            tile[v_byte(t, 8 * g + e)] = (uint8_t)(c1 >> (8 * e));
+            tile[v_byte(t, NC_HALF + 8 * g + e)] = (uint8_t)(c2 >> (8 * e));
+        }
+    }
+}

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple] = {
     "nc_kv_gather_fp8": (I32, [P, P, I32, I32, P, I32, I32, I32, P, P, P, P, P]),
     "nc_decode_workspace_bytes": (I64, [I32, I32, I32, I32]),
     "nc_decode_attn_fp8": (I32, [P, P, P, I32, I32, P, I32, I32, I32, I32, I32, F32, P, P, I64, P]),
+    "nc_decode_step_fp8": (I32, [P, I64, P, P, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P,
+                                 P, I64, P]),
     "nc_prefill_attn_fp8": (I32, [P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, F32, P, P]),
     "nc_argmax_f32": (I32, [P, I32, I32, I64, P, P]),
     "nc_add_rms_norm_bf16": (I32, [P, P, P, P, I32, I32, P]),

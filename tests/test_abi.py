@@ -60,6 +60,36 @@ def test_decode_rejects_bad_arguments(kwargs, message):
     assert message in lib.nc_last_error().decode()
 
 
+def test_decode_step_rejects_bad_arguments():
+    lib = native.hip_library()
+    qkv, out = 0x10000, 0x100000
+    #       qkv                     row_stride pos   pos_out q_gain k_gain cos sin rope cache table max_b blocks
+    base = [ctypes.c_void_p(qkv), 24 * 128, FAKE, NULL, FAKE, FAKE, FAKE, FAKE, 4096, FAKE, NULL, 512, 1 << 16,
+            # window B hq  hkv max_ctx scale out                    workspace bytes    stream
+            -1, 8, 16, 4, 4096, 0.08, ctypes.c_void_p(out), FAKE, 1 << 30, NULL]
+
+    def rejects(i, value, message):
+        args = list(base)
+        args[i] = value
+        assert lib.nc_decode_step_fp8(*args) < 0, (i, value)
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    rejects(1, 100, "row_stride")
+    rejects(15, 6, "multiple")
+    rejects(15, 64 * 4, "row_stride")  # the row no longer holds the heads
+    rejects(8, 0, "rope_len")
+    rejects(4, NULL, "null")
+    rejects(19, ctypes.c_void_p(qkv + 256), "overlap")
+    rejects(3, FAKE, "pos_out")  # pos_out on pos
+    rejects(17, 0, "max_ctx")
+    rejects(21, 0, "workspace")
+    rejects(12, 2, "contiguous")
+    rejects(0, ctypes.c_void_p(qkv + 8), "aligned")
+    empty = list(base)
+    empty[14] = 0
+    assert lib.nc_decode_step_fp8(*empty) == 0  # nothing to do, nothing launched
+
+
 def test_append_rejects_bad_arguments():
     lib = native.hip_library()
     base = [FAKE, 1024, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 16, 4, FAKE, FAKE, NULL, 8, 64, 8, NULL, NULL]
