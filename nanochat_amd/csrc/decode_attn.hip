@@ -108,9 +108,9 @@ __device__ __forceinline__ int seq_ctx(const DecodeArgs &a, int b) {
     return (v >= a.max_ctx || v >= a.rope_len) ? -1 : v + 1;
 }
 
-__device__ __forceinline__ SeqRange seq_range(const DecodeArgs &a, int b) {
+/* The key range of a sequence of context length ctx (seq_ctx). */
+__device__ __forceinline__ SeqRange seq_range_of(const DecodeArgs &a, int ctx) {
     SeqRange r;
-    const int ctx = seq_ctx(a, b);
     if (ctx <= 0) {
         r.first = 0, r.last = -1, r.begin = 0, r.p = -1;
         return r;
@@ -122,17 +122,25 @@ __device__ __forceinline__ SeqRange seq_range(const DecodeArgs &a, int b) {
     return r;
 }
 
-__device__ __forceinline__ int seq_pages(const DecodeArgs &a, int b) {
-    const SeqRange r = seq_range(a, b);
+__device__ __forceinline__ int pages_of(const DecodeArgs &a, int ctx) {
+    const SeqRange r = seq_range_of(a, ctx);
     return r.last - r.first + 1;
 }
 
-/* Schedule units of one segment of sequence b: its pages plus the fixed costs of starting a piece there and of
- * ending the segment (the fused step's append), in page equivalents, so that the waves that carry them get fewer
- * pages; an empty sequence costs nothing. */
-__device__ __forceinline__ int seq_units(const DecodeArgs &a, int b) {
-    const int pg = seq_pages(a, b);
+/* Schedule units of one segment of a sequence of context length ctx: its pages plus the fixed costs of starting a
+ * piece there and of ending the segment (the fused step's append), in page equivalents, so that the waves that
+ * carry them get fewer pages; an empty sequence costs nothing. */
+__device__ __forceinline__ int units_of(const DecodeArgs &a, int ctx) {
+    const int pg = pages_of(a, ctx);
     return pg > 0 ? pg + a.unit_start + a.unit_end : 0;
+}
+
+/* A k_decode wave's context lengths: seq_ctx of every sequence, in LDS when the batch fits (read from memory once
+ * per wave, in schedule_total), else from memory each time. */
+#define DEC_LDS_SEQS 2048
+
+__device__ __forceinline__ int ctx_at(const DecodeArgs &a, const int *lds, int b) {
+    return lds ? lds[b] : seq_ctx(a, b);
 }
 
 __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
@@ -507,17 +515,20 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, bool whol
     }
 }
 
-/* Pages per wave of the balanced schedule: every wave of k_decode and k_merge derives the same value from the
- * live context lengths. When zero_rows (k_decode), wave b % W writes sequence b's row if it is empty (zeros, or
- * NaN for the fused step's positions out of range) and its next position to pos_out. */
-__device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane, bool zero_rows) {
+/* Schedule units of the whole batch: every wave of k_decode and k_merge derives the same value from the live
+ * context lengths. k_decode (zero_rows) also keeps them in lds (if not null), and wave b % W writes sequence b's
+ * row if it is empty (zeros, or NaN for the fused step's positions out of range) and its next position to
+ * pos_out. */
+__device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane, bool zero_rows, int *lds) {
     long long total = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int b = base + lane;
-        const int pg = b < a.B ? seq_units(a, b) : 0;
+        const int c = b < a.B ? seq_ctx(a, b) : 0;
+        const int pg = units_of(a, c);
+        if (lds && b < a.B) lds[b] = c;
         if (zero_rows && a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
         if (zero_rows && b < a.B && pg == 0 && b % W == w) {
-            const uint32_t f = seq_ctx(a, b) < 0 ? 0x7fc07fc0u : 0u;
+            const uint32_t f = c < 0 ? 0x7fc07fc0u : 0u;
             const u32x4 z = {f, f, f, f};
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
                 reinterpret_cast<u32x4 *>(a.out + (size_t)b * a.hq * NC_HEAD_DIM)[r] = z;
@@ -530,9 +541,12 @@ __device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane,
 template <bool FUSED>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     __shared__ StepLds sm;
+    __shared__ int ctx_lds[DEC_LDS_SEQS];
     const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
+    int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
 
-    const long long total = schedule_total(a, w, W, lane, true);
+    const long long total = schedule_total(a, w, W, lane, true, lds);
+    __syncthreads(); /* lds complete before other lanes' reads */
     const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
     const long long start = (long long)w * chunk;
     if (start >= total) return;
@@ -543,7 +557,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     int b = -1, units_b = 0;
     for (int base = 0; base < a.B && b < 0; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < a.B ? seq_units(a, bb) : 0;
+        const int pg = bb < a.B ? units_of(a, ctx_at(a, lds, bb)) : 0;
         const int incl = wave_inclusive_sum(pg, lane);
         const unsigned long long hit = __ballot(bb < a.B && carry + (long long)incl * a.hkv > start);
         if (hit) {
@@ -559,7 +573,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     int h = (int)(into / units_b), off = (int)(into % units_b);
 
     while (remaining > 0) {
-        const SeqRange sr = seq_range(a, b);
+        const SeqRange sr = seq_range_of(a, ctx_at(a, lds, b));
         const int seg_pages = sr.last - sr.first + 1;
         /* this slice takes units [off, off + take) of the segment; its pages are [lo, hi) */
         const int take = (int)min((long long)(seg_pages + a.unit_start + a.unit_end - off), remaining);
@@ -589,7 +603,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             h = 0;
             do {
                 b++;
-            } while (remaining > 0 && b < a.B && seq_pages(a, b) == 0);
+            } while (remaining > 0 && b < a.B && pages_of(a, ctx_at(a, lds, b)) == 0);
             if (b >= a.B) break;
         }
     }
@@ -606,7 +620,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_merge(DecodeArgs a, int W) {
     int units = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < a.B ? seq_units(a, bb) : 0;
+        const int pg = bb < a.B ? units_of(a, seq_ctx(a, bb)) : 0;
         total += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
         before += __shfl(wave_inclusive_sum(bb < b ? pg : 0, lane), 63, 64);
         if (b >= base && b < base + 64) units = __shfl(pg, b - base, 64);

@@ -56,6 +56,7 @@ def test_config3_ragged_gqa_paged_full_size(gpu):
     DecodeConfig("g16-one-kv-head", 3, 16, 1, ctx=(0, 31, 2047), paged=True, seed=63),
     DecodeConfig("page-multiples", 6, 4, 4, ctx=(15, 16, 31, 32, 63, 64), seed=64),
     DecodeConfig("long-single-seq", 1, 4, 1, ctx=(30000,), paged=True, outliers=0.01, seed=65),
+    DecodeConfig("batch-past-lds-cache", 2100, 2, 1, ctx_range=(0, 60), seed=66),
 ])
 def test_decode_edge_shapes(gpu, cfg):
     run_and_check(cfg, gpu)
