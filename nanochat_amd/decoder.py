@@ -13,8 +13,8 @@ on ties, nc_argmax_f32). The decode step's weight GEMMs are this package's slot 
 reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
 per-row rstd, ReLU^2 into the up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
 through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
-attention and the token choice are HIP kernels throughout; the decode step is captured once in a hipGraph and
-replayed.
+attention and the token choice are HIP kernels throughout (a decode step's append and attention are one
+nc_decode_step_fp8 call per layer); the decode step is captured once in a hipGraph and replayed.
 
 The architecture is BASELINE config 5's: RoPE, QK-norm, ReLU^2 MLP at 4x, untied embeddings, bf16 weights
 N(0, 0.02), full causal attention in every layer. The reference's training-time extras that this config does not
@@ -30,7 +30,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from nanochat_amd.attention import decode_attention, decode_workspace, prefill_attention
+from nanochat_amd.attention import decode_step, decode_workspace, prefill_attention
 from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
 from nanochat_amd.native import check, hip_library, pointer, stream
 from nanochat_amd.rotary import rotary_tables
@@ -210,13 +210,12 @@ class Fp8Decoder:
         Returns the fp32 logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and
         attention; x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
         x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
-        ctx = pos + 1
         for l in range(self.cfg.layers):
             lw = self.model.layers[l]
             qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
-            q = self.caches[l].append(qkv, pos, self.seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin,
-                                      self.cfg.heads)
-            o = decode_attention(q, self.caches[l], ctx, max_ctx=self.max_len, workspace=self.ws)
+            # the append (decode.cu:550-565) and attention in one call: sequence b is cache row b
+            o = decode_step(qkv, self.caches[l], pos, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
+                            max_ctx=self.max_len, workspace=self.ws)
             slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
             u = slot_gemm(x, lw["wup"], RELU2_NORM)
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
