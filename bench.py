@@ -69,12 +69,13 @@ def replay_ms(graph, n: int, stream) -> float:
     return start.elapsed_time(end) / n
 
 
-def traffic_bytes():
-    """HBM bytes per nc_decode_attn_fp8 call from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes, each scaled by what
-    the counter reads for a plain 1 GiB copy (written by the profiling run into TRAFFIC_FILE); None if absent."""
+def traffic_bytes(call: str):
+    """HBM bytes per `call` (nc_decode_step_fp8 or nc_decode_attn_fp8) from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes, each scaled by what the counter reads for a plain 1 GiB copy (TRAFFIC_FILE, written from the profiling
+    runs); None if absent."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f)["bytes_per_call"]
+            return json.load(f)[call]["bytes_per_call"]
     except (OSError, KeyError, ValueError):
         return None
 
@@ -338,7 +339,8 @@ def main():
         "step_us": round(step_ms * 1e3, 3),
         "wall_s_timed": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_bytes("nc_decode_attn_fp8" if args.unfused else "nc_decode_step_fp8"),
                      "kernel": call_kernel, "bytes_per_launch": int(call_bytes)},
     }
     if not args.no_extra:
