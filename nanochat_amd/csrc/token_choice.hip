@@ -1,5 +1,7 @@
 /*
- * Greedy token choice: per row, the column of the largest fp32 logit, the lowest column among exact ties
+ * Token choice of a decode step's slots.
+ *
+ * nc_argmax_f32, greedy: per row, the column of the largest fp32 logit, the lowest column among exact ties
  * (reference: the packed-key argmax of the slot GEMM's EPI_ARGMAX epilogue, model/kernels/decode.cu:90-96,189-230).
  *
  * The key of a (score, column) pair is the score's IEEE bits mapped to an unsigned order (negatives inverted,
@@ -55,6 +57,248 @@ extern "C" int nc_argmax_f32(const float *logits, int rows, int cols, long long 
     if (rows == 0) return 0;
     NC_REQUIRE(logits && out, "nc_argmax_f32: null pointer");
     hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(TC_THREADS), 0, (hipStream_t)stream, logits, cols, ld, out);
+    NC_LAUNCH_CHECK();
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ sampling head */
+/*
+ * nc_choose_tokens: every active slot's next token by its temperature, top_p, seed and (for a masked slot) its
+ * allowed rows, then the commit (reference: the ARGMAX epilogue with CHOICE, k_nucleus and k_commit,
+ * model/kernels/decode.cu:170-230,360-404,676-689; host rules inference/decoder.py:28-40):
+ *   T == 0     the largest raw logit over the allowed rows (lowest row on ties);
+ *   T > 0      Gumbel-max: the largest z / T + g(seed, pos - first, row), z = c tanh(s / c) (c <= 0: z = s), which
+ *              samples softmax(z / T) (arXiv 1411.0030 §2);
+ *   top_p < 1  (T > 0) nucleus (arXiv 1904.09751 §3.1): e = exp(z / T - max), keep e >= e*, e* the least e with
+ *              sum(e' <= e*) > (1 - top_p) sum(e) (bisection on the IEEE bits of e* in [0, 1], fp32 sums in a fixed
+ *              order), then Gumbel-max over the kept rows;
+ *   alt        the best allowed row but `lazy` (none for a nucleus slot), for a host that rejects the lazy row;
+ *   commit     tokens = the choice's row (-1: no allowed row), alt_tokens likewise, pos += 1.
+ * The noise: Philox4x32-10 (Salmon et al., SC '11: "Parallel random numbers: as easy as 1, 2, 3") at counter
+ * (row, i, 0, 0) and key (seed low, seed high); the top 52 bits r of its first two words give u = (2r + 1) 2^-53,
+ * g = float(-log(-log(u))) in double (decode.cu:98-105's transform).
+ *
+ * k_choose: a grid of B x P workgroups of 512 threads; workgroup (b, p) scans rows [p L, (p + 1) L) of slot b and
+ * writes its best and alternative keys to the workspace. A nucleus slot needs whole-row reductions: its workgroup
+ * p = 0 does all of it (the probabilities go to the workspace), the others write empty keys. k_commit then folds
+ * each slot's P keys and commits. Sampling is ALU-bound (10 Philox rounds and two double logs per row); greedy is
+ * HBM-bound on 4 B per logit.
+ */
+
+#define CH_THREADS 512
+#define CH_WAVES (CH_THREADS / NC_WAVE)
+#define CH_ROWS_PER_THREAD 16 /* rows a thread scans on the non-nucleus paths: P = ceil(vocab / (512 x 16)) */
+#define CH_MAX_PARTS 64
+
+struct ChooseArgs {
+    const float *logits;
+    long long ld;
+    int B, vocab, parts, span;               /* workgroups per slot, rows per workgroup */
+    const unsigned long long *active;        /* [2][words]: active slots, then masked slots; null: all, none */
+    int words;
+    const uint32_t *allow;                   /* [B][allow_words]: a masked slot's allowed rows */
+    int allow_words;
+    const float *temperature, *top_p;        /* [B] */
+    const unsigned long long *seed;          /* [B] */
+    const int32_t *first;                    /* [B] */
+    int32_t *pos;                            /* [B]: the input's position; += 1 by the commit */
+    float softcap;
+    int lazy;
+    unsigned long long *keys;                /* [B][parts][2]: best, alternative */
+    float *probs;                            /* [B][vocab]: a nucleus slot's e */
+    int32_t *tokens, *alt_tokens;            /* [B] */
+};
+
+__device__ __forceinline__ bool slot_bit(const unsigned long long *mask, int b) { return (mask[b >> 6] >> (b & 63)) & 1ull; }
+
+/* Philox4x32-10 (SC '11): (hi0, lo0) = M0 c0, (hi1, lo1) = M1 c2, c = (hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0); the key
+ * advances by the Weyl increments between rounds. Returns the first two output words. */
+__device__ __forceinline__ void philox_2(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0, uint32_t k1,
+                                         uint32_t &o0, uint32_t &o1) {
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+        const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+        const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0, c1 = lo1, c2 = n2, c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    o0 = c0;
+    o1 = c1;
+}
+
+__device__ __forceinline__ float gumbel_noise(unsigned long long seed, uint32_t i, uint32_t row) {
+    uint32_t x0, x1;
+    philox_2(row, i, 0u, 0u, (uint32_t)seed, (uint32_t)(seed >> 32), x0, x1);
+    const unsigned long long r = (((unsigned long long)x0 << 32) | x1) >> 12;
+    const double u = (2.0 * (double)r + 1.0) * 0x1p-53;
+    return (float)-log(-log(u));
+}
+
+__device__ __forceinline__ float capped(float s, float c) { return c > 0.f ? c * tanhf(s / c) : s; }
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int d) {
+    return ((unsigned long long)__shfl_xor((unsigned)(v >> 32), d, NC_WAVE) << 32) | __shfl_xor((unsigned)v, d, NC_WAVE);
+}
+
+/* Block reductions over CH_WAVES waves, result in every thread; fixed order (xor tree, then waves in order). */
+__device__ unsigned long long block_max_u64(unsigned long long v, unsigned long long *sh) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = max_u64(v, shfl_xor_u64(v, d));
+    __syncthreads();
+    if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
+    __syncthreads();
+    unsigned long long r = sh[0];
+    for (int w = 1; w < CH_WAVES; w++) r = max_u64(r, sh[w]);
+    return r;
+}
+
+__device__ float block_max_f32(float v, float *sh) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, shfl_xor_f(v, d));
+    __syncthreads();
+    if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int w = 1; w < CH_WAVES; w++) r = fmaxf(r, sh[w]);
+    return r;
+}
+
+__device__ float block_sum_f32(float v, float *sh) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = v + shfl_xor_f(v, d);
+    __syncthreads();
+    if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int w = 1; w < CH_WAVES; w++) r = r + sh[w];
+    return r;
+}
+
+__device__ __forceinline__ bool row_allowed(const uint32_t *allow, int r) { return !allow || ((allow[r >> 5] >> (r & 31)) & 1u); }
+
+/* A nucleus slot, one workgroup: e to the workspace, its sum, the bisection, then Gumbel-max over the kept rows. */
+__device__ unsigned long long nucleus_choice(const ChooseArgs &a, int b, const float *s, const uint32_t *allow, float T,
+                                             float P, uint32_t i, float *fsh, unsigned long long *ksh) {
+#pragma clang fp contract(off)
+    float *e = a.probs + (size_t)b * a.vocab; /* a thread reads back only the rows it wrote */
+    float m = -INFINITY;
+    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS)
+        if (row_allowed(allow, r)) m = fmaxf(m, capped(s[r], a.softcap) / T);
+    m = block_max_f32(m, fsh);
+    float sum = 0.f;
+    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS) {
+        const float ev = row_allowed(allow, r) ? expf(capped(s[r], a.softcap) / T - m) : 0.f;
+        e[r] = ev;
+        sum = sum + ev;
+    }
+    const float drop = (1.f - P) * block_sum_f32(sum, fsh);
+    uint32_t lo = 0u, hi = __float_as_uint(1.f); /* the least bits u with C(u) > drop; C(1) is the whole sum */
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        const float x = __uint_as_float(mid);
+        float below = 0.f;
+        for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS)
+            if (e[r] <= x) below = below + e[r];
+        if (block_sum_f32(below, fsh) > drop) hi = mid; else lo = mid + 1;
+    }
+    const float least = __uint_as_float(lo);
+    unsigned long long best = 0;
+    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS) {
+        if (!(e[r] >= least) || !row_allowed(allow, r)) continue;
+        const float score = capped(s[r], a.softcap) / T + gumbel_noise(a.seed[b], i, (uint32_t)r);
+        best = max_u64(best, choice_key(score, (uint32_t)r));
+    }
+    return block_max_u64(best, ksh);
+}
+
+__global__ void __launch_bounds__(CH_THREADS) k_choose(ChooseArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float fsh[CH_WAVES];
+    __shared__ unsigned long long ksh[CH_WAVES];
+    const int b = blockIdx.x / a.parts, p = blockIdx.x % a.parts;
+    if (a.active && !slot_bit(a.active, b)) return;
+    const bool masked = a.active && slot_bit(a.active + a.words, b);
+    const uint32_t *allow = masked ? a.allow + (size_t)b * a.allow_words : nullptr;
+    const float T = a.temperature ? a.temperature[b] : 0.f, P = a.top_p ? a.top_p[b] : 1.f;
+    const float *s = a.logits + (size_t)b * a.ld;
+    const uint32_t i = (uint32_t)(a.pos[b] - (a.first ? a.first[b] : 0));
+    unsigned long long *out = a.keys + ((size_t)b * a.parts + p) * 2;
+    if (T > 0.f && P < 1.f) {
+        unsigned long long best = 0;
+        if (p == 0) best = nucleus_choice(a, b, s, allow, T, P, i, fsh, ksh);
+        if (threadIdx.x == 0) out[0] = best, out[1] = 0ull;
+        return;
+    }
+    unsigned long long best = 0, alt = 0;
+    const int r1 = min(a.vocab, (p + 1) * a.span);
+    for (int r = p * a.span + threadIdx.x; r < r1; r += CH_THREADS) {
+        if (!row_allowed(allow, r)) continue;
+        const float score = T > 0.f ? capped(s[r], a.softcap) / T + gumbel_noise(a.seed[b], i, (uint32_t)r) : s[r];
+        const unsigned long long key = choice_key(score, (uint32_t)r);
+        best = max_u64(best, key);
+        if (r != a.lazy) alt = max_u64(alt, key);
+    }
+    best = block_max_u64(best, ksh);
+    alt = block_max_u64(alt, ksh);
+    if (threadIdx.x == 0) out[0] = best, out[1] = alt;
+}
+
+__global__ void k_commit(ChooseArgs a) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= a.B || (a.active && !slot_bit(a.active, b))) return;
+    unsigned long long best = 0, alt = 0;
+    const unsigned long long *k = a.keys + (size_t)b * a.parts * 2;
+    for (int p = 0; p < a.parts; p++) best = max_u64(best, k[2 * p]), alt = max_u64(alt, k[2 * p + 1]);
+    a.tokens[b] = (int32_t)(0xffffffffu - (uint32_t)best);
+    a.alt_tokens[b] = (int32_t)(0xffffffffu - (uint32_t)alt);
+    a.pos[b] += 1;
+}
+
+static int choose_parts(int vocab) {
+    const int per = CH_THREADS * CH_ROWS_PER_THREAD;
+    const int parts = (vocab + per - 1) / per;
+    return parts < 1 ? 1 : (parts > CH_MAX_PARTS ? CH_MAX_PARTS : parts);
+}
+
+static size_t align256_c(size_t x) { return (x + 255) & ~(size_t)255; }
+
+extern "C" long long nc_choose_workspace_bytes(int B, int vocab) {
+    if (B <= 0 || vocab <= 0) return 0;
+    return (long long)(align256_c((size_t)B * choose_parts(vocab) * 2 * sizeof(unsigned long long)) +
+                       (size_t)B * vocab * sizeof(float));
+}
+
+extern "C" int nc_choose_tokens(const float *logits, int B, int vocab, long long ld, const unsigned long long *active,
+                                const uint32_t *allow, const float *temperature, const float *top_p,
+                                const unsigned long long *seed, const int32_t *first, int32_t *pos, float softcap,
+                                int lazy, int32_t *tokens, int32_t *alt_tokens, void *workspace,
+                                long long workspace_bytes, void *stream) {
+    NC_REQUIRE(B >= 0 && vocab > 0 && ld >= vocab, "nc_choose_tokens: B %d, vocab %d, ld %lld", B, vocab, ld);
+    if (B == 0) return 0;
+    NC_REQUIRE(logits && pos && tokens && alt_tokens && workspace, "nc_choose_tokens: null argument");
+    NC_REQUIRE(!active || allow, "nc_choose_tokens: a slot mask needs the allowed-row masks (allow)");
+    NC_REQUIRE((temperature && seed) || !temperature, "nc_choose_tokens: sampling needs seeds");
+    const long long need = nc_choose_workspace_bytes(B, vocab);
+    NC_REQUIRE(workspace_bytes >= need, "nc_choose_tokens: workspace %lld bytes, %lld needed", workspace_bytes, need);
+    NC_REQUIRE((uintptr_t)workspace % 16 == 0, "nc_choose_tokens: workspace must be 16-byte aligned");
+    ChooseArgs a = {};
+    a.logits = logits; a.ld = ld; a.B = B; a.vocab = vocab;
+    a.parts = choose_parts(vocab);
+    a.span = (vocab + a.parts - 1) / a.parts;
+    a.active = active; a.words = (B + 63) / 64;
+    a.allow = allow; a.allow_words = (vocab + 31) / 32;
+    a.temperature = temperature; a.top_p = top_p; a.seed = seed; a.first = first; a.pos = pos;
+    a.softcap = softcap; a.lazy = lazy;
+    a.keys = (unsigned long long *)workspace;
+    a.probs = (float *)((unsigned char *)workspace +
+                        align256_c((size_t)B * a.parts * 2 * sizeof(unsigned long long)));
+    a.tokens = tokens; a.alt_tokens = alt_tokens;
+    hipLaunchKernelGGL(k_choose, dim3((unsigned)(B * a.parts)), dim3(CH_THREADS), 0, (hipStream_t)stream, a);
+    NC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
     return 0;
 }

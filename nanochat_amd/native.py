@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
                                  P, I64, P]),
     "nc_prefill_attn_fp8": (I32, [P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, F32, P, P]),
     "nc_argmax_f32": (I32, [P, I32, I32, I64, P, P]),
+    "nc_choose_workspace_bytes": (I64, [I32, I32]),
+    "nc_choose_tokens": (I32, [P, I32, I32, I64, P, P, P, P, P, P, P, F32, I32, P, P, P, I64, P]),
     "nc_add_rms_norm_bf16": (I32, [P, P, P, P, I32, I32, P]),
     "nc_relu2_bf16": (I32, [P, P, I64, P]),
     "nc_slot_gemm_bf16": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P]),
