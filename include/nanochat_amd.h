@@ -124,8 +124,7 @@ int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, i
  * 189-230 (greedy slots). */
 int nc_argmax_f32(const float *logits, int rows, int cols, long long ld, int32_t *out, void *stream);
 
-/* Workspace bytes nc_choose_tokens needs for B slots over a vocabulary of `vocab` rows: per-workgroup keys and a
- * nucleus slot's probabilities. */
+/* Workspace bytes nc_choose_tokens needs for B slots over a vocabulary of `vocab` rows: per-workgroup keys. */
 long long nc_choose_workspace_bytes(int B, int vocab);
 
 /* Token choice and commit for every active slot b (active: [2][ceil(B / 64)] words, the active slots' bits, then
@@ -134,9 +133,9 @@ long long nc_choose_workspace_bytes(int B, int vocab);
  * allow ([B][ceil(vocab / 32)]) is set. temperature[b] == 0 (or temperature NULL): the largest raw logit, lowest row
  * on ties; > 0: Gumbel-max sampling of softmax(z / T), z = softcap tanh(s / softcap) (softcap <= 0: z = s), noise
  * from Philox4x32-10 at (row, pos[b] - first[b]) keyed by seed[b] (first NULL: 0); top_p[b] < 1 (T > 0): nucleus
- * sampling over the smallest set of rows whose probabilities sum past top_p. Writes tokens[b] (-1: no allowed row),
- * alt_tokens[b] (the best allowed row but `lazy`, -1 if none or for a nucleus slot) and pos[b] += 1. Inactive slots
- * are untouched. Calls in one stream may share the workspace (nc_choose_workspace_bytes).
+ * sampling over the smallest set of rows whose probabilities sum past top_p (vocab <= 131072). Writes tokens[b]
+ * (-1: no allowed row), alt_tokens[b] (the best allowed row but `lazy`, -1 if none or for a nucleus slot) and
+ * pos[b] += 1. Inactive slots are untouched. Calls in one stream may share the workspace (nc_choose_workspace_bytes).
  * Replaces: the CHOICE ARGMAX epilogue, k_nucleus and k_commit, model/kernels/decode.cu:98-105,170-230,360-404,
  * 676-689 (host rules: inference/decoder.py:28-40). */
 int nc_choose_tokens(const float *logits, int B, int vocab, long long ld, const unsigned long long *active,

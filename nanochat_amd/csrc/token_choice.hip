@@ -79,10 +79,12 @@ extern "C" int nc_argmax_f32(const float *logits, int rows, int cols, long long 
  * g = float(-log(-log(u))) in double (decode.cu:98-105's transform).
  *
  * k_choose: a grid of B x P workgroups of 512 threads; workgroup (b, p) scans rows [p L, (p + 1) L) of slot b and
- * writes its best and alternative keys to the workspace. A nucleus slot needs whole-row reductions: its workgroup
- * p = 0 does all of it (the probabilities go to the workspace), the others write empty keys. k_commit then folds
- * each slot's P keys and commits. Sampling is ALU-bound (10 Philox rounds and two double logs per row); greedy is
- * HBM-bound on 4 B per logit.
+ * writes its best and alternative keys to the workspace. A nucleus slot needs whole-row reductions: k_nucleus, one
+ * 512-thread workgroup per slot, keeps the slot's e values in registers (up to 128 per thread: vocabularies up to
+ * 65536; up to 131072 with spills) so that the bisection's ~30 passes are register sums and block reductions, and
+ * writes the slot's key.
+ * k_commit then folds each slot's P keys and commits. Sampling is ALU-bound (10 Philox rounds and two double logs
+ * per row); greedy is HBM-bound on 4 B per logit.
  */
 
 #define CH_THREADS 512
@@ -105,7 +107,6 @@ struct ChooseArgs {
     float softcap;
     int lazy;
     unsigned long long *keys;                /* [B][parts][2]: best, alternative */
-    float *probs;                            /* [B][vocab]: a nucleus slot's e */
     int32_t *tokens, *alt_tokens;            /* [B] */
 };
 
@@ -154,18 +155,26 @@ __device__ unsigned long long block_max_u64(unsigned long long v, unsigned long 
     return r;
 }
 
-__device__ float block_max_f32(float v, float *sh) {
+__device__ __forceinline__ bool row_allowed(const uint32_t *allow, int r) { return !allow || ((allow[r >> 5] >> (r & 31)) & 1u); }
+
+/* A nucleus slot, one workgroup of NU_THREADS: its e values stay in registers (PER per thread, row
+ * r = k NU_THREADS + thread), so the ~30 bisection passes are ALU and block sums only. Rows past the vocabulary hold
+ * e = 0, which no pass counts above a positive threshold. */
+#define NU_THREADS 512 /* 2 waves per SIMD: up to 256 VGPRs, room for 128 e values per thread */
+#define NU_WAVES (NU_THREADS / NC_WAVE)
+
+__device__ float nu_block_max(float v, float *sh) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, shfl_xor_f(v, d));
     __syncthreads();
     if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
     __syncthreads();
     float r = sh[0];
-    for (int w = 1; w < CH_WAVES; w++) r = fmaxf(r, sh[w]);
+    for (int w = 1; w < NU_WAVES; w++) r = fmaxf(r, sh[w]);
     return r;
 }
 
-__device__ float block_sum_f32(float v, float *sh) {
+__device__ float nu_block_sum(float v, float *sh) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) v = v + shfl_xor_f(v, d);
@@ -173,50 +182,88 @@ __device__ float block_sum_f32(float v, float *sh) {
     if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
     __syncthreads();
     float r = sh[0];
-    for (int w = 1; w < CH_WAVES; w++) r = r + sh[w];
+    for (int w = 1; w < NU_WAVES; w++) r = r + sh[w];
     return r;
 }
 
-__device__ __forceinline__ bool row_allowed(const uint32_t *allow, int r) { return !allow || ((allow[r >> 5] >> (r & 31)) & 1u); }
+__device__ unsigned long long nu_block_max_u64(unsigned long long v, unsigned long long *sh) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = max_u64(v, shfl_xor_u64(v, d));
+    __syncthreads();
+    if ((threadIdx.x & (NC_WAVE - 1)) == 0) sh[threadIdx.x / NC_WAVE] = v;
+    __syncthreads();
+    unsigned long long r = sh[0];
+    for (int w = 1; w < NU_WAVES; w++) r = max_u64(r, sh[w]);
+    return r;
+}
 
-/* A nucleus slot, one workgroup: e to the workspace, its sum, the bisection, then Gumbel-max over the kept rows. */
-__device__ unsigned long long nucleus_choice(const ChooseArgs &a, int b, const float *s, const uint32_t *allow, float T,
-                                             float P, uint32_t i, float *fsh, unsigned long long *ksh) {
+
+template <int PER>
+__global__ void __launch_bounds__(NU_THREADS) k_nucleus(ChooseArgs a) {
 #pragma clang fp contract(off)
-    float *e = a.probs + (size_t)b * a.vocab; /* a thread reads back only the rows it wrote */
+    __shared__ float fsh[NU_WAVES];
+    __shared__ unsigned long long ksh[NU_WAVES];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (a.active && !slot_bit(a.active, b)) return;
+    const float T = a.temperature ? a.temperature[b] : 0.f, P = a.top_p ? a.top_p[b] : 1.f;
+    if (!(T > 0.f && P < 1.f)) return;
+    const bool masked = a.active && slot_bit(a.active + a.words, b);
+    const uint32_t *allow = masked ? a.allow + (size_t)b * a.allow_words : nullptr;
+    const float *s = a.logits + (size_t)b * a.ld;
+    const uint32_t i = (uint32_t)(a.pos[b] - (a.first ? a.first[b] : 0));
+    float zt[PER];
     float m = -INFINITY;
-    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS)
-        if (row_allowed(allow, r)) m = fmaxf(m, capped(s[r], a.softcap) / T);
-    m = block_max_f32(m, fsh);
-    float sum = 0.f;
-    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS) {
-        const float ev = row_allowed(allow, r) ? expf(capped(s[r], a.softcap) / T - m) : 0.f;
-        e[r] = ev;
-        sum = sum + ev;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int r = k * NU_THREADS + tid;
+        zt[k] = (r < a.vocab && row_allowed(allow, r)) ? capped(s[r], a.softcap) / T : -INFINITY;
+        m = fmaxf(m, zt[k]);
     }
-    const float drop = (1.f - P) * block_sum_f32(sum, fsh);
+    m = nu_block_max(m, fsh);
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        zt[k] = zt[k] == -INFINITY ? 0.f : expf(zt[k] - m); /* zt now holds e */
+        sum = sum + zt[k];
+    }
+    const float drop = (1.f - P) * nu_block_sum(sum, fsh);
     uint32_t lo = 0u, hi = __float_as_uint(1.f); /* the least bits u with C(u) > drop; C(1) is the whole sum */
     while (lo < hi) {
         const uint32_t mid = lo + (hi - lo) / 2;
         const float x = __uint_as_float(mid);
         float below = 0.f;
-        for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS)
-            if (e[r] <= x) below = below + e[r];
-        if (block_sum_f32(below, fsh) > drop) hi = mid; else lo = mid + 1;
+#pragma unroll
+        for (int k = 0; k < PER; k++) below = below + (zt[k] <= x ? zt[k] : 0.f);
+        if (nu_block_sum(below, fsh) > drop) hi = mid; else lo = mid + 1;
     }
     const float least = __uint_as_float(lo);
+    /* the kept rows as bit masks (static register indices), then Gumbel-max over their set bits */
+    constexpr int WORDS = (PER + 63) / 64;
     unsigned long long best = 0;
-    for (int r = threadIdx.x; r < a.vocab; r += CH_THREADS) {
-        if (!(e[r] >= least) || !row_allowed(allow, r)) continue;
-        const float score = capped(s[r], a.softcap) / T + gumbel_noise(a.seed[b], i, (uint32_t)r);
-        best = max_u64(best, choice_key(score, (uint32_t)r));
+#pragma unroll
+    for (int wd = 0; wd < WORDS; wd++) {
+        unsigned long long kept = 0;
+#pragma unroll
+        for (int k = wd * 64; k < (wd + 1) * 64 && k < PER; k++)
+            kept |= (unsigned long long)(zt[k] >= least && zt[k] > 0.f) << (k - wd * 64);
+        while (kept) {
+            const int k = wd * 64 + __builtin_ctzll(kept);
+            kept &= kept - 1;
+            const int r = k * NU_THREADS + tid;
+            const float score = capped(s[r], a.softcap) / T + gumbel_noise(a.seed[b], i, (uint32_t)r);
+            best = max_u64(best, choice_key(score, (uint32_t)r));
+        }
     }
-    return block_max_u64(best, ksh);
+    best = nu_block_max_u64(best, ksh);
+    if (tid == 0) {
+        unsigned long long *out = a.keys + (size_t)b * a.parts * 2;
+        out[0] = best;
+        out[1] = 0ull;
+    }
 }
 
 __global__ void __launch_bounds__(CH_THREADS) k_choose(ChooseArgs a) {
 #pragma clang fp contract(off)
-    __shared__ float fsh[CH_WAVES];
     __shared__ unsigned long long ksh[CH_WAVES];
     const int b = blockIdx.x / a.parts, p = blockIdx.x % a.parts;
     if (a.active && !slot_bit(a.active, b)) return;
@@ -226,10 +273,8 @@ __global__ void __launch_bounds__(CH_THREADS) k_choose(ChooseArgs a) {
     const float *s = a.logits + (size_t)b * a.ld;
     const uint32_t i = (uint32_t)(a.pos[b] - (a.first ? a.first[b] : 0));
     unsigned long long *out = a.keys + ((size_t)b * a.parts + p) * 2;
-    if (T > 0.f && P < 1.f) {
-        unsigned long long best = 0;
-        if (p == 0) best = nucleus_choice(a, b, s, allow, T, P, i, fsh, ksh);
-        if (threadIdx.x == 0) out[0] = best, out[1] = 0ull;
+    if (T > 0.f && P < 1.f) { /* k_nucleus writes part 0 */
+        if (threadIdx.x == 0 && p > 0) out[0] = out[1] = 0ull;
         return;
     }
     unsigned long long best = 0, alt = 0;
@@ -263,12 +308,9 @@ static int choose_parts(int vocab) {
     return parts < 1 ? 1 : (parts > CH_MAX_PARTS ? CH_MAX_PARTS : parts);
 }
 
-static size_t align256_c(size_t x) { return (x + 255) & ~(size_t)255; }
-
 extern "C" long long nc_choose_workspace_bytes(int B, int vocab) {
     if (B <= 0 || vocab <= 0) return 0;
-    return (long long)(align256_c((size_t)B * choose_parts(vocab) * 2 * sizeof(unsigned long long)) +
-                       (size_t)B * vocab * sizeof(float));
+    return (long long)((size_t)B * choose_parts(vocab) * 2 * sizeof(unsigned long long));
 }
 
 extern "C" int nc_choose_tokens(const float *logits, int B, int vocab, long long ld, const unsigned long long *active,
@@ -277,6 +319,7 @@ extern "C" int nc_choose_tokens(const float *logits, int B, int vocab, long long
                                 int lazy, int32_t *tokens, int32_t *alt_tokens, void *workspace,
                                 long long workspace_bytes, void *stream) {
     NC_REQUIRE(B >= 0 && vocab > 0 && ld >= vocab, "nc_choose_tokens: B %d, vocab %d, ld %lld", B, vocab, ld);
+    NC_REQUIRE(vocab <= 256 * NU_THREADS, "nc_choose_tokens: vocab %d exceeds %d", vocab, 256 * NU_THREADS);
     if (B == 0) return 0;
     NC_REQUIRE(logits && pos && tokens && alt_tokens && workspace, "nc_choose_tokens: null argument");
     NC_REQUIRE(!active || allow, "nc_choose_tokens: a slot mask needs the allowed-row masks (allow)");
@@ -293,11 +336,23 @@ extern "C" int nc_choose_tokens(const float *logits, int B, int vocab, long long
     a.temperature = temperature; a.top_p = top_p; a.seed = seed; a.first = first; a.pos = pos;
     a.softcap = softcap; a.lazy = lazy;
     a.keys = (unsigned long long *)workspace;
-    a.probs = (float *)((unsigned char *)workspace +
-                        align256_c((size_t)B * a.parts * 2 * sizeof(unsigned long long)));
     a.tokens = tokens; a.alt_tokens = alt_tokens;
     hipLaunchKernelGGL(k_choose, dim3((unsigned)(B * a.parts)), dim3(CH_THREADS), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
+    if (temperature && top_p) { /* nucleus slots (temperature > 0, top_p < 1), if any: chosen on the device */
+        const int per = (vocab + NU_THREADS - 1) / NU_THREADS;
+        if (per <= 16)
+            hipLaunchKernelGGL(k_nucleus<16>, dim3(B), dim3(NU_THREADS), 0, (hipStream_t)stream, a);
+        else if (per <= 32)
+            hipLaunchKernelGGL(k_nucleus<32>, dim3(B), dim3(NU_THREADS), 0, (hipStream_t)stream, a);
+        else if (per <= 64)
+            hipLaunchKernelGGL(k_nucleus<64>, dim3(B), dim3(NU_THREADS), 0, (hipStream_t)stream, a);
+        else if (per <= 128)
+            hipLaunchKernelGGL(k_nucleus<128>, dim3(B), dim3(NU_THREADS), 0, (hipStream_t)stream, a);
+        else /* past 65536 rows the values spill to scratch: slower, the same result */
+            hipLaunchKernelGGL(k_nucleus<256>, dim3(B), dim3(NU_THREADS), 0, (hipStream_t)stream, a);
+        NC_LAUNCH_CHECK();
+    }
     hipLaunchKernelGGL(k_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
     return 0;

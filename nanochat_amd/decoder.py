@@ -8,8 +8,8 @@ prefilled, then every step feeds one token per sequence and appends the chosen o
     h  = x + o_proj(attention(qk_norm_rope(qkv_proj(norm(x)))))     append + attention: this package's kernels
     x' = h + down_proj(relu(up_proj(norm(h)))^2)
 
-with x0 = norm(embed(token)), a final norm, the untied lm_head and the greedy choice (largest fp32 logit, lowest id
-on ties, nc_argmax_f32). The decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the
+with x0 = norm(embed(token)), a final norm, the untied lm_head and the token choice (nc_choose_tokens: greedy, the
+largest fp32 logit with the lowest id on ties, unless set_sampling asks for temperature / nucleus sampling). The decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the
 reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
 per-row rstd, ReLU^2 into the up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
 through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
@@ -26,6 +26,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor
@@ -34,6 +35,7 @@ from nanochat_amd.attention import decode_step, decode_workspace, prefill_attent
 from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
 from nanochat_amd.native import check, hip_library, pointer, stream
 from nanochat_amd.rotary import rotary_tables
+from nanochat_amd.sampling import SOFTCAP, choose_tokens, choose_workspace
 from nanochat_amd.slot_gemm import NORM_F32, NORM_STORE, RELU2_NORM, RESID, slot_gemm
 
 EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear.py:20)
@@ -157,6 +159,24 @@ class Fp8Decoder:
         if vp != cfg.vocab:
             self.lm_head = torch.zeros((vp, cfg.d_model), dtype=torch.bfloat16, device=device)
             self.lm_head[:cfg.vocab] = model.lm_head
+        # the token choice (nc_choose_tokens): greedy until set_sampling; alternatives exclude `lazy`
+        self.choose_ws = choose_workspace(batch, cfg.vocab, device)
+        self.alt = torch.empty(batch, dtype=torch.int32, device=device)
+        self.temperature = self.top_p = self.seeds = self.first = None
+        self.softcap, self.lazy = SOFTCAP, -1
+
+    def set_sampling(self, temperature, top_p=1.0, seed=0, first=0, softcap: float = SOFTCAP) -> None:
+        """Per-slot sampling (scalars broadcast; inference/decoder.py:28-40): temperature 0 is greedy, > 0 a
+        Gumbel-max sample of softmax(capped logits / temperature) drawn from (seed, position - first) alone, top_p < 1
+        nucleus sampling. first: the position of each slot's first generated token. Takes effect for steps launched
+        (or graphs captured) afterwards."""
+        B, dev = self.batch, self.device
+        full = lambda v, dt: torch.as_tensor(np.broadcast_to(np.asarray(v), (B,)).copy()).to(dev, dt).contiguous()
+        self.temperature = full(temperature, torch.float32)
+        self.top_p = full(top_p, torch.float32)
+        self.seeds = full(np.asarray(seed, dtype=np.uint64).view(np.int64), torch.int64)
+        self.first = full(first, torch.int32)
+        self.softcap = float(softcap)
 
     # ---------------------------------------------------------------------------------------------- layers
     def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
@@ -206,9 +226,10 @@ class Fp8Decoder:
 
     # ---------------------------------------------------------------------------------------------- decode
     def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor) -> Tensor:
-        """One decode step: token tok[b] at position pos[b] of every sequence; the greedy choice into out_tok.
-        Returns the fp32 logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and
-        attention; x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
+        """One decode step: token tok[b] at position pos[b] of every sequence; the choice (greedy, or by
+        set_sampling) into out_tok, its alternative into self.alt, then pos += 1 (the commit). Returns the fp32
+        logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and attention;
+        x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
         x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
         for l in range(self.cfg.layers):
             lw = self.model.layers[l]
@@ -220,13 +241,15 @@ class Fp8Decoder:
             u = slot_gemm(x, lw["wup"], RELU2_NORM)
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
         logits = slot_gemm(x, self.lm_head, NORM_F32)
-        argmax_rows(logits[:, :self.cfg.vocab], out_tok)
+        choose_tokens(logits, self.cfg.vocab, pos, temperature=self.temperature, top_p=self.top_p, seed=self.seeds,
+                      first=self.first, softcap=self.softcap, lazy=self.lazy, tokens=out_tok, alt_tokens=self.alt,
+                      workspace=self.choose_ws)
         return logits[:, :self.cfg.vocab]
 
     @torch.no_grad()
     def start(self, last_tokens: Tensor, position: int) -> None:
         """Decode state: every sequence's next input token (int32 [batch]) at `position`; captures the step graph
-        (positions and the token history advance on the device)."""
+        (positions and the token history advance on the device: the choice commits pos + 1)."""
         B = self.batch
         self.tok = last_tokens.to(torch.int32).clone()
         self.pos = torch.full((B,), position, dtype=torch.int32, device=self.device)
@@ -238,13 +261,13 @@ class Fp8Decoder:
         with torch.cuda.stream(s):
             # warm every launch path, then restore the state the warm-up advanced
             self._step(self.tok, self.pos, self.next)
+            self.pos.fill_(position)
             s.synchronize()
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph, stream=s):
                 self._step(self.tok, self.pos, self.next)
                 self.history.index_copy_(0, self.step_idx, self.next.unsqueeze(0))
                 self.tok.copy_(self.next)
-                self.pos.add_(1)
                 self.step_idx.add_(1)
         torch.cuda.current_stream(self.device).wait_stream(s)
         self.stream = s

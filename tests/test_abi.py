@@ -166,3 +166,30 @@ def test_slot_gemm_rejects_bad_arguments():
     rejects(96, 64, 8, 0, NULL, (64, 32), "tile")  # n not a multiple of the tile
     rejects(1 << 20, 1 << 10, 8, 0, NULL, (0, 0), "2 GiB")
     assert lib.nc_slot_gemm_bf16(FAKE, 32, 64, FAKE, 0, 0, FAKE, NULL, 0, 0, NULL) == 0  # m = 0: nothing launched
+
+
+def test_choose_rejects_bad_arguments():
+    lib = native.hip_library()
+    need = lib.nc_choose_workspace_bytes(8, 1000)
+    assert need >= 8 * 2 * 8  # a best and an alternative key per slot at least
+    assert lib.nc_choose_workspace_bytes(0, 1000) == 0
+    #       logits B  vocab ld   active allow temp  top_p seed  first pos   cap  lazy tokens alt  ws    bytes stream
+    base = [FAKE, 8, 1000, 200_000, NULL, NULL, NULL, NULL, NULL, NULL, FAKE, 15.0, -1, FAKE, FAKE, FAKE, need, NULL]
+
+    def rejects(i, value, message):
+        args = list(base)
+        args[i] = value
+        assert lib.nc_choose_tokens(*args) < 0, (i, value)
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    rejects(3, 999, "ld")
+    rejects(2, 0, "vocab")
+    rejects(2, 131073, "exceeds")
+    rejects(10, NULL, "null")
+    rejects(4, FAKE, "allow")           # a slot mask without the allowed-row masks
+    rejects(6, FAKE, "seeds")           # temperatures without seeds
+    rejects(16, need - 1, "workspace")
+    rejects(15, ctypes.c_void_p(0x1008), "aligned")
+    empty = list(base)
+    empty[1] = 0
+    assert lib.nc_choose_tokens(*empty) == 0

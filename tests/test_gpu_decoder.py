@@ -124,3 +124,40 @@ def test_graph_replays_equal_eager_steps(gpu):
         torch.cuda.synchronize()
         torch.zeros(1 << 20, device=dev).sum()
     torch.testing.assert_close(graphed.tokens(steps).cpu(), want)
+
+
+def test_sampled_decoding_follows_the_choice_rules(gpu):
+    """Per-slot temperature / top_p / seed: every step's tokens are the oracle's choice (oracle/sampling.py) on that
+    step's own logits, the positions advance by the commit, and graph replays equal eager steps."""
+    from oracle import sampling as S
+
+    dev = gpu
+    B, T, steps = 4, 30, 4
+    model = RandomModel(TINY, dev, seed=11)
+    prompts = torch.from_numpy(np.random.default_rng(12).integers(0, TINY.vocab, (B, T)).astype(np.int32)).to(dev)
+    temp = np.array([0.0, 0.7, 1.5, 1.0], np.float32)
+    top_p = np.array([1.0, 1.0, 0.9, 0.5], np.float32)
+    seeds = np.array([1, 2, 3, (1 << 40) + 5], np.uint64)
+    eager = Fp8Decoder(model, B, T - 1 + steps, dev)
+    eager.prefill(prompts)
+    eager.set_sampling(temp, top_p, seeds, first=T - 1)
+    tok, outs = prompts[:, -1].clone(), []
+    pos = torch.full((B,), T - 1, dtype=torch.int32, device=dev)
+    for s in range(steps):
+        nxt = torch.empty(B, dtype=torch.int32, device=dev)
+        before = pos.cpu().numpy()
+        logits = eager._step(tok, pos, nxt).cpu().numpy()
+        want, _, want_pos = S.choose(logits, temperature=temp, top_p=top_p, seed=seeds, pos=before,
+                                     first=np.full(B, T - 1, np.int32))
+        np.testing.assert_array_equal(nxt.cpu().numpy(), want, err_msg=f"step {s}")
+        np.testing.assert_array_equal(pos.cpu().numpy(), want_pos)
+        outs.append(nxt.clone())
+        tok = nxt
+    graphed = Fp8Decoder(model, B, T - 1 + steps, dev)
+    graphed.prefill(prompts)
+    graphed.set_sampling(temp, top_p, seeds, first=T - 1)
+    graphed.start(prompts[:, -1], T - 1)
+    for _ in range(steps):
+        graphed.run(1)
+        torch.cuda.synchronize()
+    torch.testing.assert_close(graphed.tokens(steps).cpu(), torch.stack(outs, 1).cpu())
