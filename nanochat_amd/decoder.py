@@ -9,17 +9,18 @@ prefilled, then every step feeds one token per sequence and appends the chosen o
     x' = h + down_proj(relu(up_proj(norm(h)))^2)
 
 with x0 = norm(embed(token)), a final norm, the untied lm_head and the token choice (nc_choose_tokens: greedy, the
-largest fp32 logit with the lowest id on ties, unless set_sampling asks for temperature / nucleus sampling). The decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the
-reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
+largest fp32 logit with the lowest id on ties, unless set_sampling asks for temperature / nucleus sampling). The
+decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
 per-row rstd, ReLU^2 into the up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
 through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
 attention and the token choice are HIP kernels throughout (a decode step's append and attention are one
 nc_decode_step_fp8 call per layer); the decode step is captured once in a hipGraph and replayed.
 
 The architecture is BASELINE config 5's: RoPE, QK-norm, ReLU^2 MLP at 4x, untied embeddings, bf16 weights
-N(0, 0.02), full causal attention in every layer. The reference's training-time extras that this config does not
-name (value embeddings, per-layer residual / x0 mixing, which are identity and zero at the reference's init) are
-not part of it.
+N(0, 0.02), full causal attention in every layer. A trained checkpoint (checkpoint.load_hf, the export of
+inference/export_hf.py) also brings what config 5 does not name, and the decoder runs it: per-layer sliding windows,
+value embeddings (v += 2 sigmoid(ve_gate n) ve[token], inference/modeling_nanochat.py:85-88) and the per-layer
+residual / x0 mix (inference/modeling_nanochat.py:170-171), identity at the reference's initialisation.
 """
 
 from __future__ import annotations
@@ -35,7 +36,7 @@ from nanochat_amd.attention import decode_step, decode_workspace, prefill_attent
 from nanochat_amd.kv_cache import HEAD_DIM, Fp8KVCache, _require
 from nanochat_amd.native import check, hip_library, pointer, stream
 from nanochat_amd.rotary import rotary_tables
-from nanochat_amd.sampling import SOFTCAP, choose_tokens, choose_workspace
+from nanochat_amd.sampling import choose_tokens, choose_workspace
 from nanochat_amd.slot_gemm import NORM_F32, NORM_STORE, RELU2_NORM, RESID, slot_gemm
 
 EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear.py:20)
@@ -43,16 +44,26 @@ EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear
 
 @dataclass(frozen=True)
 class ModelConfig:
+    """The decoder's architecture. Beyond BASELINE config 5 (full attention everywhere, no value embeddings), the
+    fields a trained nanochat checkpoint carries (inference/export_hf.py:63-75): per-layer windows (keys before a
+    query; -1 all), the value-embedding layers, the kv head count and the logit cap."""
     layers: int
     d_model: int
     heads: int
     vocab: int
     mlp_mult: int = 4
     theta: float = 10000.0
+    windows: tuple[int, ...] = ()     # () : every layer full
+    ve_layers: tuple[int, ...] = ()
+    n_kv_heads: int = 0               # 0: heads (MHA)
+    softcap: float = 15.0
 
     @property
     def kv_heads(self) -> int:
-        return self.heads
+        return self.n_kv_heads or self.heads
+
+    def window(self, layer: int) -> int:
+        return self.windows[layer] if self.windows else -1
 
 
 @dataclass(frozen=True)
@@ -84,9 +95,35 @@ def argmax_rows(logits: Tensor, out: Tensor | None = None) -> Tensor:
     return out
 
 
-class RandomModel:
-    """bf16 weights N(0, std) from a seeded generator (random init: no checkpoint is loaded); QK-norm gains 1.
-    wqkv rows are q heads, then k heads, then v heads (the fused projection's column blocks, decode.cu:476)."""
+class Weights:
+    """A model's tensors on the device, as the decoder reads them: wte, lm_head (bf16 [vocab][d]); per layer wqkv
+    (q heads, then k heads, then v heads: the fused projection's column blocks, decode.cu:476), wo, wup, wdown (bf16),
+    q_gain, k_gain (fp32 [128], the QK-norm weights), and in value-embedding layers ve (bf16 [vocab][H 128]) and
+    ve_gate (fp32 [H][d]); resid_lambdas, x0_lambdas (fp32 [layers]) mix each layer's input as
+    bf16(resid x + x0 x0) (inference/modeling_nanochat.py:170-171)."""
+
+    cfg: ModelConfig
+    wte: Tensor
+    lm_head: Tensor
+    layers: list
+    resid_lambdas: Tensor
+    x0_lambdas: Tensor
+
+    @property
+    def mixes(self) -> bool:
+        """False when every layer's mix is the identity (resid 1, x0 0: the reference's initialisation)."""
+        return bool((self.resid_lambdas != 1).any() or (self.x0_lambdas != 0).any())
+
+    def weight_bytes(self) -> int:
+        n = self.wte.numel() + self.lm_head.numel()
+        for lw in self.layers:
+            n += sum(lw[k].numel() for k in ("wqkv", "wo", "wup", "wdown"))
+        return 2 * n
+
+
+class RandomModel(Weights):
+    """bf16 weights N(0, std) from a seeded generator (random init: no checkpoint is loaded); QK-norm gains 1, the
+    identity mix, value-embedding tables and gates (if cfg names such layers) N(0, std) and zero."""
 
     def __init__(self, cfg: ModelConfig, device, seed: int = 5, std: float = 0.02):
         self.cfg = cfg
@@ -99,18 +136,17 @@ class RandomModel:
 
         self.wte = w(cfg.vocab, d)
         self.layers = []
-        for _ in range(cfg.layers):
-            self.layers.append(dict(wqkv=w(C + 2 * ckv, d), wo=w(d, C), wup=w(cfg.mlp_mult * d, d),
-                                    wdown=w(d, cfg.mlp_mult * d),
-                                    q_gain=torch.ones(HEAD_DIM, device=device),
-                                    k_gain=torch.ones(HEAD_DIM, device=device)))
+        for i in range(cfg.layers):
+            lw = dict(wqkv=w(C + 2 * ckv, d), wo=w(d, C), wup=w(cfg.mlp_mult * d, d), wdown=w(d, cfg.mlp_mult * d),
+                      q_gain=torch.ones(HEAD_DIM, device=device), k_gain=torch.ones(HEAD_DIM, device=device))
+            if i in cfg.ve_layers:
+                lw["ve"] = w(cfg.vocab, ckv)
+                lw["ve_gate"] = torch.zeros((cfg.kv_heads, d), device=device)
+            self.layers.append(lw)
         self.lm_head = w(cfg.vocab, d)
+        self.resid_lambdas = torch.ones(cfg.layers, device=device)
+        self.x0_lambdas = torch.zeros(cfg.layers, device=device)
 
-    def weight_bytes(self) -> int:
-        n = self.wte.numel() + self.lm_head.numel()
-        for lw in self.layers:
-            n += sum(lw[k].numel() for k in ("wqkv", "wo", "wup", "wdown"))
-        return 2 * n
 
 
 def rms_norm(x: Tensor) -> Tensor:
@@ -143,7 +179,7 @@ def relu2(x: Tensor) -> Tensor:
 class Fp8Decoder:
     """Batch `batch` sequences of at most max_len tokens, one contiguous fp8 cache per layer."""
 
-    def __init__(self, model: RandomModel, batch: int, max_len: int, device, row_chunk: int = 16384):
+    def __init__(self, model: Weights, batch: int, max_len: int, device, row_chunk: int = 16384):
         cfg = model.cfg
         self.model, self.cfg, self.batch, self.max_len, self.device = model, cfg, batch, max_len, device
         self.caches = [Fp8KVCache.contiguous(batch, max_len, cfg.kv_heads, device) for _ in range(cfg.layers)]
@@ -163,9 +199,10 @@ class Fp8Decoder:
         self.choose_ws = choose_workspace(batch, cfg.vocab, device)
         self.alt = torch.empty(batch, dtype=torch.int32, device=device)
         self.temperature = self.top_p = self.seeds = self.first = None
-        self.softcap, self.lazy = SOFTCAP, -1
+        self.softcap, self.lazy = cfg.softcap, -1
+        self.mixes = model.mixes
 
-    def set_sampling(self, temperature, top_p=1.0, seed=0, first=0, softcap: float = SOFTCAP) -> None:
+    def set_sampling(self, temperature, top_p=1.0, seed=0, first=0, softcap: float | None = None) -> None:
         """Per-slot sampling (scalars broadcast; inference/decoder.py:28-40): temperature 0 is greedy, > 0 a
         Gumbel-max sample of softmax(capped logits / temperature) drawn from (seed, position - first) alone, top_p < 1
         nucleus sampling. first: the position of each slot's first generated token. Takes effect for steps launched
@@ -176,14 +213,35 @@ class Fp8Decoder:
         self.top_p = full(top_p, torch.float32)
         self.seeds = full(np.asarray(seed, dtype=np.uint64).view(np.int64), torch.int64)
         self.first = full(first, torch.int32)
-        self.softcap = float(softcap)
+        if softcap is not None:
+            self.softcap = float(softcap)
 
     # ---------------------------------------------------------------------------------------------- layers
-    def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor) -> Tensor:
-        """h = norm(x); the projection, then QK-norm + RoPE + fp8 append of k, v; returns q."""
+    def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor) -> Tensor:
+        """h = norm(x); the projection (with the value-embedding mix), then QK-norm + RoPE + fp8 append of k, v;
+        returns q."""
         lw = self.model.layers[l]
         qkv = torch.matmul(h, lw["wqkv"].t())
+        self._value_embed(l, qkv, h, tok)
         return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
+
+    def _mix(self, l: int, x: Tensor, x0: Tensor) -> None:
+        """x = bf16(resid_lambdas[l] x + x0_lambdas[l] x0) in place, fp32 products and sum rounded once
+        (inference/modeling_nanochat.py:170-171); skipped when every layer's mix is the identity."""
+        if self.mixes:
+            r, z = self.model.resid_lambdas[l], self.model.x0_lambdas[l]
+            x.copy_((r * x.float() + z * x0.float()).to(torch.bfloat16))
+
+    def _value_embed(self, l: int, qkv: Tensor, n: Tensor, tok: Tensor) -> None:
+        """In a value-embedding layer, v += 2 sigmoid(ve_gate n) ve[tok] per head in fp32, rounded to bf16 once, in
+        the projection rows qkv (inference/modeling_nanochat.py:85-88; decode.cu:478-493). n: the normed stream."""
+        lw = self.model.layers[l]
+        if "ve" not in lw:
+            return
+        rows, H, hq = qkv.shape[0], self.cfg.kv_heads, self.cfg.heads
+        gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))  # [rows][H]
+        v = qkv[:, (hq + H) * HEAD_DIM:(hq + 2 * H) * HEAD_DIM].view(rows, H, HEAD_DIM)
+        v.copy_((v.float() + gate[..., None] * lw["ve"][tok].view(rows, H, HEAD_DIM).float()).to(torch.bfloat16))
 
     def _finish_layer(self, l: int, x: Tensor, o: Tensor) -> Tensor:
         """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; returns norm(x), the next layer's
@@ -214,13 +272,17 @@ class Fp8Decoder:
         pos = torch.arange(T - 1, dtype=torch.int32, device=self.device).repeat(B)
         seq = torch.arange(B, dtype=torch.int32, device=self.device).repeat_interleave(T - 1)
         x, h = self._embed(tok)
+        x0 = x.clone() if self.mixes else None
         q = torch.empty((n, self.cfg.heads, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
         o = torch.empty_like(q)
         chunks = [(r, min(r + self.row_chunk, n)) for r in range(0, n, self.row_chunk)]
         for l in range(self.cfg.layers):
             for r0, r1 in chunks:
-                q[r0:r1] = self._qkv_append(l, h[r0:r1], pos[r0:r1], seq[r0:r1])
-            prefill_attention(q, self.caches[l], pos, seq, out=o)
+                if self.mixes:
+                    self._mix(l, x[r0:r1], x0[r0:r1])
+                    h[r0:r1] = add_rms_norm(x[r0:r1], None)
+                q[r0:r1] = self._qkv_append(l, h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1])
+            prefill_attention(q, self.caches[l], pos, seq, window=self.cfg.window(l), out=o)
             for r0, r1 in chunks:
                 h[r0:r1] = self._finish_layer(l, x[r0:r1], o[r0:r1])
 
@@ -231,12 +293,16 @@ class Fp8Decoder:
         logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and attention;
         x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
         x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
+        x0 = x.clone() if self.mixes else None
         for l in range(self.cfg.layers):
             lw = self.model.layers[l]
+            self._mix(l, x, x0)
             qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
+            if "ve" in lw:
+                self._value_embed(l, qkv, add_rms_norm(x, None), tok)
             # the append (decode.cu:550-565) and attention in one call: sequence b is cache row b
             o = decode_step(qkv, self.caches[l], pos, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
-                            max_ctx=self.max_len, workspace=self.ws)
+                            max_ctx=self.max_len, window=self.cfg.window(l), workspace=self.ws)
             slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
             u = slot_gemm(x, lw["wup"], RELU2_NORM)
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)

@@ -26,18 +26,30 @@ class CpuModel:
     """The decoder's math on the CPU: bf16 tensors and torch bf16 GEMMs; the oracle's append, rows_attention and
     decode_attention on a host copy of the cache layout."""
 
-    def __init__(self, model: RandomModel, batch: int, max_len: int):
+    def __init__(self, model, batch: int, max_len: int):
         cfg = model.cfg
         self.cfg, self.batch = cfg, batch
         self.w = [{k: v.cpu() for k, v in lw.items()} for lw in model.layers]
         self.wte, self.lm_head = model.wte.cpu(), model.lm_head.cpu()
+        self.lr, self.l0 = model.resid_lambdas.cpu(), model.x0_lambdas.cpu()
         self.max_blocks = -(-max_len // G.PAGE)
         self.caches = [G.PagedCache(batch * self.max_blocks, cfg.kv_heads) for _ in range(cfg.layers)]
         self.cos, self.sin = G.rotary_tables(max_len, cfg.theta)
 
-    def _layer(self, l, x, pos, seq, attend):
+    def _mix(self, l, x, x0):
+        """inference/modeling_nanochat.py:170-171: bf16(resid h + x0 x0) in fp32."""
+        return (self.lr[l] * x.float() + self.l0[l] * x0.float()).to(torch.bfloat16)
+
+    def _layer(self, l, x, pos, seq, tok, attend):
         lw, cfg = self.w[l], self.cfg
-        qkv = cpu_norm(x) @ lw["wqkv"].t()
+        n = cpu_norm(x)
+        qkv = n @ lw["wqkv"].t()
+        if "ve" in lw:  # inference/modeling_nanochat.py:85-88
+            H = cfg.kv_heads
+            gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))
+            v = qkv[:, (cfg.heads + H) * 128:].reshape(-1, H, 128)
+            ve = lw["ve"][torch.from_numpy(np.asarray(tok, np.int64))].reshape(-1, H, 128)
+            qkv[:, (cfg.heads + H) * 128:] = (v.float() + gate[..., None] * ve.float()).to(torch.bfloat16).flatten(1)
         q = G.append(self.caches[l], bits(qkv), pos, seq, lw["q_gain"].numpy(), lw["k_gain"].numpy(), self.cos,
                      self.sin, cfg.heads, cfg.kv_heads, None, self.max_blocks)
         o = torch.from_numpy(attend(q, self.caches[l]).astype(np.float32)).to(torch.bfloat16)
@@ -49,20 +61,23 @@ class CpuModel:
         B, T = prompts.shape
         pos = np.tile(np.arange(T - 1), B)
         seq = np.repeat(np.arange(B), T - 1)
-        x = cpu_norm(self.wte[torch.from_numpy(prompts[:, :-1].reshape(-1).astype(np.int64))])
+        tok = prompts[:, :-1].reshape(-1)
+        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
         scale = 128 ** -0.5
         for l in range(self.cfg.layers):
-            x = self._layer(l, x, pos, seq, lambda q, c: G.rows_attention(
-                q, pos, seq, c, None, self.max_blocks, B, -1, self.cfg.heads, self.cfg.kv_heads, scale))
+            w = self.cfg.window(l)
+            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.rows_attention(
+                q, pos, seq, c, None, self.max_blocks, B, w, self.cfg.heads, self.cfg.kv_heads, scale))
 
     def step(self, tok, position):
         B = self.batch
         pos, seq = np.full(B, position), np.arange(B)
-        x = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
+        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
         scale = 128 ** -0.5
         for l in range(self.cfg.layers):
-            x = self._layer(l, x, pos, seq, lambda q, c: G.decode_attention(
-                q, c, None, self.max_blocks, pos + 1, -1, self.cfg.heads, self.cfg.kv_heads, scale))
+            w = self.cfg.window(l)
+            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.decode_attention(
+                q, c, None, self.max_blocks, pos + 1, w, self.cfg.heads, self.cfg.kv_heads, scale))
         return (cpu_norm(x).float() @ self.lm_head.float().t()).numpy()
 
 
@@ -78,10 +93,37 @@ def test_argmax_lowest_index_on_ties(gpu):
 
 
 def test_decoder_matches_cpu_model_step_by_step(gpu):
+    check_against_cpu(gpu, RandomModel(TINY, gpu, seed=7))
+
+
+def test_loaded_checkpoint_matches_cpu_model(gpu, tmp_path):
+    """A trained-like export (inference/export_hf.py's format): sliding windows, value embeddings, QK-norm gains
+    and a non-identity residual / x0 mix, written by save_hf, read back by load_hf, decoded against the CPU model."""
+    from nanochat_amd.checkpoint import load_hf, save_hf
+    from nanochat_amd.decoder import ModelConfig
+
+    cfg = ModelConfig(layers=4, d_model=256, heads=2, vocab=1000, theta=1e6, windows=(16, 16, 16, -1),
+                      ve_layers=(1, 3))
+    m = RandomModel(cfg, "cpu", seed=13)
+    g = torch.Generator().manual_seed(14)
+    m.resid_lambdas = 0.8 + 0.4 * torch.rand(cfg.layers, generator=g)
+    m.x0_lambdas = 0.4 * torch.rand(cfg.layers, generator=g) - 0.2
+    for lw in m.layers:
+        lw["q_gain"] = 0.5 + torch.rand(128, generator=g)
+        lw["k_gain"] = 0.5 + torch.rand(128, generator=g)
+        if "ve_gate" in lw:
+            lw["ve_gate"] = torch.randn(lw["ve_gate"].shape, generator=g) * 0.1
+            lw["ve"] = (torch.randn(lw["ve"].shape, generator=g) * 0.5).to(torch.bfloat16)
+    save_hf(m, tmp_path, max_positions=128)
+    loaded = load_hf(tmp_path, gpu)
+    assert loaded.mixes and loaded.cfg.windows == (16, 16, 16, -1)
+    check_against_cpu(gpu, loaded)
+
+
+def check_against_cpu(gpu, model):
     dev = gpu
     B, T, steps = 3, 40, 6
-    model = RandomModel(TINY, dev, seed=7)
-    prompts = np.random.default_rng(8).integers(0, TINY.vocab, (B, T)).astype(np.int32)
+    prompts = np.random.default_rng(8).integers(0, model.cfg.vocab, (B, T)).astype(np.int32)
     dec = Fp8Decoder(model, B, T - 1 + steps, dev, row_chunk=32)  # several row chunks in the prefill
     cpu = CpuModel(model, B, T - 1 + steps)
     dec.prefill(torch.from_numpy(prompts).to(dev))

@@ -77,8 +77,9 @@ def test_greedy_is_the_first_argmax_over_allowed_rows():
     from nanochat_amd.sampling import allow_rows
     zeros = np.zeros(B)
     tok, alt, pos = S.choose(x, temperature=np.zeros(B, np.float32), top_p=np.ones(B, np.float32),
-                             seed=zeros.astype(np.uint64), pos=np.arange(B, dtype=np.int32), first=zeros.astype(np.int32),
-                             masked=masked, allow=allow_rows(allow).view(np.uint32), lazy=5)
+                             seed=zeros.astype(np.uint64), pos=np.arange(B, dtype=np.int32),
+                             first=zeros.astype(np.int32), masked=masked, allow=allow_rows(allow).view(np.uint32),
+                             lazy=5)
     for b in range(B):
         ok = allow[b] if masked[b] else np.ones(V, bool)
         cand = np.where(ok, x[b], -np.inf)
