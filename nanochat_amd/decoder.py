@@ -199,6 +199,7 @@ class Fp8Decoder:
         self.choose_ws = choose_workspace(batch, cfg.vocab, device)
         self.alt = torch.empty(batch, dtype=torch.int32, device=device)
         self.temperature = self.top_p = self.seeds = self.first = None
+        self.slots = self.allow = None  # the choice's slot masks and allowed-token rows (serving.Server sets them)
         self.softcap, self.lazy = cfg.softcap, -1
         self.mixes = model.mixes
 
@@ -265,12 +266,17 @@ class Fp8Decoder:
         B, T = prompts.shape
         if B != self.batch or T - 1 + 1 > self.max_len:
             raise ValueError(f"prompts {tuple(prompts.shape)} do not fit batch {self.batch}, max_len {self.max_len}")
-        n = B * (T - 1)
-        if n == 0:
+        if T <= 1:
             return
         tok = prompts[:, :-1].reshape(-1)
         pos = torch.arange(T - 1, dtype=torch.int32, device=self.device).repeat(B)
         seq = torch.arange(B, dtype=torch.int32, device=self.device).repeat_interleave(T - 1)
+        self._prefill_rows(tok, pos, seq)
+
+    def _prefill_rows(self, tok: Tensor, pos: Tensor, seq: Tensor) -> None:
+        """Rows (token, position, sequence) into the caches, each row attending its sequence's keys up to its
+        position; every row of a layer is appended before any attends."""
+        n = tok.shape[0]
         x, h = self._embed(tok)
         x0 = x.clone() if self.mixes else None
         q = torch.empty((n, self.cfg.heads, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
@@ -308,8 +314,8 @@ class Fp8Decoder:
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
         logits = slot_gemm(x, self.lm_head, NORM_F32)
         choose_tokens(logits, self.cfg.vocab, pos, temperature=self.temperature, top_p=self.top_p, seed=self.seeds,
-                      first=self.first, softcap=self.softcap, lazy=self.lazy, tokens=out_tok, alt_tokens=self.alt,
-                      workspace=self.choose_ws)
+                      first=self.first, slots=self.slots, allow=self.allow, softcap=self.softcap, lazy=self.lazy,
+                      tokens=out_tok, alt_tokens=self.alt, workspace=self.choose_ws)
         return logits[:, :self.cfg.vocab]
 
     @torch.no_grad()

@@ -1,0 +1,170 @@
+"""Continuous batching over the decoder's slots: the host protocol of the reference's NativeDecoder.generate
+(inference/decoder.py:28-40,194-324) on this package's kernels.
+
+Requests queue for `batch` slots. A free slot takes the next request: its prompt but the last token is prefilled
+into the slot's cache rows (all newly admitted prompts in one prefill), the slot's token, position, first generated
+position and sampling parameters are set, and it joins the next decode step. Each step is one replay of a captured
+hipGraph over every slot: idle slots carry position -1, so the fused decode step does no work for them and the
+token choice (nc_choose_tokens' slot mask) leaves them untouched. After a step the host reads the choices and
+finishes a slot on BOS (dropped), at max_new_tokens, or when the request's stopping criteria hold for its tokens,
+then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
+constraints, decode.cu:1077-1094's dec_masks rows); a masked slot chooses among them, -1 when none is allowed.
+The reference's prompt store (pinned host copies of prompt KV for reuse, decode.cu:1053-1075) is not part of this.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Iterable, Iterator, Sequence
+
+import numpy as np
+import torch
+
+from nanochat_amd.decoder import Fp8Decoder, Weights
+from nanochat_amd.sampling import allow_rows, slot_masks
+
+
+@dataclass(frozen=True, kw_only=True)
+class Request:
+    """A continuation of input_ids (at least two tokens) by at most max_new_tokens (>= 1) tokens (inference/decoder.py
+    :28-40): temperature 0 argmax, > 0 a sample drawn from (seed, generated position) alone, top_p < 1 nucleus."""
+    input_ids: Sequence[int]
+    max_new_tokens: int
+    stopping_criteria: Callable[[list[int]], bool] | None = None
+    mask: Callable[[list[int]], np.ndarray | None] | None = None  # generated so far -> bool [vocab] or None
+    temperature: float = 0.0
+    top_p: float = 1.0
+    seed: int = 0
+
+
+@dataclass
+class _Slot:
+    index: int
+    request: Request
+    out: list
+
+
+class Server:
+    """`batch` slots over one Fp8Decoder; bos ends a continuation (inference/decoder.py:310-312)."""
+
+    def __init__(self, model: Weights, batch: int, max_len: int, device, bos: int):
+        self.dec = Fp8Decoder(model, batch, max_len, device)
+        self.batch, self.max_len, self.bos, self.device = batch, max_len, bos, device
+        vocab = model.cfg.vocab
+        B = batch
+        dev = device
+        self.tok = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.pos = torch.full((B,), -1, dtype=torch.int32, device=dev)
+        self.next = torch.zeros(B, dtype=torch.int32, device=dev)
+        d = self.dec
+        d.temperature = torch.zeros(B, dtype=torch.float32, device=dev)
+        d.top_p = torch.ones(B, dtype=torch.float32, device=dev)
+        d.seeds = torch.zeros(B, dtype=torch.int64, device=dev)
+        d.first = torch.zeros(B, dtype=torch.int32, device=dev)
+        d.slots = torch.zeros((2, (B + 63) // 64), dtype=torch.int64, device=dev)
+        d.allow = torch.zeros((B, (vocab + 31) // 32), dtype=torch.int32, device=dev)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.stream = torch.cuda.Stream(dev)
+
+    def _capture(self) -> None:
+        """The step graph: the decode step over every slot, then each slot's next input is its choice."""
+        s = self.stream
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            pos0 = self.pos.clone()
+            self.dec._step(self.tok, self.pos, self.next)  # warm every launch path (no slot is active yet)
+            self.pos.copy_(pos0)
+            s.synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=s):
+                self.dec._step(self.tok, self.pos, self.next)
+                self.tok.copy_(self.next)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+
+    @torch.no_grad()
+    def generate(self, requests: Iterable[Request]) -> Iterator[tuple[int, list[int]]]:
+        """Continuations of requests, consumed lazily; yields (request index, generated ids) in completion order."""
+        B, dev = self.batch, self.device
+        d = self.dec
+        if self.graph is None:
+            self._capture()
+        queue = enumerate(requests)
+        slots: list[_Slot | None] = [None] * B
+        admitted: list[int] = []
+
+        def fill(b: int) -> None:
+            for i, r in queue:
+                n = len(r.input_ids) - 1
+                if n < 1 or r.max_new_tokens < 1 or n + r.max_new_tokens > self.max_len:
+                    raise ValueError(f"request {i}: {n + 1} prompt tokens and {r.max_new_tokens} new tokens do not "
+                                     f"fit max_len {self.max_len}")
+                slots[b] = _Slot(i, r, [])
+                admitted.append(b)
+                return
+            slots[b] = None
+
+        for b in range(B):
+            fill(b)
+        while any(s is not None for s in slots):
+            with torch.cuda.stream(self.stream):
+                if admitted:
+                    self._admit(slots, admitted)
+                    admitted.clear()
+                masked = self._masks(slots)
+                d.slots.copy_(torch.from_numpy(slot_masks([s is not None for s in slots], masked)).to(dev))
+                self.graph.replay()
+                chosen = self.next.cpu().numpy()
+            finished = []
+            for b, s in enumerate(slots):
+                if s is None:
+                    continue
+                token = int(chosen[b])
+                if token == self.bos:
+                    finished.append(b)
+                    continue
+                if token < 0:
+                    raise ValueError(f"request {s.index}: its mask allows no token at position {len(s.out)}")
+                s.out.append(token)
+                r = s.request
+                if len(s.out) == r.max_new_tokens or (r.stopping_criteria and r.stopping_criteria(s.out)):
+                    finished.append(b)
+            if finished:
+                with torch.cuda.stream(self.stream):
+                    idle = torch.tensor(finished, dtype=torch.int64, device=dev)
+                    self.pos.index_fill_(0, idle, -1)
+                for b in finished:
+                    done = slots[b]
+                    fill(b)
+                    yield done.index, done.out
+
+    def _admit(self, slots, admitted) -> None:
+        """Prefill the admitted slots' prompts but their last tokens in one pass, then set their decode state."""
+        d, dev = self.dec, self.device
+        rows = [np.array([s.request.input_ids[:-1], range(len(s.request.input_ids) - 1),
+                          [b] * (len(s.request.input_ids) - 1)], dtype=np.int32)
+                for b in admitted for s in (slots[b],)]
+        rows = torch.from_numpy(np.concatenate(rows, axis=1)).to(dev)
+        d._prefill_rows(rows[0].contiguous(), rows[1].contiguous(), rows[2].contiguous())
+        for b in admitted:
+            r = slots[b].request
+            n = len(r.input_ids) - 1
+            self.tok[b] = int(r.input_ids[-1])
+            self.pos[b] = n
+            d.first[b] = n
+            d.temperature[b] = float(r.temperature)
+            d.top_p[b] = float(r.top_p)
+            d.seeds[b] = int(np.uint64(r.seed).view(np.int64))
+
+    def _masks(self, slots) -> list[bool]:
+        """Each masked slot's allowed-token row for its next position; returns which slots are masked."""
+        d = self.dec
+        masked = [False] * self.batch
+        for b, s in enumerate(slots):
+            if s is None or s.request.mask is None:
+                continue
+            allowed = s.request.mask(s.out)
+            if allowed is None:
+                continue
+            masked[b] = True
+            d.allow[b].copy_(torch.from_numpy(allow_rows(np.asarray(allowed, bool)[None])[0]).to(self.device))
+        return masked

@@ -1,0 +1,70 @@
+"""Continuous batching (serving.Server, the reference's NativeDecoder.generate protocol): more requests than slots,
+mixed prompt lengths, greedy and sampled, a masked request, BOS and stopping criteria. Every request's tokens are
+checked against a CPU restatement of the model run on that request alone (the decoder test's CpuModel): at each
+generated position the CPU logits' choice (greedy, or Gumbel-max with the request's seed and generated index) must
+equal the served token wherever the choice is clear of the logit tolerance."""
+
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.decoder import RandomModel
+from nanochat_amd.serving import Request, Server
+from oracle import sampling as S
+from test_gpu_decoder import LOGIT_ATOL, TINY, CpuModel
+
+pytestmark = pytest.mark.gpu
+
+BOS = 7
+
+
+def expected_choice(logits, r: Request, i: int, allowed):
+    """The oracle's choice on CPU logits, and whether it is clear of the tolerance."""
+    x = logits.astype(np.float32)
+    if allowed is not None:
+        x = np.where(allowed, x, -np.inf).astype(np.float32)
+    if r.temperature > 0:
+        score = S.capped(x, 15.0) / np.float32(r.temperature) + S.gumbel(r.seed, i, np.arange(len(x)))
+        tol = 2 * LOGIT_ATOL / r.temperature
+    else:
+        score, tol = x, 2 * LOGIT_ATOL
+    top2 = np.sort(score)[-2:]
+    return int(np.argmax(score)), bool(top2[1] - top2[0] > tol)
+
+
+def test_continuous_batching_matches_each_request_alone(gpu):
+    model = RandomModel(TINY, gpu, seed=21)
+    rng = np.random.default_rng(22)
+    lens, news = [6, 12, 25, 9, 30, 4, 17], [5, 3, 6, 8, 2, 7, 4]
+    temps = [0.0, 0.0, 0.8, 0.0, 1.2, 0.0, 0.5]
+    even = np.arange(TINY.vocab) % 2 == 0
+    reqs = []
+    for k, (n, m, t) in enumerate(zip(lens, news, temps)):
+        ids = [BOS] + rng.integers(8, TINY.vocab, n - 1).tolist()
+        mask = (lambda out: even) if k == 3 else None
+        stop = (lambda out: len(out) >= 2 and out[-1] == out[-2]) if k == 1 else None
+        reqs.append(Request(input_ids=ids, max_new_tokens=m, temperature=t, seed=1000 + k, mask=mask,
+                            stopping_criteria=stop))
+    server = Server(model, batch=3, max_len=48, device=gpu, bos=BOS)
+    got = dict(server.generate(reqs))
+    assert sorted(got) == list(range(len(reqs)))
+    checked = 0
+    for k, r in enumerate(reqs):
+        out = got[k]
+        assert 1 <= len(out) + (len(out) < r.max_new_tokens) and len(out) <= r.max_new_tokens
+        if r.mask is not None:
+            assert all(t % 2 == 0 for t in out)
+        cpu = CpuModel(model, 1, 48)
+        ids = np.array(r.input_ids, np.int32)
+        cpu.prefill(ids[None])
+        tok, p = ids[-1:], len(ids) - 1
+        stopped_early = len(out) < r.max_new_tokens and not (r.stopping_criteria and r.stopping_criteria(out))
+        for i in range(len(out) + stopped_early):
+            logits = cpu.step(tok, p)[0]
+            want, sure = expected_choice(logits, r, i, even if r.mask is not None else None)
+            served = out[i] if i < len(out) else BOS
+            if sure:
+                assert served == want, (k, i, served, want)
+                checked += 1
+            tok, p = np.array([served], np.int32), p + 1
+    assert checked >= 25, checked
