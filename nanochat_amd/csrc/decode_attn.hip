@@ -48,6 +48,7 @@
 #define DEC_THREADS 64
 #define DEC_MAX_G 16
 #define DEC_MAX_WAVES 8192  /* workspace slots are sized for this many waves */
+#define DEC_MERGE_DIRECT 8  /* pieces of a segment k_merge reads in its first round trip */
 #define DEC_MIN_CHUNK 8     /* pages per wave at least: fewer pieces to merge on small problems */
 #define DEC_LAZY 8.0f       /* log2 headroom before the softmax reference moves */
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
@@ -88,8 +89,9 @@ struct DecodeArgs {
     int B, hq, hkv, group;
     float score_scale;        /* sm_scale * log2(e) */
     bf16_t *out;              /* [B][hq][128] */
-    float *ws_o;              /* [DEC_MAX_WAVES + S][group][128]: the pieces' Σ p v, slot wave + segment */
-    float *ws_ml;             /* [DEC_MAX_WAVES + S][group][2] */
+    float *ws_o;              /* [slots][group][128]: the pieces' Σ p v (slot layout at merge_slot) */
+    float *ws_ml;             /* [slots][group][2]: their max and sum */
+    int2 *ws_desc;            /* [S]: each segment's piece count and first piece's wave */
     int max_ctx;              /* ctx_len is clamped to it */
     int unit_start, unit_end; /* schedule units a non-empty segment costs before its first and after its last page */
 };
@@ -477,10 +479,18 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
     }
 }
 
-/* Finish a piece of segment (b, h): the whole segment writes the normalised bf16 output; a part of it writes
- * (Σ p v in value units, max, sum) to slot w + b * hkv + h, which k_merge combines. Slots are unique: a wave's
- * pieces lie in consecutive segments and the waves' slices are in segment order, so w + s never repeats. */
-__device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, bool whole, int lane, State &st) {
+/* The workspace slot of piece i (the i-th wave to touch segment s, wave w): the first DEC_MERGE_DIRECT pieces of a
+ * segment sit together at s * DEC_MERGE_DIRECT + i, so k_merge reads them with the segment's descriptor in one
+ * round trip; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's pieces lie in consecutive segments and
+ * the waves' slices are in segment order, so w + s never repeats). */
+__device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, int w) {
+    const int S = a.B * a.hkv;
+    return i < DEC_MERGE_DIRECT ? (size_t)s * DEC_MERGE_DIRECT + i : (size_t)S * DEC_MERGE_DIRECT + w + s;
+}
+
+/* Finish piece `piece` of segment (b, h), wave w: the whole segment writes the normalised bf16 output; a part of it
+ * writes (Σ p v in value units, max, sum) to its merge slot, which k_merge combines. */
+__device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st) {
     const int n = lane & 15, j = lane >> 4;
     float l = st.l;
     l += shfl_xor_f(l, 16);
@@ -500,7 +510,7 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, bool whol
         }
         return;
     }
-    const size_t slot = (size_t)(w + b * a.hkv + h) * a.group + n;
+    const size_t slot = merge_slot(a, b * a.hkv + h, piece, w) * a.group + n;
     float *dst = a.ws_o + slot * NC_HEAD_DIM;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -528,6 +538,7 @@ __device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane,
         if (lds && b < a.B) lds[b] = c;
         if (zero_rows && a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
         if (zero_rows && b < a.B && pg == 0 && b % W == w) {
+            for (int h = 0; h < a.hkv; h++) a.ws_desc[b * a.hkv + h] = make_int2(0, 0); /* nothing to merge */
             const uint32_t f = c < 0 ? 0x7fc07fc0u : 0u;
             const u32x4 z = {f, f, f, f};
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
@@ -571,15 +582,21 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     }
     const long long into = start - carry; /* flattened offset inside sequence b */
     int h = (int)(into / units_b), off = (int)(into % units_b);
+    long long seg_base = start - off; /* the segment's first unit in the flattened list */
 
     while (remaining > 0) {
         const SeqRange sr = seq_range_of(a, ctx_at(a, lds, b));
         const int seg_pages = sr.last - sr.first + 1;
         /* this slice takes units [off, off + take) of the segment; its pages are [lo, hi) */
-        const int take = (int)min((long long)(seg_pages + a.unit_start + a.unit_end - off), remaining);
+        const int units = seg_pages + a.unit_start + a.unit_end;
+        const int take = (int)min((long long)(units - off), remaining);
         const int lo = max(off - a.unit_start, 0), hi = min(off + take - a.unit_start, seg_pages);
+        /* the waves holding the segment's first and last pages: piece i of the segment is wave w_first + i */
+        const long long page0 = seg_base + a.unit_start;
+        const int w_first = (int)(page0 / chunk), pieces = (int)((page0 + seg_pages - 1) / chunk) - w_first + 1;
         remaining -= take;
         off = 0;
+        seg_base += units;
         if (hi > lo) {
             bf16x8 qop[4]; /* the fused step builds it in attend_run */
             if constexpr (!FUSED) {
@@ -596,7 +613,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             State st;
             state_init(st);
             attend_run<FUSED>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
-            finish_piece(a, b, h, w, lo == 0 && hi == seg_pages, lane, st);
+            finish_piece(a, b, h, w, w - w_first, lo == 0 && hi == seg_pages, lane, st);
+            if (lo == 0 && lane == 0) a.ws_desc[b * a.hkv + h] = make_int2(pieces, w_first);
             if (FUSED && hi == seg_pages) store_new_kv(a, h, sr.p, lane, sm);
         }
         if (++h == a.hkv) {
@@ -609,67 +627,57 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     }
 }
 
-/* One wave per segment (b, h) = blockIdx.x: combine the pieces of a segment that more than one wave touched
- * (pieces are waves floor(seg_lo / chunk) .. floor((seg_hi - 1) / chunk), slots wave + segment), weights
- * exp2(m_k - max m) as decode.cu:547-548's rescale, combined online. Lane (j, n) produces dims 32j..32j+31 of head
- * n. The kernel is latency-bound: one pass over the context lengths gives the schedule, then the pieces' partial
- * results are loaded 4 at a time, every load of a batch in flight together. */
-__global__ void __launch_bounds__(DEC_THREADS) k_merge(DecodeArgs a, int W) {
-    const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
-    long long total = 0, before = 0; /* units of every sequence, of the sequences before b */
-    int units = 0;
-    for (int base = 0; base < a.B; base += 64) {
-        const int bb = base + lane;
-        const int pg = bb < a.B ? units_of(a, seq_ctx(a, bb)) : 0;
-        total += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
-        before += __shfl(wave_inclusive_sum(bb < b ? pg : 0, lane), 63, 64);
-        if (b >= base && b < base + 64) units = __shfl(pg, b - base, 64);
+/* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
+ * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale, combined online. Thread t holds head t / 16,
+ * dims 8 (t % 16)..+8 (16 lanes per head, ceil(G / 4) waves). The kernel is latency-bound, so it needs no schedule:
+ * the segment's descriptor (piece count, first wave) and the first DEC_MERGE_DIRECT pieces' slots are loaded
+ * together, in one round trip; a segment with more pieces reads the rest in a second. */
+#define MERGE_LANES 16
+
+__global__ void __launch_bounds__(256) k_merge(DecodeArgs a) {
+    const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, n = t / MERGE_LANES, c = t % MERGE_LANES;
+    if (n >= a.group) return; /* whole 16-lane groups */
+    const int2 d = a.ws_desc[s];
+    f32x2 ml[DEC_MERGE_DIRECT];
+    f32x4 ov[DEC_MERGE_DIRECT][2];
+#pragma unroll
+    for (int k = 0; k < DEC_MERGE_DIRECT; k++) { /* speculative: slots past the piece count are not used */
+        const size_t slot = ((size_t)s * DEC_MERGE_DIRECT + k) * a.group + n;
+        ml[k] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
+        ov[k][0] = src[0];
+        ov[k][1] = src[1];
     }
-    if (units <= 0) return;
-    total *= a.hkv;
-    const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
-    /* the segment's pages in schedule units */
-    const long long seg_lo = before * a.hkv + (long long)h * units + a.unit_start;
-    const long long seg_hi = seg_lo + units - a.unit_start - a.unit_end;
-    const int w_first = (int)(seg_lo / chunk), w_last = (int)((seg_hi - 1) / chunk);
-    if (w_first == w_last || n >= a.group) return; /* one piece: k_decode wrote the output */
-    float mmax = DEC_M_INIT, sum = 0.f, acc[32];
+    const int pieces = d.x;
+    if (pieces <= 1) return; /* one piece: k_decode wrote the output; none: an empty sequence's zero row */
+    float mmax = DEC_M_INIT, sum = 0.f, acc[8];
 #pragma unroll
-    for (int e = 0; e < 32; e++) acc[e] = 0.f;
-    for (int k0 = w_first; k0 <= w_last; k0 += 4) {
-        f32x2 ml[4];
-        f32x4 ov[4][8];
+    for (int e = 0; e < 8; e++) acc[e] = 0.f;
+    auto fold = [&](f32x2 m_l, const f32x4 &o0, const f32x4 &o1) {
+        const float m_new = fmaxf(mmax, m_l[0]);
+        const float a_old = __builtin_amdgcn_exp2f(mmax - m_new), a_new = __builtin_amdgcn_exp2f(m_l[0] - m_new);
+        sum = sum * a_old + m_l[1] * a_new;
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const int k = min(k0 + p, w_last); /* a short batch re-reads the last piece: weight 0 below */
-            const size_t slot = (size_t)(k + s) * a.group + n;
-            ml[p] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
-            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 32 * j);
-#pragma unroll
-            for (int c = 0; c < 8; c++) ov[p][c] = src[c];
+        for (int e = 0; e < 4; e++) {
+            acc[e] = acc[e] * a_old + o0[e] * a_new;
+            acc[4 + e] = acc[4 + e] * a_old + o1[e] * a_new;
         }
+        mmax = m_new;
+    };
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            if (k0 + p > w_last) break;
-            const float m_new = fmaxf(mmax, ml[p][0]);
-            const float a_old = __builtin_amdgcn_exp2f(mmax - m_new), a_new = __builtin_amdgcn_exp2f(ml[p][0] - m_new);
-            sum = sum * a_old + ml[p][1] * a_new;
-#pragma unroll
-            for (int c = 0; c < 8; c++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[4 * c + e] = acc[4 * c + e] * a_old + ov[p][c][e] * a_new;
-            mmax = m_new;
-        }
+    for (int k = 0; k < DEC_MERGE_DIRECT; k++)
+        if (k < pieces) fold(ml[k], ov[k][0], ov[k][1]);
+    for (int k = DEC_MERGE_DIRECT; k < pieces; k++) {
+        const size_t slot = merge_slot(a, s, k, d.y + k) * a.group + n;
+        const f32x2 m_l = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
+        fold(m_l, src[0], src[1]);
     }
     const float inv = sum > 0.f ? 1.0f / sum : 0.f;
-    bf16_t *dst = a.out + ((size_t)b * a.hq + h * a.group + n) * NC_HEAD_DIM + 32 * j;
+    float v[8];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = acc[8 * c + e] * inv;
-        store_bf16x8(dst + 8 * c, v);
-    }
+    for (int e = 0; e < 8; e++) v[e] = acc[e] * inv;
+    store_bf16x8(a.out + ((size_t)b * a.hq + h * a.group + n) * NC_HEAD_DIM + 8 * c, v);
 }
 
 /* Resident single-wave workgroups of k_decode on the current device (cached per device). */
@@ -713,10 +721,14 @@ static void schedule_units(int *start, int *end) {
     *end = e;
 }
 
+/* Partial-result slots: the first DEC_MERGE_DIRECT pieces of every segment, then one per (wave, segment) offset. */
+static size_t merge_slots(size_t S) { return S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S; }
+
 extern "C" long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx) {
     if (B <= 0 || hq <= 0 || hkv <= 0 || max_ctx <= 0 || hq % hkv) return 0;
-    const size_t S = (size_t)B * hkv, G = hq / hkv, slots = DEC_MAX_WAVES + S;
-    return (long long)(align256(slots * G * NC_HEAD_DIM * sizeof(float)) + slots * G * 2 * sizeof(float));
+    const size_t S = (size_t)B * hkv, G = hq / hkv, slots = merge_slots(S);
+    return (long long)(align256(slots * G * NC_HEAD_DIM * sizeof(float)) + align256(slots * G * 2 * sizeof(float)) +
+                       S * sizeof(int2));
 }
 
 /* Checks shared by both entry points, then the launch of k_decode<FUSED> and k_merge. */
@@ -740,9 +752,13 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     a.score_scale = sm_scale * 1.4426950408889634f;
     a.out = (bf16_t *)out;
     a.max_ctx = max_ctx;
-    const size_t S = (size_t)B * hkv, slots = DEC_MAX_WAVES + S;
-    a.ws_o = (float *)workspace;
-    a.ws_ml = (float *)((unsigned char *)workspace + align256(slots * a.group * NC_HEAD_DIM * sizeof(float)));
+    const size_t S = (size_t)B * hkv, slots = merge_slots(S);
+    unsigned char *ws = (unsigned char *)workspace;
+    a.ws_o = (float *)ws;
+    ws += align256(slots * a.group * NC_HEAD_DIM * sizeof(float));
+    a.ws_ml = (float *)ws;
+    ws += align256(slots * a.group * 2 * sizeof(float));
+    a.ws_desc = (int2 *)ws;
     schedule_units(&a.unit_start, &a.unit_end);
     const int W = decode_waves();
     if (fused)
@@ -750,7 +766,8 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else
         hipLaunchKernelGGL(k_decode<false>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(DEC_THREADS), 0, (hipStream_t)stream, a, W);
+    const unsigned merge_threads = (unsigned)(((a.group * MERGE_LANES + NC_WAVE - 1) / NC_WAVE) * NC_WAVE);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(merge_threads), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
     return 0;
 }
