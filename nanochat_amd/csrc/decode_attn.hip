@@ -60,10 +60,10 @@
  * rows and the append's quantisation; the same in both entry points, so that they split the work alike and give
  * bit-identical outputs). */
 #ifndef DEC_UNITS_START
-#define DEC_UNITS_START 3
+#define DEC_UNITS_START 4
 #endif
 #ifndef DEC_UNITS_END
-#define DEC_UNITS_END 6
+#define DEC_UNITS_END 10
 #endif
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 1 /* one wave per SIMD: no older/younger wave competing for issue on a SIMD */
