@@ -8,12 +8,12 @@
  * included. Rows may come in any order and from any sequences; the kernel is fastest when a sequence's rows are
  * consecutive.
  *
- * Work: one workgroup of 4 waves per (kv head h, tile of 16 R consecutive rows), R = floor(16 / G) rows per
- * 16-column MFMA block, G = Hq / Hkv. A wave holds 4 blocks; column n of a block is (row n / G, query head
- * h G + n % G), so the G heads of a row share every key read. The workgroup walks the pages of the union key
- * range of its rows in pairs; all four waves consume the same pair from LDS.
+ * Work: one workgroup of 8 waves (two per SIMD) per (kv head h, tile of 16 R consecutive rows), R = floor(16 / G)
+ * rows per 16-column MFMA block, G = Hq / Hkv. A wave holds 2 blocks; column n of a block is (row n / G, query
+ * head h G + n % G), so the G heads of a row share every key read. The workgroup walks the pages of the union key
+ * range of its rows in pairs; all eight waves consume the same pair from LDS.
  *
- * Per page pair (32 keys) a wave computes, for each of its 4 blocks,
+ * Per page pair (32 keys) a wave computes, for each of its 2 blocks,
  *   scores  Sᵀ[16 keys][16 columns] per page = K · Qᵀ on fp8 MFMAs: v_mfma_scale_f32_16x16x128_f8f6f4 takes the
  *           page's e4m3 K codes as they are (A: key lane % 16, dims 32 (lane / 16) .. + 31, all 128 dims in one
  *           instruction) against q split into two e4m3 terms, q 2^e = hi + lo (hi = e4m3(q 2^e), lo = e4m3 of the
@@ -36,7 +36,9 @@
  * Software pipeline: iteration k issues the score MFMAs of pair k + 1 and, independent of them, the softmax and
  * the value MFMAs of pair k. A wave's VALU work does not issue under its own MFMAs on gfx950 (measured: an MFMA
  * plus 4 independent v_mul cost their sum), but it does under the other wave's on the same SIMD; the pipeline
- * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps.
+ * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps, and the MFMA bursts
+ * run at raised wave priority (s_setprio 1) so that the other wave's VALU fills them (config 4: 187-190 us against
+ * 191-192 us without).
  */
 #include "layout.h"
 
@@ -279,6 +281,7 @@ __device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32
                                                      k.a1[3]});
     const i32x8 kb = __builtin_bit_cast(i32x8, u32x8{k.b0[0], k.b0[1], k.b0[2], k.b0[3], k.b1[0], k.b1[1], k.b1[2],
                                                      k.b1[3]});
+    __builtin_amdgcn_s_setprio(1); /* MFMA bursts issue ahead of the other wave's VALU, which fills their cycles */
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -287,6 +290,7 @@ __device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32
         s[bl][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, q8[bl].lo, sa, 0, 0, 0, 127, 0, q8[bl].scale);
         s[bl][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kb, q8[bl].lo, sb, 0, 0, 0, 127, 0, q8[bl].scale);
     }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 /* Softmax and value MFMAs of a pair whose scores are s (keys of pages page0, page0 + 1 with blocks ida, idb) and
@@ -383,6 +387,7 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
 #pragma unroll
         for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vw[i]);
     }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int bb = 0; bb < 8; bb++) {
         const uint32_t wa = bb < 4 ? v.a0[bb] : v.a1[bb - 4];
@@ -392,6 +397,7 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
         for (int bl = 0; bl < PF_BLOCKS; bl++)
             st.o[bl][bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pp[bl], st.o[bl][bb], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 __device__ __forceinline__ bool row_valid(const PrefillArgs &a, int p, int s) {
