@@ -9,7 +9,12 @@ token choice (nc_choose_tokens' slot mask) leaves them untouched. After a step t
 finishes a slot on BOS (dropped), at max_new_tokens, or when the request's stopping criteria hold for its tokens,
 then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
 constraints, decode.cu:1077-1094's dec_masks rows); a masked slot chooses among them, -1 when none is allowed.
-The reference's prompt store (pinned host copies of prompt KV for reuse, decode.cu:1053-1075) is not part of this.
+
+The prompt store (decode.cu:1053-1075; inference/decoder.py:196-232): pinned host memory for `prompt_store`
+positions. A prefilled prompt's cache pages (every layer's fp8 codes and scales of the slot's first ceil(n / 16)
+pages) are copied there once, in order, never evicted; a later request with the same input_ids loads them into its
+slot instead of prefilling. Positions of a loaded last page past the prompt hold whatever the stored slot held:
+they are appended before any step attends them.
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ import numpy as np
 import torch
 
 from nanochat_amd.decoder import Fp8Decoder, Weights
+from nanochat_amd.kv_cache import PAGE
 from nanochat_amd.sampling import allow_rows, slot_masks
 
 
@@ -47,9 +53,16 @@ class _Slot:
 class Server:
     """`batch` slots over one Fp8Decoder; bos ends a continuation (inference/decoder.py:310-312)."""
 
-    def __init__(self, model: Weights, batch: int, max_len: int, device, bos: int):
+    def __init__(self, model: Weights, batch: int, max_len: int, device, bos: int, prompt_store: int = 0):
         self.dec = Fp8Decoder(model, batch, max_len, device)
         self.batch, self.max_len, self.bos, self.device = batch, max_len, bos, device
+        caches = self.dec.caches
+        self.store_pages = prompt_store // PAGE
+        self.store = torch.empty((len(caches), self.store_pages) + tuple(caches[0].pages.shape[1:]), dtype=torch.uint8,
+                                 pin_memory=True) if self.store_pages else None
+        self.stored: dict[tuple[int, ...], int] = {}  # prompt -> its first store page
+        self.used = 0
+        self.loads = 0
         vocab = model.cfg.vocab
         B = batch
         dev = device
@@ -137,14 +150,34 @@ class Server:
                     fill(b)
                     yield done.index, done.out
 
+    def _pages(self, l: int, b: int, n: int) -> torch.Tensor:
+        """Slot b's first ceil(n / 16) pages of layer l (a contiguous cache: the slot's blocks are consecutive)."""
+        mb = self.dec.caches[l].max_blocks
+        return self.dec.caches[l].pages[b * mb:b * mb + -(-n // PAGE)]
+
     def _admit(self, slots, admitted) -> None:
-        """Prefill the admitted slots' prompts but their last tokens in one pass, then set their decode state."""
+        """Load stored prompts, prefill the others but their last tokens in one pass (then store them), and set the
+        admitted slots' decode state."""
         d, dev = self.dec, self.device
-        rows = [np.array([s.request.input_ids[:-1], range(len(s.request.input_ids) - 1),
-                          [b] * (len(s.request.input_ids) - 1)], dtype=np.int32)
-                for b in admitted for s in (slots[b],)]
-        rows = torch.from_numpy(np.concatenate(rows, axis=1)).to(dev)
-        d._prefill_rows(rows[0].contiguous(), rows[1].contiguous(), rows[2].contiguous())
+        fresh = []
+        for b in admitted:
+            ids = tuple(int(t) for t in slots[b].request.input_ids)
+            at = self.stored.get(ids)
+            if at is None:
+                fresh.append(b)
+                continue
+            n = len(ids) - 1
+            for l in range(len(d.caches)):
+                self._pages(l, b, n).copy_(self.store[l, at:at + -(-n // PAGE)], non_blocking=True)
+            self.loads += 1
+        if fresh:
+            rows = [np.array([s.request.input_ids[:-1], range(len(s.request.input_ids) - 1),
+                              [b] * (len(s.request.input_ids) - 1)], dtype=np.int32)
+                    for b in fresh for s in (slots[b],)]
+            rows = torch.from_numpy(np.concatenate(rows, axis=1)).to(dev)
+            d._prefill_rows(rows[0].contiguous(), rows[1].contiguous(), rows[2].contiguous())
+            for b in fresh:
+                self._save(b, tuple(int(t) for t in slots[b].request.input_ids))
         for b in admitted:
             r = slots[b].request
             n = len(r.input_ids) - 1
@@ -154,6 +187,17 @@ class Server:
             d.temperature[b] = float(r.temperature)
             d.top_p[b] = float(r.top_p)
             d.seeds[b] = int(np.uint64(r.seed).view(np.int64))
+
+    def _save(self, b: int, ids: tuple[int, ...]) -> None:
+        """Keep slot b's prompt pages in the store's next free pages, unless stored already or out of room."""
+        n = len(ids) - 1
+        pages = -(-n // PAGE)
+        if self.store is None or ids in self.stored or self.used + pages > self.store_pages:
+            return
+        for l in range(len(self.dec.caches)):
+            self.store[l, self.used:self.used + pages].copy_(self._pages(l, b, n), non_blocking=True)
+        self.stored[ids] = self.used
+        self.used += pages
 
     def _masks(self, slots) -> list[bool]:
         """Each masked slot's allowed-token row for its next position; returns which slots are masked."""

@@ -68,3 +68,23 @@ def test_continuous_batching_matches_each_request_alone(gpu):
                 checked += 1
             tok, p = np.array([served], np.int32), p + 1
     assert checked >= 25, checked
+
+
+def test_prompt_store_loads_instead_of_prefilling(gpu):
+    """A repeated prompt is loaded from the pinned prompt store (decode.cu:1053-1075) instead of prefilled, and
+    decodes exactly as the first time (one slot: the same schedule every step); a prompt past the store's room is
+    prefilled each time."""
+    model = RandomModel(TINY, gpu, seed=31)
+    rng = np.random.default_rng(32)
+    a = [BOS] + rng.integers(8, TINY.vocab, 37).tolist()   # 38 tokens: 3 pages of prompt positions
+    b = [BOS] + rng.integers(8, TINY.vocab, 20).tolist()
+    big = [BOS] + rng.integers(8, TINY.vocab, 40).tolist()
+    reqs = [Request(input_ids=ids, max_new_tokens=5) for ids in (a, b, a, big, a, big)]
+    server = Server(model, batch=1, max_len=48, device=gpu, bos=BOS, prompt_store=5 * 16)
+    out = dict(server.generate(reqs))
+    assert server.loads == 2          # a twice; b stored too (2 pages), big (3 pages) no longer fits
+    assert set(server.stored) == {tuple(a), tuple(b)}
+    assert out[0] == out[2] == out[4]
+    assert out[3] == out[5]
+    plain = Server(model, batch=1, max_len=48, device=gpu, bos=BOS)
+    assert dict(plain.generate(reqs[:1]))[0] == out[0]
