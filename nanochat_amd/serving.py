@@ -6,8 +6,9 @@ into the slot's cache rows (all newly admitted prompts in one prefill), the slot
 position and sampling parameters are set, and it joins the next decode step. Each step is one replay of a captured
 hipGraph over every slot: idle slots carry position -1, so the fused decode step does no work for them and the
 token choice (nc_choose_tokens' slot mask) leaves them untouched. After a step the host reads the choices and
-finishes a slot on BOS (dropped), at max_new_tokens, or when the request's stopping criteria hold for its tokens,
-then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
+finishes a slot on BOS (dropped; unless the request's accept_bos rejects it, when the step's alternative, the best
+token but BOS, is taken instead, as the reference's lazy BOS), at max_new_tokens, or when the request's stopping
+criteria hold for its tokens, then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
 constraints, decode.cu:1077-1094's dec_masks rows); a masked slot chooses among them, -1 when none is allowed.
 
 The prompt store (decode.cu:1053-1075; inference/decoder.py:196-232): pinned host memory for `prompt_store`
@@ -38,6 +39,7 @@ class Request:
     max_new_tokens: int
     stopping_criteria: Callable[[list[int]], bool] | None = None
     mask: Callable[[list[int]], np.ndarray | None] | None = None  # generated so far -> bool [vocab] or None
+    accept_bos: Callable[[list[int]], bool] | None = None  # False: a chosen BOS gives way to the alternative
     temperature: float = 0.0
     top_p: float = 1.0
     seed: int = 0
@@ -63,6 +65,8 @@ class Server:
         self.stored: dict[tuple[int, ...], int] = {}  # prompt -> its first store page
         self.used = 0
         self.loads = 0
+        self.dec.lazy = bos  # every choice also reports its best row but BOS (the alternative)
+        self.alts_taken = 0
         vocab = model.cfg.vocab
         B = batch
         dev = device
@@ -127,11 +131,19 @@ class Server:
                 d.slots.copy_(torch.from_numpy(slot_masks([s is not None for s in slots], masked)).to(dev))
                 self.graph.replay()
                 chosen = self.next.cpu().numpy()
+                alts = d.alt.cpu().numpy()
             finished = []
             for b, s in enumerate(slots):
                 if s is None:
                     continue
                 token = int(chosen[b])
+                if token == self.bos and s.request.accept_bos and not s.request.accept_bos(s.out):
+                    token = int(alts[b])  # the host rejects the lazy BOS (inference/decoder.py:233-248)
+                    if token < 0:
+                        raise ValueError(f"request {s.index}: nothing but BOS allowed at position {len(s.out)}")
+                    with torch.cuda.stream(self.stream):
+                        self.tok[b] = token  # the next input: the alternative (dec_take_alt)
+                    self.alts_taken += 1
                 if token == self.bos:
                     finished.append(b)
                     continue

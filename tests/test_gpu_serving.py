@@ -88,3 +88,22 @@ def test_prompt_store_loads_instead_of_prefilling(gpu):
     assert out[3] == out[5]
     plain = Server(model, batch=1, max_len=48, device=gpu, bos=BOS)
     assert dict(plain.generate(reqs[:1]))[0] == out[0]
+
+
+def test_rejected_bos_takes_the_alternative(gpu):
+    """Masks allowing only BOS and one token x, and a request that never accepts BOS: every chosen BOS gives way to
+    the choice's alternative, so the continuation is x repeated to max_new_tokens."""
+    model = RandomModel(TINY, gpu, seed=41)
+    rng = np.random.default_rng(42)
+    reqs = []
+    for k in range(6):
+        allowed = np.zeros(TINY.vocab, bool)
+        x = 100 + 37 * k
+        allowed[[BOS, x]] = True
+        reqs.append(Request(input_ids=[BOS] + rng.integers(8, TINY.vocab, 12).tolist(), max_new_tokens=4,
+                            mask=lambda out, m=allowed: m, accept_bos=lambda out: False))
+    server = Server(model, batch=3, max_len=32, device=gpu, bos=BOS)
+    out = dict(server.generate(reqs))
+    for k in range(6):
+        assert out[k] == [100 + 37 * k] * 4, (k, out[k])
+    assert server.alts_taken > 0
