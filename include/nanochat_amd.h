@@ -150,6 +150,16 @@ int nc_choose_tokens(const float *logits, int B, int vocab, long long ld, const 
  * model/modeling.py:47-49. */
 int nc_add_rms_norm_bf16(const void *x, const void *delta, void *x_out, void *y, int rows, int d, void *stream);
 
+/* The value-embedding mix of a layer's projection rows, in place: per row r, n = bf16(x[r] rstd) (x: the layer
+ * input, bf16 [rows][x_stride], d columns; the norm of nc_add_rms_norm_bf16), per kv head h
+ * g = 2 sigmoid(gate[h] . n) (gate fp32 [hkv][d]), then v_h = bf16(v_h + g ve[tok[r]]_h) on the row's v heads
+ * (qkv bf16 [rows][row_stride]: hq q heads, hkv k heads, hkv v heads; ve bf16 [vocab][hkv 128]). A row whose token
+ * is outside [0, vocab) is left as is. d % 8 == 0, d <= 8192, hkv <= 64.
+ * Replaces: the VE term of attn_prologue, model/kernels/decode.cu:476-493 (inference/modeling_nanochat.py:85-88). */
+int nc_value_embed_bf16(void *qkv, long long row_stride, const void *x, long long x_stride, const int32_t *tok,
+                        const void *ve, long long vocab, const float *gate, int rows, int d, int hq, int hkv,
+                        void *stream);
+
 /* out = bf16(relu(in)^2) over n bf16 (n % 8 == 0); out may be in.
  * Replaces: the RELU2 epilogue of the slot GEMM, model/kernels/decode.cu:174-178. */
 int nc_relu2_bf16(const void *in, void *out, long long n, void *stream);

@@ -1,5 +1,6 @@
 /*
- * Row kernels of the decoder's layer body: the residual add fused with the RMS norm, and the MLP's ReLU^2.
+ * Row kernels of the decoder's layer body: the residual add fused with the RMS norm, the MLP's ReLU^2, and the
+ * value-embedding mix.
  * Reference: the slot GEMM's RESID epilogue (out = bf16(s + res)) with k_rstd (r = rsqrt(Σ x² / K + FLT_EPSILON)),
  * and the RELU2 epilogue (bf16(relu(p) p)), model/kernels/decode.cu:107-123,169-184,447-456; the model's norm,
  * model/modeling.py:47-49. Here the weight GEMMs are library GEMMs, so these run as their own bandwidth-bound
@@ -7,6 +8,11 @@
  *
  * add_rms_norm: x_out = bf16(x + delta) (delta NULL: x_out = x), y = bf16(x_out * r), r = 1 / sqrt(Σ x_out² / d +
  * FLT_EPSILON) over the rounded x_out, Σ in fp32 (thread partials, then a fixed wave and workgroup tree).
+ *
+ * value_embed (a value-embedding layer's v, reference: attn_prologue, model/kernels/decode.cu:476-493;
+ * inference/modeling_nanochat.py:85-88): per row, n = bf16(x r) exactly as add_rms_norm (the same sums), per kv head
+ * g = 2 sigmoid(Σ_c n_c gate[h][c]) (fp32, a fixed lane order), then v = bf16(v + g ve[token]) in the projection
+ * row, in place (fp32 product and sum, one rounding). One workgroup per row: the normed row in LDS, a wave per head.
  */
 #include "common.h"
 
@@ -57,6 +63,68 @@ __global__ void __launch_bounds__(RN_THREADS) k_add_rms_norm(const bf16_t *x, co
     }
 }
 
+#define VE_MAX_HEADS 64
+
+__global__ void __launch_bounds__(RN_THREADS) k_value_embed(bf16_t *qkv, long long row_stride, const bf16_t *x,
+                                                            long long x_stride, const int32_t *tok, const bf16_t *ve,
+                                                            long long vocab, const float *gate, int d, int hq,
+                                                            int hkv) {
+    __shared__ float part[RN_THREADS / NC_WAVE];
+    __shared__ float nrow[8 * RN_THREADS * RN_MAX_CHUNKS];
+    __shared__ float g[VE_MAX_HEADS];
+    const int row = blockIdx.x, tid = threadIdx.x, chunks = d / 8, lane = tid & (NC_WAVE - 1);
+    const int t = tok[row];
+    if (t < 0 || t >= vocab) return; /* no table row: v stays as projected */
+    const bf16_t *xr = x + (size_t)row * x_stride;
+    float v[RN_MAX_CHUNKS][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+        load_bf16x8(xr + 8 * c, v[k]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += v[k][e] * v[k][e];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+    if (lane == 0) part[tid / NC_WAVE] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < RN_THREADS / NC_WAVE; w++) total += part[w];
+    const float r = 1.0f / sqrtf(total / (float)d + 1.1920928955078125e-07f);
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+#pragma unroll
+        for (int e = 0; e < 8; e++) nrow[8 * c + e] = bf16_to_f32(f32_to_bf16(v[k][e] * r));
+    }
+    __syncthreads();
+    for (int h = tid / NC_WAVE; h < hkv; h += RN_THREADS / NC_WAVE) {
+        const float *gh = gate + (size_t)h * d;
+        float dot = 0.f;
+        for (int c = lane; c < d; c += NC_WAVE) dot += nrow[c] * gh[c];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) dot += shfl_xor_f(dot, m);
+        if (lane == 0) g[h] = 2.0f / (1.0f + expf(-dot));
+    }
+    __syncthreads();
+    bf16_t *vr = qkv + (size_t)row * row_stride + (size_t)(hq + hkv) * NC_HEAD_DIM;
+    const bf16_t *er = ve + (size_t)t * hkv * NC_HEAD_DIM;
+    for (int c = tid; c < hkv * NC_HEAD_DIM / 8; c += RN_THREADS) {
+#pragma clang fp contract(off)
+        float vv[8], ev[8];
+        load_bf16x8(vr + 8 * c, vv);
+        load_bf16x8(er + 8 * c, ev);
+        const float gh = g[(8 * c) / NC_HEAD_DIM];
+#pragma unroll
+        for (int e = 0; e < 8; e++) vv[e] = vv[e] + gh * ev[e];
+        store_bf16x8(vr + 8 * c, vv);
+    }
+}
+
 __global__ void __launch_bounds__(RN_THREADS) k_relu2(const bf16_t *in, bf16_t *out, /* may be in */
                                                       long long n8) {
     const long long stride = (long long)gridDim.x * RN_THREADS;
@@ -97,6 +165,27 @@ extern "C" int nc_relu2_bf16(const void *in, void *out, long long n, void *strea
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(k_relu2, dim3((unsigned)blocks), dim3(RN_THREADS), 0, (hipStream_t)stream, (const bf16_t *)in,
                        (bf16_t *)out, n8);
+    NC_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int nc_value_embed_bf16(void *qkv, long long row_stride, const void *x, long long x_stride,
+                                   const int32_t *tok, const void *ve, long long vocab, const float *gate, int rows,
+                                   int d, int hq, int hkv, void *stream) {
+    NC_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 8 * RN_THREADS * RN_MAX_CHUNKS,
+               "nc_value_embed_bf16: rows %d, d %d (d a multiple of 8, at most %d)", rows, d,
+               8 * RN_THREADS * RN_MAX_CHUNKS);
+    NC_REQUIRE(hq > 0 && hkv > 0 && hkv <= VE_MAX_HEADS && hq % hkv == 0,
+               "nc_value_embed_bf16: hq %d, hkv %d (hkv <= %d dividing hq)", hq, hkv, VE_MAX_HEADS);
+    NC_REQUIRE(row_stride >= (long long)(hq + 2 * hkv) * NC_HEAD_DIM && row_stride % 8 == 0 && x_stride >= d &&
+                   x_stride % 8 == 0,
+               "nc_value_embed_bf16: row_stride %lld, x_stride %lld", row_stride, x_stride);
+    NC_REQUIRE(vocab > 0, "nc_value_embed_bf16: vocab %lld", vocab);
+    if (rows == 0) return 0;
+    NC_REQUIRE(qkv && x && tok && ve && gate, "nc_value_embed_bf16: null pointer");
+    NC_REQUIRE(((uintptr_t)qkv | (uintptr_t)x | (uintptr_t)ve) % 16 == 0, "nc_value_embed_bf16: 16-byte alignment");
+    hipLaunchKernelGGL(k_value_embed, dim3(rows), dim3(RN_THREADS), 0, (hipStream_t)stream, (bf16_t *)qkv, row_stride,
+                       (const bf16_t *)x, x_stride, tok, (const bf16_t *)ve, vocab, gate, d, hq, hkv);
     NC_LAUNCH_CHECK();
     return 0;
 }

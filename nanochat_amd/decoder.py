@@ -176,6 +176,28 @@ def relu2(x: Tensor) -> Tensor:
     return x
 
 
+def value_embed(qkv: Tensor, x: Tensor, tok: Tensor, ve: Tensor, gate: Tensor, hq: int, hkv: int) -> Tensor:
+    """nc_value_embed_bf16: in the v heads of the projection rows qkv (bf16 [rows][>= (hq + 2 hkv) 128]),
+    v_h = bf16(v_h + 2 sigmoid(gate[h] . norm(x)) ve[tok]_h) (inference/modeling_nanochat.py:85-88). x: the layer
+    input rows (bf16 [rows][d]); ve bf16 [vocab][hkv 128]; gate fp32 [hkv][d]. Rows whose token is outside the
+    vocabulary are left as they are."""
+    rows, d = x.shape
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.shape[0] != rows or qkv.stride(1) != 1:
+        raise ValueError("qkv must be bf16 [rows][cols] with unit column stride")
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be bf16 with unit column stride")
+    _require(ve, "ve", torch.bfloat16, 2)
+    _require(gate, "gate", torch.float32, 2)
+    if ve.shape[1] != hkv * HEAD_DIM or tuple(gate.shape) != (hkv, d):
+        raise ValueError(f"ve {tuple(ve.shape)} / gate {tuple(gate.shape)} do not fit {hkv} kv heads, d {d}")
+    tok = tok.to(torch.int32).contiguous()
+    if tok.numel() != rows:
+        raise ValueError(f"{tok.numel()} tokens for {rows} rows")
+    check(hip_library().nc_value_embed_bf16(pointer(qkv), qkv.stride(0), pointer(x), x.stride(0), pointer(tok),
+                                            pointer(ve), ve.shape[0], pointer(gate), rows, d, hq, hkv, stream()))
+    return qkv
+
+
 class Fp8Decoder:
     """Batch `batch` sequences of at most max_len tokens, one contiguous fp8 cache per layer."""
 
@@ -218,12 +240,12 @@ class Fp8Decoder:
             self.softcap = float(softcap)
 
     # ---------------------------------------------------------------------------------------------- layers
-    def _qkv_append(self, l: int, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor) -> Tensor:
+    def _qkv_append(self, l: int, x: Tensor, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor) -> Tensor:
         """h = norm(x); the projection (with the value-embedding mix), then QK-norm + RoPE + fp8 append of k, v;
         returns q."""
         lw = self.model.layers[l]
         qkv = torch.matmul(h, lw["wqkv"].t())
-        self._value_embed(l, qkv, h, tok)
+        self._value_embed(l, qkv, x, tok)
         return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
 
     def _mix(self, l: int, x: Tensor, x0: Tensor) -> None:
@@ -233,16 +255,14 @@ class Fp8Decoder:
             r, z = self.model.resid_lambdas[l], self.model.x0_lambdas[l]
             x.copy_((r * x.float() + z * x0.float()).to(torch.bfloat16))
 
-    def _value_embed(self, l: int, qkv: Tensor, n: Tensor, tok: Tensor) -> None:
-        """In a value-embedding layer, v += 2 sigmoid(ve_gate n) ve[tok] per head in fp32, rounded to bf16 once, in
-        the projection rows qkv (inference/modeling_nanochat.py:85-88; decode.cu:478-493). n: the normed stream."""
+    def _value_embed(self, l: int, qkv: Tensor, x: Tensor, tok: Tensor) -> None:
+        """In a value-embedding layer, v += 2 sigmoid(ve_gate norm(x)) ve[tok] per head in fp32, rounded to bf16 once,
+        in the projection rows qkv (nc_value_embed_bf16; inference/modeling_nanochat.py:85-88, decode.cu:478-493).
+        x: the layer input rows."""
         lw = self.model.layers[l]
         if "ve" not in lw:
             return
-        rows, H, hq = qkv.shape[0], self.cfg.kv_heads, self.cfg.heads
-        gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))  # [rows][H]
-        v = qkv[:, (hq + H) * HEAD_DIM:(hq + 2 * H) * HEAD_DIM].view(rows, H, HEAD_DIM)
-        v.copy_((v.float() + gate[..., None] * lw["ve"][tok].view(rows, H, HEAD_DIM).float()).to(torch.bfloat16))
+        value_embed(qkv, x, tok, lw["ve"], lw["ve_gate"], self.cfg.heads, self.cfg.kv_heads)
 
     def _finish_layer(self, l: int, x: Tensor, o: Tensor) -> Tensor:
         """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; returns norm(x), the next layer's
@@ -287,7 +307,7 @@ class Fp8Decoder:
                 if self.mixes:
                     self._mix(l, x[r0:r1], x0[r0:r1])
                     h[r0:r1] = add_rms_norm(x[r0:r1], None)
-                q[r0:r1] = self._qkv_append(l, h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1])
+                q[r0:r1] = self._qkv_append(l, x[r0:r1], h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1])
             prefill_attention(q, self.caches[l], pos, seq, window=self.cfg.window(l), out=o)
             for r0, r1 in chunks:
                 h[r0:r1] = self._finish_layer(l, x[r0:r1], o[r0:r1])
@@ -304,8 +324,7 @@ class Fp8Decoder:
             lw = self.model.layers[l]
             self._mix(l, x, x0)
             qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
-            if "ve" in lw:
-                self._value_embed(l, qkv, add_rms_norm(x, None), tok)
+            self._value_embed(l, qkv, x, tok)
             # the append (decode.cu:550-565) and attention in one call: sequence b is cache row b
             o = decode_step(qkv, self.caches[l], pos, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
                             max_ctx=self.max_len, window=self.cfg.window(l), workspace=self.ws)

@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "nc_choose_tokens": (I32, [P, I32, I32, I64, P, P, P, P, P, P, P, F32, I32, P, P, P, I64, P]),
     "nc_add_rms_norm_bf16": (I32, [P, P, P, P, I32, I32, P]),
     "nc_relu2_bf16": (I32, [P, P, I64, P]),
+    "nc_value_embed_bf16": (I32, [P, I64, P, I64, P, P, I64, P, I32, I32, I32, I32, P]),
     "nc_slot_gemm_bf16": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P]),
 }
 

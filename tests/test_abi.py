@@ -193,3 +193,28 @@ def test_choose_rejects_bad_arguments():
     empty = list(base)
     empty[1] = 0
     assert lib.nc_choose_tokens(*empty) == 0
+
+
+def test_value_embed_rejects_bad_arguments():
+    lib = native.hip_library()
+    #       qkv   stride x     xs   tok   ve    vocab gate  rows d    hq hkv stream
+    base = [FAKE, 1024, FAKE, 256, FAKE, FAKE, 100, FAKE, 4, 256, 4, 2, NULL]
+
+    def rejects(i, value, message):
+        args = list(base)
+        args[i] = value
+        assert lib.nc_value_embed_bf16(*args) < 0, (i, value)
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    rejects(9, 260, "d")            # not a multiple of 8
+    rejects(9, 8200, "d")           # past the row limit
+    rejects(11, 3, "hkv")           # does not divide hq
+    rejects(11, 0, "hkv")
+    rejects(1, 1016, "row_stride")  # narrower than hq + 2 hkv heads
+    rejects(3, 248, "x_stride")
+    rejects(6, 0, "vocab")
+    rejects(4, NULL, "null")
+    rejects(0, ctypes.c_void_p(0x1008), "alignment")
+    empty = list(base)
+    empty[8] = 0
+    assert lib.nc_value_embed_bf16(*empty) == 0  # no rows, nothing launched
