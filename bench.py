@@ -11,7 +11,8 @@ nc_kv_append_fp8 call, then nc_decode_attn_fp8). Each step also writes the next 
 Output: one JSON line. value = algorithmic attention bytes per step / measured step time (GB/s, inputs resident in
 HBM); roofline = the step's attention call (k_decode, then k_merge): the timed steps themselves (one
 nc_decode_step_fp8 call each), or with --unfused the attention call alone at the last step's context, timed over
-graph replays of 10 back-to-back calls, with HIP events on their stream;
+graph replays of 10 back-to-back calls, with HIP events on their stream; attention_only = that attention call
+alone in either mode (the decode kernel and the split-K merge without the append, the kernels the metric counts);
 cpu_baseline = the numpy oracle over a bounded sample of the same sequences on this host's cores.
 """
 
@@ -296,17 +297,20 @@ def main():
         q = case.cache.append(qkv, ctx_len - 1, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
     step_bytes = np.mean([decode_bytes(base + i + 1, cfg.hkv, cfg.window) for i in range(steps)])
     value = step_bytes / (step_ms * 1e-3) / 1e9
+    # the attention call alone (the metric's decode kernel + split-K merge, without the append): ATTN_REPS calls at
+    # the last step's context in one graph
+    with torch.cuda.stream(stream):
+        decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+        stream.synchronize()
+        with torch.cuda.graph(attn_graph, stream=stream):
+            for _ in range(ATTN_REPS):
+                decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+    attn_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
+    attn_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
+    attn_kernel = (f"nc_decode_attn_fp8 = k_decode<false> + k_merge, a graph of {ATTN_REPS} calls at the last "
+                   "step's context, HIP events on their stream")
     if args.unfused:
-        # roofline of the attention call alone: ATTN_REPS calls at the last step's context in one graph
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(attn_graph, stream=stream):
-                for _ in range(ATTN_REPS):
-                    decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out,
-                                     workspace=ws)
-        call_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
-        call_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
-        call_kernel = (f"nc_decode_attn_fp8 = k_decode<false> + k_merge, a graph of {ATTN_REPS} calls at the last "
-                       "step's context, HIP events on their stream")
+        call_ms, call_bytes, call_kernel = attn_ms, attn_bytes, attn_kernel
     else:
         # the step is one nc_decode_step_fp8 call: the timed region is the roofline measurement itself
         call_ms, call_bytes = step_ms, step_bytes
@@ -335,6 +339,9 @@ def main():
                            "decode attention, one attention layer, graph replays of two steps"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_one_layer": round(B / (step_ms * 1e-3), 1),
+        "attention_only": {"kernel": attn_kernel, "call_us": round(attn_ms * 1e3, 3),
+                           "GB_s": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 2),
+                           "frac_of_hbm_peak": round(attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "call_us": round(call_ms * 1e3, 3),
         "step_us": round(step_ms * 1e3, 3),
         "wall_s_timed": round(wall, 4),

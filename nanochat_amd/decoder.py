@@ -313,11 +313,14 @@ class Fp8Decoder:
                 h[r0:r1] = self._finish_layer(l, x[r0:r1], o[r0:r1])
 
     # ---------------------------------------------------------------------------------------------- decode
-    def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor) -> Tensor:
-        """One decode step: token tok[b] at position pos[b] of every sequence; the choice (greedy, or by
-        set_sampling) into out_tok, its alternative into self.alt, then pos += 1 (the commit). Returns the fp32
-        logits. Per layer four slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and attention;
-        x += o_proj(o); u = relu(up(norm(x)))^2; x += down(u)."""
+    def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor, slots: Tensor | None = None) -> Tensor:
+        """One decode step: token tok[b] at position pos[b] of sequences b < len(tok) (all, or the first ones: the
+        narrow step, whose slot masks `slots` replace self.slots); the choice (greedy, or by set_sampling) into
+        out_tok, its alternative into self.alt, then pos += 1 (the commit). Returns the fp32 logits. Per layer four
+        slot GEMMs (decode.cu:848-877): qkv of norm(x), then append and attention; x += o_proj(o);
+        u = relu(up(norm(x)))^2; x += down(u)."""
+        n = tok.shape[0]
+        part = lambda t: None if t is None else t[:n]
         x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
         x0 = x.clone() if self.mixes else None
         for l in range(self.cfg.layers):
@@ -332,9 +335,10 @@ class Fp8Decoder:
             u = slot_gemm(x, lw["wup"], RELU2_NORM)
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
         logits = slot_gemm(x, self.lm_head, NORM_F32)
-        choose_tokens(logits, self.cfg.vocab, pos, temperature=self.temperature, top_p=self.top_p, seed=self.seeds,
-                      first=self.first, slots=self.slots, allow=self.allow, softcap=self.softcap, lazy=self.lazy,
-                      tokens=out_tok, alt_tokens=self.alt, workspace=self.choose_ws)
+        choose_tokens(logits, self.cfg.vocab, pos, temperature=part(self.temperature), top_p=part(self.top_p),
+                      seed=part(self.seeds), first=part(self.first), slots=self.slots if slots is None else slots,
+                      allow=part(self.allow), softcap=self.softcap, lazy=self.lazy, tokens=out_tok,
+                      alt_tokens=self.alt[:n], workspace=self.choose_ws)
         return logits[:, :self.cfg.vocab]
 
     @torch.no_grad()

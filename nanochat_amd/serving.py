@@ -5,7 +5,9 @@ Requests queue for `batch` slots. A free slot takes the next request: its prompt
 into the slot's cache rows (all newly admitted prompts in one prefill), the slot's token, position, first generated
 position and sampling parameters are set, and it joins the next decode step. Each step is one replay of a captured
 hipGraph over every slot: idle slots carry position -1, so the fused decode step does no work for them and the
-token choice (nc_choose_tokens' slot mask) leaves them untouched. After a step the host reads the choices and
+token choice (nc_choose_tokens' slot mask) leaves them untouched. As the reference's narrow graphs
+(decode.cu:32-33,995-1005,1090-1093), a second graph over the first `narrow` slots runs the steps in which no
+higher slot is active: its GEMMs, its lm_head and its choice cover those rows only. After a step the host reads the choices and
 finishes a slot on BOS (dropped; unless the request's accept_bos rejects it, when the step's alternative, the best
 token but BOS, is taken instead, as the reference's lazy BOS), at max_new_tokens, or when the request's stopping
 criteria hold for its tokens, then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
@@ -55,8 +57,12 @@ class _Slot:
 class Server:
     """`batch` slots over one Fp8Decoder; bos ends a continuation (inference/decoder.py:310-312)."""
 
-    def __init__(self, model: Weights, batch: int, max_len: int, device, bos: int, prompt_store: int = 0):
+    def __init__(self, model: Weights, batch: int, max_len: int, device, bos: int, prompt_store: int = 0,
+                 narrow: int = 256):
+        if narrow < 0 or narrow % 64:
+            raise ValueError(f"narrow = {narrow}: a multiple of 64 slots (whole slot-mask words)")
         self.dec = Fp8Decoder(model, batch, max_len, device)
+        self.narrow = narrow if narrow < batch else 0  # 0: one graph
         self.batch, self.max_len, self.bos, self.device = batch, max_len, bos, device
         caches = self.dec.caches
         self.store_pages = prompt_store // PAGE
@@ -80,22 +86,37 @@ class Server:
         d.first = torch.zeros(B, dtype=torch.int32, device=dev)
         d.slots = torch.zeros((2, (B + 63) // 64), dtype=torch.int64, device=dev)
         d.allow = torch.zeros((B, (vocab + 31) // 32), dtype=torch.int32, device=dev)
+        self.narrow_slots = torch.zeros((2, self.narrow // 64), dtype=torch.int64, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
+        self.narrow_graph: torch.cuda.CUDAGraph | None = None
+        self.narrow_steps = self.steps = 0
         self.stream = torch.cuda.Stream(dev)
 
     def _capture(self) -> None:
-        """The step graph: the decode step over every slot, then each slot's next input is its choice."""
+        """The step graphs: the decode step over every slot (and over the first `narrow`), then each slot's next
+        input is its choice."""
         s = self.stream
         s.wait_stream(torch.cuda.current_stream(self.device))
+
+        def body(n: int) -> None:
+            self.dec._step(self.tok[:n], self.pos[:n], self.next[:n], None if n == self.batch else self.narrow_slots)
+            self.tok[:n].copy_(self.next[:n])
+
         with torch.cuda.stream(s):
-            pos0 = self.pos.clone()
-            self.dec._step(self.tok, self.pos, self.next)  # warm every launch path (no slot is active yet)
-            self.pos.copy_(pos0)
+            saved = self.pos.clone(), self.tok.clone()
+            for n in (self.batch, self.narrow):  # warm every launch path (no slot is active yet)
+                if n:
+                    body(n)
+            self.pos.copy_(saved[0])
+            self.tok.copy_(saved[1])
             s.synchronize()
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph, stream=s):
-                self.dec._step(self.tok, self.pos, self.next)
-                self.tok.copy_(self.next)
+                body(self.batch)
+            if self.narrow:
+                self.narrow_graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.narrow_graph, stream=s):
+                    body(self.narrow)
         torch.cuda.current_stream(self.device).wait_stream(s)
 
     @torch.no_grad()
@@ -128,8 +149,16 @@ class Server:
                     self._admit(slots, admitted)
                     admitted.clear()
                 masked = self._masks(slots)
-                d.slots.copy_(torch.from_numpy(slot_masks([s is not None for s in slots], masked)).to(dev))
-                self.graph.replay()
+                words = slot_masks([s is not None for s in slots], masked)
+                high = max(b for b, s in enumerate(slots) if s is not None)
+                self.steps += 1
+                if high < self.narrow:  # dec_set_active's choice (decode.cu:1090-1093)
+                    self.narrow_slots.copy_(torch.from_numpy(words[:, :self.narrow // 64].copy()).to(dev))
+                    self.narrow_graph.replay()
+                    self.narrow_steps += 1
+                else:
+                    d.slots.copy_(torch.from_numpy(words).to(dev))
+                    self.graph.replay()
                 chosen = self.next.cpu().numpy()
                 alts = d.alt.cpu().numpy()
             finished = []

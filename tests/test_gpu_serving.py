@@ -48,26 +48,47 @@ def test_continuous_batching_matches_each_request_alone(gpu):
     server = Server(model, batch=3, max_len=48, device=gpu, bos=BOS)
     got = dict(server.generate(reqs))
     assert sorted(got) == list(range(len(reqs)))
-    checked = 0
-    for k, r in enumerate(reqs):
-        out = got[k]
-        assert 1 <= len(out) + (len(out) < r.max_new_tokens) and len(out) <= r.max_new_tokens
-        if r.mask is not None:
-            assert all(t % 2 == 0 for t in out)
-        cpu = CpuModel(model, 1, 48)
-        ids = np.array(r.input_ids, np.int32)
-        cpu.prefill(ids[None])
-        tok, p = ids[-1:], len(ids) - 1
-        stopped_early = len(out) < r.max_new_tokens and not (r.stopping_criteria and r.stopping_criteria(out))
-        for i in range(len(out) + stopped_early):
-            logits = cpu.step(tok, p)[0]
-            want, sure = expected_choice(logits, r, i, even if r.mask is not None else None)
-            served = out[i] if i < len(out) else BOS
-            if sure:
-                assert served == want, (k, i, served, want)
-                checked += 1
-            tok, p = np.array([served], np.int32), p + 1
+    checked = sum(check_alone(model, k, r, got[k], even) for k, r in enumerate(reqs))
     assert checked >= 25, checked
+
+
+def check_alone(model, k, r: Request, out, allowed=None) -> int:
+    """Request k's served tokens against a CPU run of that request alone; returns how many choices were clear of
+    the tolerance (and so checked)."""
+    assert 1 <= len(out) + (len(out) < r.max_new_tokens) and len(out) <= r.max_new_tokens
+    if r.mask is not None:
+        assert all(allowed[t] for t in out)
+    cpu = CpuModel(model, 1, 48)
+    ids = np.array(r.input_ids, np.int32)
+    cpu.prefill(ids[None])
+    tok, p = ids[-1:], len(ids) - 1
+    stopped_early = len(out) < r.max_new_tokens and not (r.stopping_criteria and r.stopping_criteria(out))
+    checked = 0
+    for i in range(len(out) + stopped_early):
+        logits = cpu.step(tok, p)[0]
+        want, sure = expected_choice(logits, r, i, allowed if r.mask is not None else None)
+        served = out[i] if i < len(out) else BOS
+        if sure:
+            assert served == want, (k, i, served, want)
+            checked += 1
+        tok, p = np.array([served], np.int32), p + 1
+    return checked
+
+
+def test_narrow_graph_serves_the_low_slots(gpu):
+    """batch 128 with a narrow graph over the first 64 slots (decode.cu:995-1005): while slots 64 and 65 are busy
+    the full graph runs, afterwards the narrow one; requests on both sides of the boundary decode as alone."""
+    model = RandomModel(TINY, gpu, seed=41)
+    rng = np.random.default_rng(42)
+    reqs = [Request(input_ids=[BOS] + rng.integers(8, TINY.vocab, 5 + k % 7).tolist(),
+                    max_new_tokens=2 if k >= 64 else 6, temperature=0.7 if k % 3 == 0 else 0.0, seed=500 + k)
+            for k in range(66)]
+    server = Server(model, batch=128, max_len=48, device=gpu, bos=BOS, narrow=64)
+    got = dict(server.generate(reqs))
+    assert sorted(got) == list(range(len(reqs)))
+    assert 0 < server.narrow_steps < server.steps, (server.narrow_steps, server.steps)
+    checked = sum(check_alone(model, k, reqs[k], got[k]) for k in (0, 1, 2, 62, 63, 64, 65))
+    assert checked >= 20, checked
 
 
 def test_prompt_store_loads_instead_of_prefilling(gpu):
