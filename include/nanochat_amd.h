@@ -1,7 +1,7 @@
 /*
  * nanochat_amd: the C ABI of the MI355X (gfx950) fp8-KV decode path, libnanochat_amd.so.
  *
- * Conventions (the reference's, model/kernels/*.cu with native.py:43-65): every tensor is a raw device pointer,
+ * Conventions (the reference's, model/kernels/<name>.cu with native.py:43-65): every tensor is a raw device pointer,
  * counts are C ints, the HIP stream is the last argument, and every launch is stream-ordered and asynchronous.
  * Two error classes:
  *   - argument errors are checked on the host before any launch: the call returns a negative status and
@@ -160,6 +160,18 @@ int nc_value_embed_bf16(void *qkv, long long row_stride, const void *x, long lon
                         const void *ve, long long vocab, const float *gate, int rows, int d, int hq, int hkv,
                         void *stream);
 
+/* The embedding and its norm: x[r] = bf16(e r) for e = table[tok[r]] (fp32 if table_fp32, else bf16; [vocab][d]),
+ * r = 1 / sqrt(Σ e² / d + FLT_EPSILON), Σ in fp32 as nc_add_rms_norm_bf16 sums; x bf16 [rows][d]. A token outside
+ * [0, vocab) gives a zero row. d % 8 == 0, d <= 8192.
+ * Replaces: k_norm's EMBED kind, model/kernels/decode.cu:413-441 (x0 = norm(embed(tok)), kept fp32 there, bf16 here
+ * as in inference/modeling_nanochat.py:150-165). */
+int nc_embed_rms_norm(const void *table, int table_fp32, long long vocab, const int32_t *tok, int rows, int d,
+                      void *x, void *stream);
+
+/* The per-layer residual mix, in place over n bf16 (n % 8 == 0): x = bf16(lr x + l0 x0), products and sum in fp32.
+ * Replaces: k_norm's RESID_NORM mix, model/kernels/decode.cu:428-431 (inference/modeling_nanochat.py:170-171). */
+int nc_mix_bf16(void *x, const void *x0, long long n, float lr, float l0, void *stream);
+
 /* out = bf16(relu(in)^2) over n bf16 (n % 8 == 0); out may be in.
  * Replaces: the RELU2 epilogue of the slot GEMM, model/kernels/decode.cu:174-178. */
 int nc_relu2_bf16(const void *in, void *out, long long n, void *stream);
@@ -182,6 +194,79 @@ enum {
  * model/kernels/decode.cu:107-123,169-184,292-338,447-456, launched per layer at :848-877. */
 int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out, const void *res,
                       int tile_n, int tile_m, void *stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * The decoder handle (the reference's dec_* runtime, model/kernels/decode.cu:693-1131, bound by
+ * inference/decoder.py:129-324): B slots of at most max_len positions over this library's kernels, an fp8 cache per
+ * layer, captured step graphs over all slots and over the first 256, pinned token and mask buffers, and a prompt
+ * store in pinned host memory. One host thread; every call is ordered on the handle's stream (the caller's, not the
+ * legacy default stream, alive past dec_destroy); dec_tokens is the only call that waits. Weights are borrowed and
+ * must stay unchanged while the handle lives.
+ */
+
+/* cfg: L, C (hidden size, a multiple of 128), F (MLP width, a multiple of 64), vocab (<= 131072), max_len (positions
+ * per slot; cos / sin hold at least that many rows), store (prompt-store positions), lazy (the token whose
+ * alternative each choice also reports, BOS). ptrs: wte (fp32 [vocab][C]), cos, sin (fp32 [max_len][64]), lm_head
+ * (bf16 [vocab][C]), then per layer qkv ([(H + 2 Hkv) 128][C]), o, up ([F][C]), down ([C][F]) (bf16), the
+ * value-embedding table (bf16 [vocab][Hkv 128]) and its gate (fp32 [Hkv][C]) or 0, 0, and the q and k norm gains
+ * (fp32 [128]). scal: per layer the residual and x0 lambdas, then the logit cap. window: per layer, keys before a
+ * query (< 0: all). Returns NULL on a bad argument (nc_last_error). H = C / 128; the slot count is the most whose
+ * caches fit the free device memory, at most 1024.
+ * Replaces: dec_create, model/kernels/decode.cu:950-1023 (same arguments; the cache is fp8). */
+void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream);
+
+/* dec_create with ncfg configuration fields: cfg[7] Hkv (0: H), cfg[8] the slot count (0: as dec_create),
+ * cfg[9] 1 for a bf16 embedding table. No counterpart in the reference: its fields 0-6 keep their meaning and the
+ * new ones are appended, as the grouped-query caches and bf16 checkpoint exports need. */
+void *dec_create_v2(const int *cfg, int ncfg, const uint64_t *ptrs, const float *scal, const int *window,
+                    void *stream);
+
+/* Releases every resource of the handle (after waiting for its stream). Replaces: dec_destroy, decode.cu:904-924. */
+void dec_destroy(void *handle);
+
+/* The handle's slot count. Replaces: dec_batch, decode.cu:948. */
+int dec_batch(void *handle);
+
+/* Rows per dec_prefill call (1024). Replaces: dec_prefill_rows, decode.cu:1037. */
+int dec_prefill_rows(void *handle);
+
+/* Slot b starts at its prompt's last token `token`, position `last` (earlier positions cached or queued for
+ * prefill), with its sampling parameters (inference/decoder.py:28-40). Replaces: dec_set_prompt, decode.cu:1026-1035. */
+void dec_set_prompt(void *handle, int b, int32_t token, int32_t last, float temperature, float top_p,
+                    unsigned long long seed);
+
+/* Runs n <= dec_prefill_rows rows (rows: int32 [3][n], tokens, positions, slots) through every layer, caching each
+ * row's key and value; a row attends its slot's cached positions and the earlier rows of the call. Waits for the
+ * handle's previous work before reading rows. Replaces: dec_prefill, decode.cu:1041-1051. */
+void dec_prefill(void *handle, int n, const int32_t *rows);
+
+/* Slot b's cache pages holding positions [at, at + n) to the prompt store's pages from position store_at (save)
+ * or back (load), every layer; whole 16-position pages (at and store_at multiples of 16). Returns 0 or a negative
+ * status. Replaces: dec_save_prompt / dec_load_prompt, decode.cu:1069-1075 (position-granular bf16 rows there). */
+int dec_save_prompt(void *handle, int b, int at, int store_at, int n);
+int dec_load_prompt(void *handle, int b, int at, int store_at, int n);
+
+/* The pinned allowed-token rows [B][ceil(vocab / 32)] (bit t % 32 of word t / 32 of row b: slot b may choose t),
+ * written by the caller between dec_tokens and dec_set_active. Replaces: dec_masks, decode.cu:1079. */
+uint32_t *dec_masks(void *handle);
+
+/* The active and masked slots, slots[2][ceil(B / 64)] (slot b at bit b % 64 of word b / 64); the masked slots'
+ * rows of dec_masks are copied; a slot that is not active idles (position -1). The next launches run the narrow
+ * graphs when no slot past the first 256 is active. Replaces: dec_set_active, decode.cu:1083-1105. */
+void dec_set_active(void *handle, const unsigned long long *slots);
+
+/* Launch a step's body (embedding, every layer) and its head (lm_head, the choice and its commit: each active slot's
+ * next token, position + 1). Replaces: dec_launch_body / dec_launch_head, decode.cu:1107-1116. */
+void dec_launch_body(void *handle);
+void dec_launch_head(void *handle);
+
+/* Waits for the launched step; out[b]: the token slot b took, out[B + b]: its alternative, the best allowed token
+ * but lazy (-1 if none; stale for idle slots). Replaces: dec_tokens, decode.cu:1120-1124. */
+void dec_tokens(void *handle, int32_t *out);
+
+/* Slot b's next input becomes its last alternative (the host rejected the lazy token). Replaces: dec_take_alt,
+ * decode.cu:1128-1131. */
+void dec_take_alt(void *handle, int b);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,75 @@ __global__ void __launch_bounds__(RN_THREADS) k_add_rms_norm(const bf16_t *x, co
     }
 }
 
+/* x[r] = bf16(e r), e = table[tok[r]] (fp32 or bf16), r = 1 / sqrt(Σ e² / d + FLT_EPSILON), Σ in fp32 in
+ * k_add_rms_norm's order; a token outside [0, vocab) gives a zero row. */
+template <bool FP32>
+__global__ void __launch_bounds__(RN_THREADS) k_embed_norm(const void *table, const int32_t *tok, long long vocab,
+                                                           bf16_t *x, int d) {
+    __shared__ float part[RN_THREADS / NC_WAVE];
+    const int row = blockIdx.x, tid = threadIdx.x, chunks = d / 8;
+    const int t = tok[row];
+    bf16_t *dst = x + (size_t)row * d;
+    if (t < 0 || t >= vocab) {
+        for (int c = tid; c < chunks; c += RN_THREADS) reinterpret_cast<u32x4 *>(dst)[c] = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
+    float v[RN_MAX_CHUNKS][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+        if constexpr (FP32) {
+            const f32x4 *src = reinterpret_cast<const f32x4 *>((const float *)table + (size_t)t * d + 8 * c);
+            const f32x4 a = src[0], b = src[1];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[k][e] = a[e];
+                v[k][4 + e] = b[e];
+            }
+        } else {
+            load_bf16x8((const bf16_t *)table + (size_t)t * d + 8 * c, v[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += v[k][e] * v[k][e];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+    if ((tid & (NC_WAVE - 1)) == 0) part[tid / NC_WAVE] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < RN_THREADS / NC_WAVE; w++) total += part[w];
+    const float r = 1.0f / sqrtf(total / (float)d + 1.1920928955078125e-07f);
+#pragma unroll
+    for (int k = 0; k < RN_MAX_CHUNKS; k++) {
+        const int c = tid + k * RN_THREADS;
+        if (c >= chunks) break;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = v[k][e] * r;
+        store_bf16x8(dst + 8 * c, o);
+    }
+}
+
+/* x = bf16(lr x + l0 x0): the two products and their sum each rounded to fp32, then one bf16 rounding. */
+__global__ void __launch_bounds__(RN_THREADS) k_mix(bf16_t *x, const bf16_t *x0, long long n8, float lr, float l0) {
+#pragma clang fp contract(off)
+    const long long stride = (long long)gridDim.x * RN_THREADS;
+    for (long long c = (long long)blockIdx.x * RN_THREADS + threadIdx.x; c < n8; c += stride) {
+        float a[8], b[8];
+        load_bf16x8(x + 8 * c, a);
+        load_bf16x8(x0 + 8 * c, b);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = lr * a[e], q = l0 * b[e];
+            a[e] = p + q;
+        }
+        store_bf16x8(x + 8 * c, a);
+    }
+}
+
 #define VE_MAX_HEADS 64
 
 __global__ void __launch_bounds__(RN_THREADS) k_value_embed(bf16_t *qkv, long long row_stride, const bf16_t *x,
@@ -186,6 +255,39 @@ extern "C" int nc_value_embed_bf16(void *qkv, long long row_stride, const void *
     NC_REQUIRE(((uintptr_t)qkv | (uintptr_t)x | (uintptr_t)ve) % 16 == 0, "nc_value_embed_bf16: 16-byte alignment");
     hipLaunchKernelGGL(k_value_embed, dim3(rows), dim3(RN_THREADS), 0, (hipStream_t)stream, (bf16_t *)qkv, row_stride,
                        (const bf16_t *)x, x_stride, tok, (const bf16_t *)ve, vocab, gate, d, hq, hkv);
+    NC_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int nc_embed_rms_norm(const void *table, int table_fp32, long long vocab, const int32_t *tok, int rows,
+                                 int d, void *x, void *stream) {
+    NC_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 8 * RN_THREADS * RN_MAX_CHUNKS,
+               "nc_embed_rms_norm: rows %d, d %d (d a multiple of 8, at most %d)", rows, d,
+               8 * RN_THREADS * RN_MAX_CHUNKS);
+    NC_REQUIRE(vocab > 0, "nc_embed_rms_norm: vocab %lld", vocab);
+    if (rows == 0) return 0;
+    NC_REQUIRE(table && tok && x, "nc_embed_rms_norm: null pointer");
+    NC_REQUIRE(((uintptr_t)table | (uintptr_t)x) % 16 == 0, "nc_embed_rms_norm: 16-byte alignment");
+    if (table_fp32)
+        hipLaunchKernelGGL(k_embed_norm<true>, dim3(rows), dim3(RN_THREADS), 0, (hipStream_t)stream, table, tok,
+                           vocab, (bf16_t *)x, d);
+    else
+        hipLaunchKernelGGL(k_embed_norm<false>, dim3(rows), dim3(RN_THREADS), 0, (hipStream_t)stream, table, tok,
+                           vocab, (bf16_t *)x, d);
+    NC_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int nc_mix_bf16(void *x, const void *x0, long long n, float lr, float l0, void *stream) {
+    NC_REQUIRE(n >= 0 && n % 8 == 0, "nc_mix_bf16: n = %lld must be a non-negative multiple of 8", n);
+    if (n == 0) return 0;
+    NC_REQUIRE(x && x0, "nc_mix_bf16: null pointer");
+    NC_REQUIRE(((uintptr_t)x | (uintptr_t)x0) % 16 == 0, "nc_mix_bf16: 16-byte alignment");
+    const long long n8 = n / 8;
+    long long blocks = (n8 + RN_THREADS - 1) / RN_THREADS;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_mix, dim3((unsigned)blocks), dim3(RN_THREADS), 0, (hipStream_t)stream, (bf16_t *)x,
+                       (const bf16_t *)x0, n8, lr, l0);
     NC_LAUNCH_CHECK();
     return 0;
 }

@@ -168,6 +168,26 @@ def add_rms_norm(x: Tensor, delta: Tensor | None, x_out: Tensor | None = None) -
     return y
 
 
+def embed_norm(table: Tensor, tok: Tensor) -> Tensor:
+    """nc_embed_rms_norm: bf16 norm(table[tok]) per token (table bf16 or fp32 [vocab][d]; tok int32 [n])."""
+    if table.dtype not in (torch.bfloat16, torch.float32) or table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("table must be a contiguous bf16 or fp32 [vocab][d] tensor")
+    tok = tok.to(torch.int32).contiguous()
+    x = torch.empty((tok.shape[0], table.shape[1]), dtype=torch.bfloat16, device=table.device)
+    check(hip_library().nc_embed_rms_norm(pointer(table), int(table.dtype == torch.float32), table.shape[0],
+                                          pointer(tok), tok.shape[0], table.shape[1], pointer(x), stream()))
+    return x
+
+
+def mix(x: Tensor, x0: Tensor, lr: float, l0: float) -> Tensor:
+    """nc_mix_bf16: x = bf16(lr x + l0 x0) in place (contiguous bf16 of one shape)."""
+    if x.dtype != torch.bfloat16 or x0.dtype != torch.bfloat16 or x.shape != x0.shape or not (
+            x.is_contiguous() and x0.is_contiguous()):
+        raise ValueError("mix needs contiguous bf16 x and x0 of one shape")
+    check(hip_library().nc_mix_bf16(pointer(x), pointer(x0), x.numel(), float(lr), float(l0), stream()))
+    return x
+
+
 def relu2(x: Tensor) -> Tensor:
     """bf16(relu(x)^2) in place (nc_relu2_bf16)."""
     if x.dtype != torch.bfloat16 or not x.is_contiguous():
@@ -224,6 +244,7 @@ class Fp8Decoder:
         self.slots = self.allow = None  # the choice's slot masks and allowed-token rows (serving.Server sets them)
         self.softcap, self.lazy = cfg.softcap, -1
         self.mixes = model.mixes
+        self.lambdas = list(zip(model.resid_lambdas.tolist(), model.x0_lambdas.tolist()))
 
     def set_sampling(self, temperature, top_p=1.0, seed=0, first=0, softcap: float | None = None) -> None:
         """Per-slot sampling (scalars broadcast; inference/decoder.py:28-40): temperature 0 is greedy, > 0 a
@@ -249,11 +270,11 @@ class Fp8Decoder:
         return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
 
     def _mix(self, l: int, x: Tensor, x0: Tensor) -> None:
-        """x = bf16(resid_lambdas[l] x + x0_lambdas[l] x0) in place, fp32 products and sum rounded once
-        (inference/modeling_nanochat.py:170-171); skipped when every layer's mix is the identity."""
-        if self.mixes:
-            r, z = self.model.resid_lambdas[l], self.model.x0_lambdas[l]
-            x.copy_((r * x.float() + z * x0.float()).to(torch.bfloat16))
+        """x = bf16(resid_lambdas[l] x + x0_lambdas[l] x0) in place (nc_mix_bf16; inference/modeling_nanochat.py:
+        170-171); skipped where the mix is the identity (it would return x unchanged)."""
+        lr, l0 = self.lambdas[l]
+        if self.mixes and (lr != 1.0 or l0 != 0.0):
+            mix(x, x0, lr, l0)
 
     def _value_embed(self, l: int, qkv: Tensor, x: Tensor, tok: Tensor) -> None:
         """In a value-embedding layer, v += 2 sigmoid(ve_gate norm(x)) ve[tok] per head in fp32, rounded to bf16 once,
@@ -274,7 +295,7 @@ class Fp8Decoder:
 
     def _embed(self, tok: Tensor) -> tuple[Tensor, Tensor]:
         """The residual stream x0 = norm(embed(tok)) and its norm, the first layer's input."""
-        x = add_rms_norm(self.model.wte[tok], None)
+        x = embed_norm(self.model.wte, tok)
         return x, add_rms_norm(x, None)
 
     # ---------------------------------------------------------------------------------------------- prefill
@@ -321,7 +342,7 @@ class Fp8Decoder:
         u = relu(up(norm(x)))^2; x += down(u)."""
         n = tok.shape[0]
         part = lambda t: None if t is None else t[:n]
-        x = add_rms_norm(self.model.wte[tok], None)  # the residual stream x0 = norm(embed(tok))
+        x = embed_norm(self.model.wte, tok)  # the residual stream x0 = norm(embed(tok))
         x0 = x.clone() if self.mixes else None
         for l in range(self.cfg.layers):
             lw = self.model.layers[l]

@@ -37,7 +37,24 @@ SIGNATURES: dict[str, tuple] = {
     "nc_add_rms_norm_bf16": (I32, [P, P, P, P, I32, I32, P]),
     "nc_relu2_bf16": (I32, [P, P, I64, P]),
     "nc_value_embed_bf16": (I32, [P, I64, P, I64, P, P, I64, P, I32, I32, I32, I32, P]),
+    "nc_embed_rms_norm": (I32, [P, I32, I64, P, I32, I32, P, P]),
+    "nc_mix_bf16": (I32, [P, P, I64, F32, F32, P]),
     "nc_slot_gemm_bf16": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P]),
+    "dec_create": (P, [P, P, P, P, P]),
+    "dec_create_v2": (P, [P, I32, P, P, P, P]),
+    "dec_destroy": (None, [P]),
+    "dec_batch": (I32, [P]),
+    "dec_prefill_rows": (I32, [P]),
+    "dec_set_prompt": (None, [P, I32, ctypes.c_int32, ctypes.c_int32, F32, F32, ctypes.c_ulonglong]),
+    "dec_prefill": (None, [P, I32, P]),
+    "dec_save_prompt": (I32, [P, I32, I32, I32, I32]),
+    "dec_load_prompt": (I32, [P, I32, I32, I32, I32]),
+    "dec_masks": (P, [P]),
+    "dec_set_active": (None, [P, P]),
+    "dec_launch_body": (None, [P]),
+    "dec_launch_head": (None, [P]),
+    "dec_tokens": (None, [P, P]),
+    "dec_take_alt": (None, [P, I32]),
 }
 
 

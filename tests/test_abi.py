@@ -218,3 +218,34 @@ def test_value_embed_rejects_bad_arguments():
     empty = list(base)
     empty[8] = 0
     assert lib.nc_value_embed_bf16(*empty) == 0  # no rows, nothing launched
+
+
+def test_decoder_handle_rejects_bad_configurations():
+    """dec_create_v2 checks its configuration before any device call and returns NULL with a message."""
+    import numpy as np
+
+    lib = native.hip_library()
+    ptrs = np.full(4 + 8 * 2, 0x1000, dtype=np.uint64)
+    ptrs[4 + 4] = ptrs[4 + 5] = ptrs[12 + 4] = ptrs[12 + 5] = 0  # no value embeddings
+    scal = np.array([1, 0, 1, 0, 15], dtype=np.float32)
+    window = np.array([-1, -1], dtype=np.int32)
+
+    def rejects(cfg, message):
+        cfg = np.array(cfg, dtype=np.int32)
+        h = lib.dec_create_v2(cfg.ctypes.data, len(cfg), ptrs.ctypes.data, scal.ctypes.data, window.ctypes.data, NULL)
+        assert not h
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    good = [2, 256, 1024, 1000, 48, 0, 7, 2, 4, 1]
+    rejects(good[:6], "config fields")
+    rejects([2, 200] + good[2:], "C 200")               # not a multiple of 128
+    rejects(good[:2] + [1000] + good[3:], "F 1000")     # not a multiple of 64
+    rejects(good[:3] + [200000] + good[4:], "vocab")
+    rejects(good[:7] + [3] + good[8:], "kv heads")      # 2 heads over 3 kv heads
+    rejects(good[:8] + [2000] + good[9:], "batch")      # more than 1024 slots
+    bad = ptrs.copy()
+    bad[4 + 8 + 1] = 0                                   # layer 1 without its o projection
+    cfg = np.array(good, dtype=np.int32)
+    assert not lib.dec_create_v2(cfg.ctypes.data, len(cfg), bad.ctypes.data, scal.ctypes.data, window.ctypes.data,
+                                 NULL)
+    assert "layer 1" in lib.nc_last_error().decode()

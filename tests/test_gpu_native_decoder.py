@@ -1,0 +1,109 @@
+"""The decoder handle (dec_*, nanochat_amd/native_decoder.py over csrc/decoder.hip): the reference's NativeDecoder
+protocol run natively. Every request's tokens are checked against a CPU run of that request alone (the serving
+tests' check_alone), for a random model and for a trained-like export (windows, value embeddings, residual mix);
+the prompt store and the narrow graphs are exercised on the way."""
+
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.decoder import ModelConfig, RandomModel
+from nanochat_amd.native_decoder import NativeDecoder
+from nanochat_amd.serving import Request
+from test_gpu_decoder import TINY
+from test_gpu_serving import BOS, check_alone
+
+pytestmark = pytest.mark.gpu
+
+
+def mixed_requests(rng, vocab, even):
+    lens, news = [6, 12, 25, 9, 30, 4, 17], [5, 3, 6, 8, 2, 7, 4]
+    temps = [0.0, 0.0, 0.8, 0.0, 1.2, 0.0, 0.5]
+    reqs = []
+    for k, (n, m, t) in enumerate(zip(lens, news, temps)):
+        ids = [BOS] + rng.integers(8, vocab, n - 1).tolist()
+        mask = (lambda out: even) if k == 3 else None
+        stop = (lambda out: len(out) >= 2 and out[-1] == out[-2]) if k == 1 else None
+        reqs.append(Request(input_ids=ids, max_new_tokens=m, temperature=t, seed=1000 + k, mask=mask,
+                            stopping_criteria=stop))
+    return reqs
+
+
+def test_native_decoder_matches_each_request_alone(gpu):
+    print("native decoder: random model, 3 slots", flush=True)
+    model = RandomModel(TINY, gpu, seed=51)
+    even = np.arange(TINY.vocab) % 2 == 0
+    reqs = mixed_requests(np.random.default_rng(52), TINY.vocab, even)
+    dec = NativeDecoder(model, bos=BOS, max_length=48, batch=3)
+    assert dec.batch == 3
+    got = dict(dec.generate(reqs))
+    assert sorted(got) == list(range(len(reqs)))
+    checked = sum(check_alone(model, k, r, got[k], even) for k, r in enumerate(reqs))
+    assert checked >= 25, checked
+
+
+def test_native_decoder_runs_a_trained_like_export(gpu, tmp_path):
+    """Sliding windows, value embeddings, QK-norm gains and a non-identity residual / x0 mix (fp32 lambdas), loaded
+    from the export format: the handle's mix, value-embedding and window paths against the CPU model."""
+    print("native decoder: trained-like export", flush=True)
+    from nanochat_amd.checkpoint import load_hf, save_hf
+
+    cfg = ModelConfig(layers=4, d_model=256, heads=2, vocab=1000, theta=1e6, windows=(16, 16, 16, -1),
+                      ve_layers=(1, 3))
+    m = RandomModel(cfg, "cpu", seed=53)
+    g = torch.Generator().manual_seed(54)
+    m.resid_lambdas = 0.8 + 0.4 * torch.rand(cfg.layers, generator=g)
+    m.x0_lambdas = 0.4 * torch.rand(cfg.layers, generator=g) - 0.2
+    for lw in m.layers:
+        lw["q_gain"] = 0.5 + torch.rand(128, generator=g)
+        lw["k_gain"] = 0.5 + torch.rand(128, generator=g)
+        if "ve_gate" in lw:
+            lw["ve_gate"] = torch.randn(lw["ve_gate"].shape, generator=g) * 0.1
+            lw["ve"] = (torch.randn(lw["ve"].shape, generator=g) * 0.5).to(torch.bfloat16)
+    save_hf(m, tmp_path, max_positions=128)
+    model = load_hf(tmp_path, gpu)
+    rng = np.random.default_rng(55)
+    reqs = [Request(input_ids=[BOS] + rng.integers(8, cfg.vocab, n).tolist(), max_new_tokens=6,
+                    temperature=0.0 if k % 2 == 0 else 0.9, seed=70 + k) for k, n in enumerate([20, 33, 9, 26])]
+    dec = NativeDecoder(model, bos=BOS, max_length=48, batch=2)
+    got = dict(dec.generate(reqs))
+    checked = sum(check_alone(model, k, r, got[k]) for k, r in enumerate(reqs))
+    assert checked >= 12, checked
+
+
+def test_native_prompt_store_and_narrow_graphs(gpu):
+    """300 slots (the narrow graphs cover the first 256): requests in slots past 256 end first, the rest then run on
+    the narrow graphs; repeated prompts load their stored pages (and decode as their CPU runs alone)."""
+    print("native decoder: 300 slots, prompt store", flush=True)
+    model = RandomModel(TINY, gpu, seed=61)
+    rng = np.random.default_rng(62)
+    base = [BOS] + rng.integers(8, TINY.vocab, 22).tolist()
+    reqs = [Request(input_ids=base if k in (0, 299) else [BOS] + rng.integers(8, TINY.vocab, 5 + k % 9).tolist(),
+                    max_new_tokens=2 if k >= 256 else 5, temperature=0.0, seed=k) for k in range(300)]
+    dec = NativeDecoder(model, bos=BOS, max_length=48, prompt_store=256, batch=300)
+    got = dict(dec.generate(reqs))
+    assert sorted(got) == list(range(300))
+    assert dec.loads == 0  # every prompt was new when its slot started (all 300 start together)
+    again = dict(dec.generate([reqs[0], reqs[1]]))
+    assert dec.loads == 2  # both prompts come from the store now
+    checked = sum(check_alone(model, k, reqs[k], got[k]) for k in (0, 1, 2, 255, 256, 298))
+    checked += sum(check_alone(model, k, reqs[k], again[k]) for k in (0, 1))
+    assert checked >= 14, checked
+
+
+def test_native_rejected_bos_takes_the_alternative(gpu):
+    """Masks allowing only BOS and one token x, and requests that never accept BOS: every chosen BOS gives way to the
+    alternative through dec_take_alt, so each continuation is x repeated (the serving test, on the handle)."""
+    model = RandomModel(TINY, gpu, seed=41)
+    rng = np.random.default_rng(42)
+    reqs = []
+    for k in range(6):
+        allowed = np.zeros(TINY.vocab, bool)
+        allowed[[BOS, 100 + 37 * k]] = True
+        reqs.append(Request(input_ids=[BOS] + rng.integers(8, TINY.vocab, 12).tolist(), max_new_tokens=4,
+                            mask=lambda out, m=allowed: m, accept_bos=lambda out: False))
+    dec = NativeDecoder(model, bos=BOS, max_length=32, batch=3)
+    out = dict(dec.generate(reqs))
+    for k in range(6):
+        assert out[k] == [100 + 37 * k] * 4, (k, out[k])
+    assert dec.alts_taken > 0
