@@ -249,3 +249,14 @@ def test_decoder_handle_rejects_bad_configurations():
     assert not lib.dec_create_v2(cfg.ctypes.data, len(cfg), bad.ctypes.data, scal.ctypes.data, window.ctypes.data,
                                  NULL)
     assert "layer 1" in lib.nc_last_error().decode()
+
+
+def test_embed_and_mix_reject_bad_arguments():
+    lib = native.hip_library()
+    assert lib.nc_embed_rms_norm(FAKE, 0, 100, FAKE, 4, 260, FAKE, NULL) < 0 and "d" in lib.nc_last_error().decode()
+    assert lib.nc_embed_rms_norm(FAKE, 0, 0, FAKE, 4, 256, FAKE, NULL) < 0 and "vocab" in lib.nc_last_error().decode()
+    assert lib.nc_embed_rms_norm(NULL, 0, 100, FAKE, 4, 256, FAKE, NULL) < 0
+    assert lib.nc_embed_rms_norm(FAKE, 0, 100, FAKE, 0, 256, FAKE, NULL) == 0  # no rows, nothing launched
+    assert lib.nc_mix_bf16(FAKE, FAKE, 12, 1.0, 0.0, NULL) < 0 and "multiple of 8" in lib.nc_last_error().decode()
+    assert lib.nc_mix_bf16(NULL, FAKE, 16, 1.0, 0.0, NULL) < 0
+    assert lib.nc_mix_bf16(FAKE, FAKE, 0, 1.0, 0.0, NULL) == 0

@@ -1,6 +1,7 @@
 """GPU row kernels of the decoder against torch fp32 references of the same ops: the fused residual add + RMS norm
-(nc_add_rms_norm_bf16), relu^2 (nc_relu2_bf16) and the value-embedding mix (nc_value_embed_bf16). Rounded results
-agree within one bf16 step; the cases where the math is exact in fp32 agree bit for bit."""
+(nc_add_rms_norm_bf16), relu^2 (nc_relu2_bf16), the value-embedding mix (nc_value_embed_bf16), the embedding norm
+(nc_embed_rms_norm) and the residual mix (nc_mix_bf16). Rounded results agree within one bf16 step; the cases where
+the math is exact in fp32 agree bit for bit."""
 
 import numpy as np
 import pytest
@@ -132,3 +133,37 @@ def test_value_embed_gate_saturates(gpu):
     got = out.cpu()[:, v0:].view(rows, hkv, 128)
     assert torch.equal(got[:, 0], (v[:, 0] + 2 * e[:, 0]).to(torch.bfloat16))
     assert torch.equal(got[:, 1], v[:, 1].to(torch.bfloat16))
+
+
+def test_embed_norm_matches_the_row_norm_and_torch(gpu):
+    """nc_embed_rms_norm: a bf16 table gives add_rms_norm(table[tok]) bit for bit; an fp32 table is within one bf16
+    step of torch's fp64 norm; a token outside the vocabulary gives a zero row."""
+    from nanochat_amd.decoder import embed_norm
+
+    g = torch.Generator().manual_seed(12)
+    vocab, d = 500, 1664
+    table32 = torch.randn((vocab, d), generator=g) * 0.7
+    table16 = table32.to(torch.bfloat16)
+    tok = torch.tensor([0, 499, 17, 17, 500, -3, 250], dtype=torch.int32)
+    ok = (tok >= 0) & (tok < vocab)
+    got16 = embed_norm(table16.to(gpu), tok.to(gpu)).cpu()
+    want16 = add_rms_norm(table16.to(gpu)[tok.clamp(0, vocab - 1).long().to(gpu)].contiguous(), None).cpu()
+    assert torch.equal(got16[ok], want16[ok])
+    assert (got16[~ok].float() == 0).all()
+    got32 = embed_norm(table32.to(gpu), tok.to(gpu)).cpu()
+    want32 = F.rms_norm(table32[tok[ok].long()].double(), (d,), eps=EPS).to(torch.bfloat16)
+    assert ulps(got32[ok], want32) <= 1
+    assert (got32[~ok].float() == 0).all()
+
+
+def test_mix_matches_torch_bit_for_bit(gpu):
+    """nc_mix_bf16: bf16(lr x + l0 x0) with fp32 products and sum, exactly torch's three fp32 operations."""
+    from nanochat_amd.decoder import mix
+
+    g = torch.Generator().manual_seed(13)
+    x = (torch.randn(4096 + 8, generator=g) * 3).to(torch.bfloat16)
+    x0 = torch.randn(4096 + 8, generator=g).to(torch.bfloat16)
+    for lr, l0 in [(0.93, 0.11), (1.0, 0.0), (1.2, -0.2)]:
+        got = mix(x.to(gpu), x0.to(gpu), lr, l0).cpu()
+        a, b = torch.tensor(lr, dtype=torch.float32), torch.tensor(l0, dtype=torch.float32)
+        assert torch.equal(got, (a * x.float() + b * x0.float()).to(torch.bfloat16)), (lr, l0)
