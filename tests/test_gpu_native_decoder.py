@@ -43,13 +43,14 @@ def test_native_decoder_matches_each_request_alone(gpu):
 
 
 def test_native_decoder_runs_a_trained_like_export(gpu, tmp_path):
-    """Sliding windows, value embeddings, QK-norm gains and a non-identity residual / x0 mix (fp32 lambdas), loaded
-    from the export format: the handle's mix, value-embedding and window paths against the CPU model."""
+    """Grouped-query heads (4 over 2), sliding windows, value embeddings, QK-norm gains and a non-identity residual /
+    x0 mix (fp32 lambdas), loaded from the export format: the handle's GQA, mix, value-embedding and window paths
+    against the CPU model."""
     print("native decoder: trained-like export", flush=True)
     from nanochat_amd.checkpoint import load_hf, save_hf
 
-    cfg = ModelConfig(layers=4, d_model=256, heads=2, vocab=1000, theta=1e6, windows=(16, 16, 16, -1),
-                      ve_layers=(1, 3))
+    cfg = ModelConfig(layers=4, d_model=512, heads=4, vocab=1000, theta=1e6, windows=(16, 16, 16, -1),
+                      ve_layers=(1, 3), n_kv_heads=2)
     m = RandomModel(cfg, "cpu", seed=53)
     g = torch.Generator().manual_seed(54)
     m.resid_lambdas = 0.8 + 0.4 * torch.rand(cfg.layers, generator=g)
@@ -62,6 +63,7 @@ def test_native_decoder_runs_a_trained_like_export(gpu, tmp_path):
             lw["ve"] = (torch.randn(lw["ve"].shape, generator=g) * 0.5).to(torch.bfloat16)
     save_hf(m, tmp_path, max_positions=128)
     model = load_hf(tmp_path, gpu)
+    assert model.cfg.kv_heads == 2
     rng = np.random.default_rng(55)
     reqs = [Request(input_ids=[BOS] + rng.integers(8, cfg.vocab, n).tolist(), max_new_tokens=6,
                     temperature=0.0 if k % 2 == 0 else 0.9, seed=70 + k) for k, n in enumerate([20, 33, 9, 26])]
