@@ -27,6 +27,10 @@ from nanochat_amd.sampling import allow_rows
 from nanochat_amd.serving import Request
 
 
+def _destroy(lib, handle, stream, weights) -> None:
+    lib.dec_destroy(handle)
+
+
 class NativeDecoder:
     """Up to `batch` slots (0: as many as the free device memory holds, at most 1024) of max_length positions over
     `model`'s weights (kept referenced: the handle reads them through pointers); bos ends a continuation;
@@ -61,7 +65,8 @@ class NativeDecoder:
         if not handle:
             raise ValueError(lib.nc_last_error().decode())
         self.handle = ctypes.c_void_p(handle)
-        weakref.finalize(self, lib.dec_destroy, self.handle)
+        # the finalizer holds the stream and the weights, so both outlive the handle it destroys
+        weakref.finalize(self, _destroy, lib, self.handle, self.stream, weights)
         self.batch = B = lib.dec_batch(self.handle)
         self.tokens = np.zeros(2 * B, dtype=np.int32)  # dec_tokens: the choices, then their alternatives
         words = -(-cfg.vocab // 32)
