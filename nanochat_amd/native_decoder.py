@@ -28,6 +28,7 @@ from nanochat_amd.serving import Request
 
 
 def _destroy(lib, handle, stream, weights) -> None:
+    """dec_destroy; stream and weights are arguments only so that they stay referenced until the handle is gone."""
     lib.dec_destroy(handle)
 
 
