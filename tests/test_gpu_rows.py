@@ -3,7 +3,6 @@
 (nc_embed_rms_norm) and the residual mix (nc_mix_bf16). Rounded results agree within one bf16 step; the cases where
 the math is exact in fp32 agree bit for bit."""
 
-import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F

@@ -6,7 +6,6 @@ equal the served token wherever the choice is clear of the logit tolerance."""
 
 import numpy as np
 import pytest
-import torch
 
 from nanochat_amd.decoder import RandomModel
 from nanochat_amd.serving import Request, Server

@@ -6,7 +6,6 @@ operand, a wrong rounding mode) fails it; none retypes the oracle's own formula.
 import math
 
 import numpy as np
-import pytest
 import torch
 
 from oracle import golden as G
