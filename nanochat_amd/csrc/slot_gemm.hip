@@ -7,12 +7,13 @@
  * M rows of x, which stay L2-resident. The work unit is an output tile of NT weight rows x MT batch rows over the full
  * K, so the epilogue sees complete sums and the result is deterministic (no split-K atomics):
  *
- *   - a workgroup of 4 waves splits K into 4 contiguous ranges of 64-column chunks; each wave multiplies its range with
- *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles), loading its fragments straight from global
- *     memory with buffer loads (16 bytes per lane, the 4 lanes of a row covering 64 contiguous bytes of it), 2 to 7 chunks
- *     in flight in a register ring;
- *   - the 4 partial tiles meet in LDS and are summed in a fixed order, then the epilogue stores 4 adjacent outputs
- *     per lane;
+ *   - K is walked in 64-column chunks through an LDS ring of up to 8 slots; each chunk's NT + MT rows of 128 bytes
+ *     arrive by global_load_lds_dwordx4 (8 whole rows per instruction), shared evenly by the 4 waves, at a swizzled
+ *     position so the fragment reads (ds_read_b128) are bank-conflict free;
+ *   - the 4 waves split the tile as WN x 4 / WN over W rows and batch rows and multiply with
+ *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles); per chunk a wave waits for its own DMAs,
+ *     meets the others at one barrier, refills the slot everyone has finished, reads the next chunk's fragments
+ *     while this chunk's MFMAs run, and settles them;
  *   - the RMS norm of the input rows is fused: the same x fragments feed one more MFMA per 16 rows, x·xᵀ, whose
  *     diagonal is Σ x² of each row, so r = 1 / sqrt(Σ x² / K + FLT_EPSILON) (model/modeling.py:47-49, decode.cu:448-456)
  *     scales the sums in the epilogue instead of a separate normalised copy of x (the reference's RELU2 epilogue,
