@@ -100,8 +100,8 @@ def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_g
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
     check(hip_library().nc_decode_step_fp8(
-        pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos), pointer(sin),
-        cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks, cache.num_blocks, window, B,
+        pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos),
+        pointer(sin), cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks, cache.num_blocks, window, B,
         hq, cache.hkv, max_ctx, scale, pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
         stream()))
     return out
@@ -129,6 +129,6 @@ def prefill_attention(q: Tensor, cache: Fp8KVCache, pos: Tensor, seq: Tensor, *,
             raise ValueError("out must have q's shape")
     lib = hip_library()
     check(lib.nc_prefill_attn_fp8(pointer(q), pointer(pos), pointer(seq), n, pointer(cache.pages),
-                                  pointer(cache.block_table), cache.max_blocks, cache.num_blocks, cache.num_seqs, window,
-                                  hq, cache.hkv, scale, pointer(out), stream()))
+                                  pointer(cache.block_table), cache.max_blocks, cache.num_blocks, cache.num_seqs,
+                                  window, hq, cache.hkv, scale, pointer(out), stream()))
     return out

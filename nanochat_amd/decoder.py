@@ -10,8 +10,9 @@ prefilled, then every step feeds one token per sequence and appends the chosen o
 
 with x0 = norm(embed(token)), a final norm, the untied lm_head and the token choice (nc_choose_tokens: greedy, the
 largest fp32 logit with the lowest id on ties, unless set_sampling asks for temperature / nucleus sampling). The
-decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the reference's fused epilogues (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a
-per-row rstd, ReLU^2 into the up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
+decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the reference's fused epilogues
+(decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a per-row rstd, ReLU^2 into the
+up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
 through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
 attention and the token choice are HIP kernels throughout (a decode step's append and attention are one
 nc_decode_step_fp8 call per layer); the decode step is captured once in a hipGraph and replayed.
@@ -154,15 +155,16 @@ def rms_norm(x: Tensor) -> Tensor:
     return F.rms_norm(x.float(), (x.shape[-1],), eps=EPS).to(torch.bfloat16)
 
 
-def add_rms_norm(x: Tensor, delta: Tensor | None, x_out: Tensor | None = None) -> Tensor:
+def add_rms_norm(x: Tensor, delta: Tensor | None, x_out: Tensor | None = None, y: Tensor | None = None) -> Tensor:
     """nc_add_rms_norm_bf16 over rows of x (bf16 [n][d], contiguous): x_out = bf16(x + delta) (in place when x_out
-    is x), returns norm(x_out)."""
+    is x), returns norm(x_out) (written into y if given)."""
     _require(x, "x", torch.bfloat16, 2)
     n, d = x.shape
-    for t in (delta, x_out):
+    for t in (delta, x_out, y):
         if t is not None and (t.shape != x.shape or t.dtype != torch.bfloat16 or not t.is_contiguous()):
-            raise ValueError("delta / x_out must be contiguous bf16 of x's shape")
-    y = torch.empty_like(x)
+            raise ValueError("delta / x_out / y must be contiguous bf16 of x's shape")
+    if y is None:
+        y = torch.empty_like(x)
     check(hip_library().nc_add_rms_norm_bf16(pointer(x), pointer(delta), pointer(x_out), pointer(y), n, d,
                                              stream()))
     return y
@@ -261,13 +263,15 @@ class Fp8Decoder:
             self.softcap = float(softcap)
 
     # ---------------------------------------------------------------------------------------------- layers
-    def _qkv_append(self, l: int, x: Tensor, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor) -> Tensor:
+    def _qkv_append(self, l: int, x: Tensor, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor,
+                    q_out: Tensor) -> None:
         """h = norm(x); the projection (with the value-embedding mix), then QK-norm + RoPE + fp8 append of k, v;
-        returns q."""
+        q into q_out."""
         lw = self.model.layers[l]
         qkv = torch.matmul(h, lw["wqkv"].t())
         self._value_embed(l, qkv, x, tok)
-        return self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads)
+        self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
+                              q_out=q_out)
 
     def _mix(self, l: int, x: Tensor, x0: Tensor) -> None:
         """x = bf16(resid_lambdas[l] x + x0_lambdas[l] x0) in place (nc_mix_bf16; inference/modeling_nanochat.py:
@@ -285,13 +289,13 @@ class Fp8Decoder:
             return
         value_embed(qkv, x, tok, lw["ve"], lw["ve_gate"], self.cfg.heads, self.cfg.kv_heads)
 
-    def _finish_layer(self, l: int, x: Tensor, o: Tensor) -> Tensor:
-        """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; returns norm(x), the next layer's
-        (or the final) normed input."""
+    def _finish_layer(self, l: int, x: Tensor, o: Tensor, h: Tensor) -> None:
+        """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; h = norm(x), the next layer's (or
+        the final) normed input."""
         lw = self.model.layers[l]
         m = add_rms_norm(x, torch.matmul(o.reshape(o.shape[0], -1), lw["wo"].t()), x)
         u = relu2(torch.matmul(m, lw["wup"].t()))
-        return add_rms_norm(x, torch.matmul(u, lw["wdown"].t()), x)
+        add_rms_norm(x, torch.matmul(u, lw["wdown"].t()), x, y=h)
 
     def _embed(self, tok: Tensor) -> tuple[Tensor, Tensor]:
         """The residual stream x0 = norm(embed(tok)) and its norm, the first layer's input."""
@@ -327,11 +331,11 @@ class Fp8Decoder:
             for r0, r1 in chunks:
                 if self.mixes:
                     self._mix(l, x[r0:r1], x0[r0:r1])
-                    h[r0:r1] = add_rms_norm(x[r0:r1], None)
-                q[r0:r1] = self._qkv_append(l, x[r0:r1], h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1])
+                    add_rms_norm(x[r0:r1], None, y=h[r0:r1])
+                self._qkv_append(l, x[r0:r1], h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1], q[r0:r1])
             prefill_attention(q, self.caches[l], pos, seq, window=self.cfg.window(l), out=o)
             for r0, r1 in chunks:
-                h[r0:r1] = self._finish_layer(l, x[r0:r1], o[r0:r1])
+                self._finish_layer(l, x[r0:r1], o[r0:r1], h[r0:r1])
 
     # ---------------------------------------------------------------------------------------------- decode
     def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor, slots: Tensor | None = None) -> Tensor:

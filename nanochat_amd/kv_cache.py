@@ -88,11 +88,12 @@ class Fp8KVCache:
         return (pointer(self.pages), pointer(self.block_table), self.max_blocks, self.num_blocks, self.num_seqs)
 
     def append(self, qkv: Tensor, pos: Tensor, seq: Tensor, q_gain: Tensor, k_gain: Tensor, cos: Tensor,
-               sin: Tensor, hq: int, ctx_out: Tensor | None = None) -> Tensor:
+               sin: Tensor, hq: int, ctx_out: Tensor | None = None, q_out: Tensor | None = None) -> Tensor:
         """Fused append of n rows of the projection qkv bf16 [n][>= (hq + 2 hkv) 128] (q heads, k heads, v heads):
         q and k normed, gained and rotated at pos[n] (int32), k and v quantised into sequence seq[n]'s page.
         Returns q_out bf16 [n][hq][128]. Rows out of range write nothing and get a NaN q_out row. ctx_out (int32
-        [n], another tensor than pos) receives pos + 1: the context lengths for the decode step that follows."""
+        [n], another tensor than pos) receives pos + 1: the context lengths for the decode step that follows.
+        q_out: where to write q (contiguous bf16 [n][hq][128]), a new tensor if None."""
         if qkv.dim() != 2 or qkv.dtype != torch.bfloat16 or not qkv.is_cuda or qkv.stride(1) != 1:
             raise ValueError("qkv must be a row-major bf16 [n][width] GPU tensor")
         n = qkv.shape[0]
@@ -106,7 +107,10 @@ class Fp8KVCache:
             _require(ctx_out, "ctx_out", torch.int32, 1)
             if ctx_out.shape[0] != n:
                 raise ValueError(f"ctx_out has {ctx_out.shape[0]} rows, qkv {n}")
-        q_out = torch.empty((n, hq, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+        if q_out is None:
+            q_out = torch.empty((n, hq, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+        elif q_out.shape != (n, hq, HEAD_DIM) or q_out.dtype != torch.bfloat16 or not q_out.is_contiguous():
+            raise ValueError(f"q_out must be contiguous bf16 [{n}][{hq}][{HEAD_DIM}]")
         lib = hip_library()
         check(lib.nc_kv_append_fp8(pointer(qkv), qkv.stride(0), n, pointer(pos), pointer(seq), pointer(q_gain),
                                    pointer(k_gain), pointer(cos), pointer(sin), cos.shape[0], hq, self.hkv,

@@ -7,11 +7,12 @@ position and sampling parameters are set, and it joins the next decode step. Eac
 hipGraph over every slot: idle slots carry position -1, so the fused decode step does no work for them and the
 token choice (nc_choose_tokens' slot mask) leaves them untouched. As the reference's narrow graphs
 (decode.cu:32-33,995-1005,1090-1093), a second graph over the first `narrow` slots runs the steps in which no
-higher slot is active: its GEMMs, its lm_head and its choice cover those rows only. After a step the host reads the choices and
-finishes a slot on BOS (dropped; unless the request's accept_bos rejects it, when the step's alternative, the best
-token but BOS, is taken instead, as the reference's lazy BOS), at max_new_tokens, or when the request's stopping
-criteria hold for its tokens, then refills it. A request's mask callable, if any, gives the next position's allowed tokens (the reference's
-constraints, decode.cu:1077-1094's dec_masks rows); a masked slot chooses among them, -1 when none is allowed.
+higher slot is active: its GEMMs, its lm_head and its choice cover those rows only. After a step the host reads
+the choices and finishes a slot on BOS (dropped; unless the request's accept_bos rejects it, when the step's
+alternative, the best token but BOS, is taken instead, as the reference's lazy BOS), at max_new_tokens, or when the
+request's stopping criteria hold for its tokens, then refills it. A request's mask callable, if any, gives the next
+position's allowed tokens (the reference's constraints, decode.cu:1077-1094's dec_masks rows); a masked slot
+chooses among them, -1 when none is allowed.
 
 The prompt store (decode.cu:1053-1075; inference/decoder.py:196-232): pinned host memory for `prompt_store`
 positions. A prefilled prompt's cache pages (every layer's fp8 codes and scales of the slot's first ceil(n / 16)
