@@ -101,9 +101,9 @@ def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_g
         raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
     check(hip_library().nc_decode_step_fp8(
         pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos),
-        pointer(sin), cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks, cache.num_blocks, window, B,
-        hq, cache.hkv, max_ctx, scale, pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(),
-        stream()))
+        pointer(sin), cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks,
+        cache.num_blocks, window, B, hq, cache.hkv, max_ctx, scale, pointer(out), pointer(workspace),
+        workspace.numel() * workspace.element_size(), stream()))
     return out
 
 
