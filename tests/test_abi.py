@@ -260,3 +260,28 @@ def test_embed_and_mix_reject_bad_arguments():
     assert lib.nc_mix_bf16(FAKE, FAKE, 12, 1.0, 0.0, NULL) < 0 and "multiple of 8" in lib.nc_last_error().decode()
     assert lib.nc_mix_bf16(NULL, FAKE, 16, 1.0, 0.0, NULL) < 0
     assert lib.nc_mix_bf16(FAKE, FAKE, 0, 1.0, 0.0, NULL) == 0
+
+
+def test_a_c_caller_compiles_links_and_runs(tmp_path):
+    """The header is plain C: a C program includes it, links libnanochat_amd.so and calls the host-only entry points
+    (no device work), the way a C or cgo caller would."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    lib = Path(native.hip_library()._name)
+    src = tmp_path / "caller.c"
+    src.write_text('#include "nanochat_amd.h"\n#include <stdio.h>\n'
+                   'int main(void) {\n'
+                   '    printf("%d %lld %lld\\n", nc_abi_version(), nc_decode_workspace_bytes(64, 16, 4, 8192),\n'
+                   '           nc_choose_workspace_bytes(8, 1000));\n'
+                   '    return nc_decode_attn_fp8(0, 0, 0, 0, 0, 0, -1, 1, 16, 4, 16, 1.0f, 0, 0, 0, 0) < 0 ? 0 : 1;\n'
+                   '}\n')
+    exe = tmp_path / "caller"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{HEADER.parent}", str(src), f"-L{lib.parent}",
+                    "-lnanochat_amd", f"-Wl,-rpath,{lib.parent}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out[0] == "1"
+    assert int(out[1]) == native.hip_library().nc_decode_workspace_bytes(64, 16, 4, 8192)
+    assert int(out[2]) == native.hip_library().nc_choose_workspace_bytes(8, 1000)
