@@ -230,11 +230,7 @@ struct PfQ8 {
     int scale;
 };
 
-__device__ __forceinline__ float e4m3_value(uint32_t c) {
-    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-    const float v = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f; /* m 2^-9 */
-    return (c & 0x80u) ? -v : v;
-}
+typedef short pf_i16x2 __attribute__((ext_vector_type(2)));
 
 /* 32 bf16 of q (this lane's dims 32j .. 32j+31 of its column) -> the two e4m3 terms; the column's exponent from
  * its absmax over the four lanes holding it (xor 16, 32). A zero column gives zero terms. */
@@ -259,18 +255,23 @@ __device__ PfQ8 quantize_q(const u32x4 (&u)[4]) {
     const float up = __uint_as_float((uint32_t)(e + 127) << 23);
     PfQ8 q;
     q.scale = max(min(127 - e, 254), 0);
+    /* the hardware conversions (round to nearest even; |v| < 256 is in range): byte b of a dword is element b */
 #pragma unroll
     for (int w = 0; w < 8; w++) {
-        uint32_t hi = 0, lo = 0;
+        float v[4];
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const float v = x[4 * w + b] * up; /* exact: a power of two */
-            const uint32_t ch = f32_to_e4m3(v);
-            hi |= ch << (8 * b);
-            lo |= f32_to_e4m3(v - e4m3_value(ch)) << (8 * b); /* the remainder is exact in fp32 */
-        }
-        q.hi[w] = (int)hi;
-        q.lo[w] = (int)lo;
+        for (int b = 0; b < 4; b++) v[b] = x[4 * w + b] * up; /* exact: a power of two */
+        pf_i16x2 h = {0, 0}, l = {0, 0};
+        h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(h, v[0], v[1], 1.0f, false);
+        h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(h, v[2], v[3], 1.0f, true);
+        const uint32_t hu = __builtin_bit_cast(uint32_t, h);
+        const f32x2 d01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hu, 1.0f, false);
+        const f32x2 d23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hu, 1.0f, true);
+        /* the remainders v - hi are exact in fp32 */
+        l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(l, v[0] - d01[0], v[1] - d01[1], 1.0f, false);
+        l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(l, v[2] - d23[0], v[3] - d23[1], 1.0f, true);
+        q.hi[w] = (int)hu;
+        q.lo[w] = __builtin_bit_cast(int, l);
     }
     return q;
 }
@@ -414,6 +415,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
               const int32_t *__restrict__ block_table) {
     __shared__ __attribute__((aligned(16))) unsigned char ring[PF_RING * PF_PAIR_BYTES];
     __shared__ __attribute__((aligned(16))) int ids[PF_IDS];
+    __shared__ int2 rows_ps[PF_WAVES * PF_BLOCKS * 16]; /* the tile's (position, sequence) pairs */
 
     /* XCD-aware unit order: workgroup b runs on XCD b % 8, which takes a contiguous range of units, so the row
      * tiles of one (sequence, kv head) -- the readers of the same pages -- share an L2 */
@@ -452,12 +454,19 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     st.w = pf_exp2i(126);
     st.vlim = pf_exp2i(-126);
 
+    /* the tile's positions and sequences, read once into LDS ((-1, -1) past the rows) */
+    for (int k = tid; k < TR; k += PF_THREADS) {
+        const int r = row0 + k;
+        rows_ps[k] = r < a.n ? make_int2(pos[r], seq[r]) : make_int2(-1, -1);
+    }
+    __syncthreads();
+
     /* rows of the tile still to attend, 4 per lane (row0 + lane + 64 i); every wave derives the same segments */
     unsigned pend = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int k = lane + 64 * i, r = row0 + k;
-        if (k < TR && r < a.n && row_valid(a, pos[r], seq[r])) pend |= 1u << i;
+        const int k = lane + 64 * i;
+        if (k < TR && row_valid(a, rows_ps[k].x, rows_ps[k].y)) pend |= 1u << i;
     }
 
     for (;;) {
@@ -468,7 +477,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             const unsigned long long bal = __ballot((pend >> i) & 1);
             if (s < 0 && bal) {
                 const int src = __builtin_ctzll(bal);
-                s = __shfl((pend >> i) & 1 ? seq[row0 + lane + 64 * i] : -1, src, 64);
+                s = __shfl((pend >> i) & 1 ? rows_ps[lane + 64 * i].y : -1, src, 64);
             }
         }
         s = __builtin_amdgcn_readfirstlane(s);
@@ -476,9 +485,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         int lo = PF_NO_KEY, hi = -1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int r = row0 + lane + 64 * i;
-            if ((pend >> i) & 1 && seq[r] == s) {
-                const int p = pos[r];
+            const int k = lane + 64 * i;
+            if ((pend >> i) & 1 && rows_ps[k].y == s) {
+                const int p = rows_ps[k].x;
                 lo = min(lo, key_lo(a, p));
                 hi = max(hi, p);
                 pend &= ~(1u << i);
@@ -494,7 +503,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
             const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
             const bool used = n < R * G && r < a.n;
-            const int p = used ? pos[r] : -1, sq = used ? seq[r] : -1;
+            const int2 ps = used ? rows_ps[r - row0] : make_int2(-1, -1);
+            const int p = ps.x, sq = ps.y;
             const bool ok = used && row_valid(a, p, sq), in_seg = ok && sq == s;
             other |= ok && !in_seg;
             mine |= in_seg;
@@ -582,7 +592,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         l += shfl_xor_f(l, 32);
         const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
         if (!(n < R * G && r < a.n)) continue;
-        const bool zero = !(row_valid(a, pos[r], seq[r]) && l > 0.f); /* +0, not o * 0 (which keeps signs) */
+        const int2 ps = rows_ps[r - row0];
+        const bool zero = !(row_valid(a, ps.x, ps.y) && l > 0.f); /* +0, not o * 0 (which keeps signs) */
         const float inv = zero ? 0.f : scale_unit / l;
         bf16_t *dst = a.out + ((size_t)r * a.hq + h * G + n % G) * NC_HEAD_DIM;
 #pragma unroll
