@@ -72,6 +72,23 @@ int nc_kv_gather_fp8(const uint8_t *cache, const int32_t *block_table, int max_b
                      const int32_t *ctx_len, int B, int hkv, int max_ctx, uint8_t *k_out, uint8_t *v_out,
                      float *ks_out, float *vs_out, void *stream);
 
+/* Position rows: positions [at, at + n) of sequence seq (any at, any n), every kv head, in `layers` pools spaced
+ * pool_bytes apart (layer l's pool at cache + l * pool_bytes), to rows (uint8 [layers][n][hkv][264]: K codes
+ * 128 B, V codes 128 B in dim order, K scale fp32, V scale fp32). A position whose block is missing gives a zero
+ * row. Requires 0 <= seq < num_seqs, at + n <= max_blocks * 16.
+ * Replaces: the device side of prompt_copy, model/kernels/decode.cu:1053-1075 (slot K/V rows to the prompt store,
+ * position-granular bf16 rows there). */
+int nc_kv_export_fp8(const uint8_t *cache, long long pool_bytes, int layers, const int32_t *block_table,
+                     int max_blocks, int num_blocks, int num_seqs, int seq, int at, int n, int hkv, uint8_t *rows,
+                     void *stream);
+
+/* The inverse of nc_kv_export_fp8: rows (uint8 [layers][n][hkv][264]) into positions [at, at + n) of sequence seq;
+ * only those positions' bytes of the pages change, and a position whose block is missing is not written.
+ * Replaces: the load direction of prompt_copy, model/kernels/decode.cu:1053-1075. */
+int nc_kv_import_fp8(const uint8_t *rows, int layers, uint8_t *cache, long long pool_bytes,
+                     const int32_t *block_table, int max_blocks, int num_blocks, int num_seqs, int seq, int at, int n,
+                     int hkv, void *stream);
+
 /* Workspace bytes nc_decode_attn_fp8 needs for B sequences of hq / hkv heads (independent of max_ctx and of the
  * device): a partial-result slot (Σ p v, max, sum) per wave and per (sequence, kv head). */
 long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx);
@@ -201,7 +218,9 @@ int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi
  * layer, captured step graphs over all slots and over the first 256, pinned token and mask buffers, and a prompt
  * store in pinned host memory. One host thread; every call is ordered on the handle's stream (the caller's, not the
  * legacy default stream, alive past dec_destroy); dec_tokens is the only call that waits. Weights are borrowed and
- * must stay unchanged while the handle lives.
+ * must stay unchanged while the handle lives. As the reference's handle (decode.cu:47-53,927-931), a call that cannot
+ * do what it was asked (an argument out of range, a failed HIP call) prints a message and aborts; only
+ * dec_create_v2, which the reference does not have, returns NULL with nc_last_error() instead.
  */
 
 /* cfg: L, C (hidden size, a multiple of 128), F (MLP width, a multiple of 64), vocab (<= 131072), max_len (positions
@@ -210,14 +229,15 @@ int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi
  * (bf16 [vocab][C]), then per layer qkv ([(H + 2 Hkv) 128][C]), o, up ([F][C]), down ([C][F]) (bf16), the
  * value-embedding table (bf16 [vocab][Hkv 128]) and its gate (fp32 [Hkv][C]) or 0, 0, and the q and k norm gains
  * (fp32 [128]). scal: per layer the residual and x0 lambdas, then the logit cap. window: per layer, keys before a
- * query (< 0: all). Returns NULL on a bad argument (nc_last_error). H = C / 128; the slot count is the most whose
- * caches fit the free device memory, at most 1024.
+ * query (< 0: all). Aborts with a message on a bad argument. H = C / 128; the slot count is the most whose caches
+ * fit the free device memory, at most 1024.
  * Replaces: dec_create, model/kernels/decode.cu:950-1023 (same arguments; the cache is fp8). */
 void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream);
 
 /* dec_create with ncfg configuration fields: cfg[7] Hkv (0: H), cfg[8] the slot count (0: as dec_create),
- * cfg[9] 1 for a bf16 embedding table. No counterpart in the reference: its fields 0-6 keep their meaning and the
- * new ones are appended, as the grouped-query caches and bf16 checkpoint exports need. */
+ * cfg[9] 1 for a bf16 embedding table. Returns NULL on a bad argument (nc_last_error). No counterpart in the
+ * reference: its fields 0-6 keep their meaning and the new ones are appended, as the grouped-query caches and bf16
+ * checkpoint exports need. */
 void *dec_create_v2(const int *cfg, int ncfg, const uint64_t *ptrs, const float *scal, const int *window,
                     void *stream);
 
@@ -236,15 +256,17 @@ void dec_set_prompt(void *handle, int b, int32_t token, int32_t last, float temp
                     unsigned long long seed);
 
 /* Runs n <= dec_prefill_rows rows (rows: int32 [3][n], tokens, positions, slots) through every layer, caching each
- * row's key and value; a row attends its slot's cached positions and the earlier rows of the call. Waits for the
- * handle's previous work before reading rows. Replaces: dec_prefill, decode.cu:1041-1051. */
+ * row's key and value; a row attends its slot's cached positions and the earlier rows of the call. Stream-ordered:
+ * rows is copied into one of a ring of pinned staging buffers before the call returns (the host waits only when
+ * that buffer's copy from 4 calls earlier is still pending). Replaces: dec_prefill, decode.cu:1041-1051. */
 void dec_prefill(void *handle, int n, const int32_t *rows);
 
-/* Slot b's cache pages holding positions [at, at + n) to the prompt store's pages from position store_at (save)
- * or back (load), every layer; whole 16-position pages (at and store_at multiples of 16). Returns 0 or a negative
- * status. Replaces: dec_save_prompt / dec_load_prompt, decode.cu:1069-1075 (position-granular bf16 rows there). */
-int dec_save_prompt(void *handle, int b, int at, int store_at, int n);
-int dec_load_prompt(void *handle, int b, int at, int store_at, int n);
+/* Slot b's cache positions [at, at + n), every layer, to the prompt store's positions [store_at, store_at + n)
+ * (save) or back (load); any positions (the store holds nc_kv_export_fp8 rows, [L][store][Hkv][264]). Stream-ordered.
+ * A slot, range or store position out of bounds aborts with a message, as every other failure of the handle.
+ * Replaces: dec_save_prompt / dec_load_prompt, decode.cu:1069-1075 (bf16 rows there). */
+void dec_save_prompt(void *handle, int b, int at, int store_at, int n);
+void dec_load_prompt(void *handle, int b, int at, int store_at, int n);
 
 /* The pinned allowed-token rows [B][ceil(vocab / 32)] (bit t % 32 of word t / 32 of row b: slot b may choose t),
  * written by the caller between dec_tokens and dec_set_active. Replaces: dec_masks, decode.cu:1079. */

@@ -55,7 +55,7 @@
 #ifndef DEC_DEPTH
 #define DEC_DEPTH 4         /* page buffers per wave: 3 pages (12.4 KiB) in flight while one is computed */
 #endif
-/* Schedule units (page equivalents, measured on config 3 with NC_DECODE_UNITS sweeps) of a piece start (the
+/* Schedule units (page equivalents, measured on config 3 by sweeping these values) of a piece start (the
  * segment's context length and block ids: two dependent round trips) and of a segment's end (the fused step's q
  * rows and the append's quantisation; the same in both entry points, so that they split the work alike and give
  * bit-identical outputs). */
@@ -696,30 +696,13 @@ static int decode_waves() {
         /* CDNA: 4 SIMDs per CU. Resident waves beyond DEC_WAVES_PER_SIMD per SIMD are not used: a second wave on
          * a SIMD loses issue arbitration to the older one and finishes its equal share last. */
         if (per_cu > 4 * DEC_WAVES_PER_SIMD) per_cu = 4 * DEC_WAVES_PER_SIMD;
-        const char *e = getenv("NC_DECODE_WAVES"); /* tuning knob: a smaller persistent grid */
-        int w = per_cu * cus;
-        if (e && atoi(e) > 0 && atoi(e) < w) w = atoi(e);
+        const int w = per_cu * cus;
         cached[dev] = w < 1 ? 1 : (w > DEC_MAX_WAVES ? DEC_MAX_WAVES : w);
     }
     return cached[dev];
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-/* Schedule units (page equivalents) a segment costs besides its pages: starting a piece there, and ending it.
- * NC_DECODE_UNITS="start,end" overrides them (a tuning knob, read once per process). */
-static void schedule_units(int *start, int *end) {
-    static int s = -1, e = 0;
-    if (s < 0) {
-        int v[2] = {DEC_UNITS_START, DEC_UNITS_END};
-        const char *env = getenv("NC_DECODE_UNITS");
-        if (env) sscanf(env, "%d,%d", &v[0], &v[1]);
-        e = v[1] < 0 ? 0 : v[1];
-        s = v[0] < 0 ? 0 : v[0];
-    }
-    *start = s;
-    *end = e;
-}
 
 /* Partial-result slots: the first DEC_MERGE_DIRECT pieces of every segment, then one per (wave, segment) offset. */
 static size_t merge_slots(size_t S) { return S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S; }
@@ -759,7 +742,8 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     a.ws_ml = (float *)ws;
     ws += align256(slots * a.group * 2 * sizeof(float));
     a.ws_desc = (int2 *)ws;
-    schedule_units(&a.unit_start, &a.unit_end);
+    a.unit_start = DEC_UNITS_START;
+    a.unit_end = DEC_UNITS_END;
     const int W = decode_waves();
     if (fused)
         hipLaunchKernelGGL(k_decode<true>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
@@ -786,12 +770,12 @@ extern "C" int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int
     return decode_launch(a, false, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
 }
 
-extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
-                                  const float *q_gain,
-                                  const float *k_gain, const float *cos, const float *sin, int rope_len,
-                                  uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks,
-                                  int window, int B, int hq, int hkv, int max_ctx, float sm_scale, void *out,
-                                  void *workspace, long long workspace_bytes, void *stream) {
+/* The fused step's checks and launch, shared by the workspace and the static-scratch entry points. */
+static int decode_step(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                       const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                       uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks, int window, int B,
+                       int hq, int hkv, int max_ctx, float sm_scale, void *out, void *workspace,
+                       long long workspace_bytes, void *stream) {
     NC_REQUIRE(B >= 0, "B = %d < 0", B);
     if (B == 0) return 0;
     NC_REQUIRE(hkv > 0 && hq > 0 && hq % hkv == 0, "hq = %d must be a positive multiple of hkv = %d", hq, hkv);
@@ -813,4 +797,14 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const i
     a.cos = cos; a.sin = sin; a.rope_len = rope_len;
     a.window = window; a.B = B; a.hq = hq; a.hkv = hkv;
     return decode_launch(a, true, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
+}
+
+extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                                  const float *q_gain, const float *k_gain, const float *cos, const float *sin,
+                                  int rope_len, uint8_t *cache, const int32_t *block_table, int max_blocks,
+                                  int num_blocks, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
+                                  void *out, void *workspace, long long workspace_bytes, void *stream) {
+    return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, workspace, workspace_bytes,
+                       stream);
 }

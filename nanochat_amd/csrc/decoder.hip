@@ -12,7 +12,13 @@
  *   - two captured hipGraphs per width, the body (embedding, norm, every layer) and the head (lm_head and the token
  *     choice with its commit), over all B slots and, when B > DEC_NARROW, over the first DEC_NARROW slots (the
  *     reference's narrow graphs, decode.cu:995-1005);
- *   - pinned host memory for the tokens, the allowed-token rows (dec_masks) and the prompt store.
+ *   - pinned host memory for the tokens, the allowed-token rows (dec_masks), a ring of DEC_STAGES prefill row
+ *     buffers and the prompt store, and a device staging buffer for the store's copies.
+ *
+ * The prompt store holds positions as nc_kv_export_fp8 rows, [L][store][Hkv][264] (a position's K and V codes
+ * and scales), so dec_save_prompt / dec_load_prompt move any positions of a slot to any store positions: a kernel
+ * packs the slot's pages into the staging rows and one 2-D copy moves them (L rows of n positions) to the store, or
+ * the reverse. Everything is ordered on the handle's stream.
  *
  * A decode step is dec_set_active, dec_launch_body, dec_launch_head, dec_tokens. The body runs per layer: the
  * residual mix (nc_mix_bf16, where it is not the identity), the qkv slot GEMM of the normed rows, the
@@ -22,7 +28,12 @@
  * carry position -1: the decode step does no work for them and the choice leaves them untouched.
  *
  * Small host-to-device updates (a slot's prompt state, the slot words, dec_take_alt) are kernels whose values travel
- * in the kernel arguments, so no host buffer is read after the call returns.
+ * in the kernel arguments, so no host buffer is read after the call returns. dec_prefill's rows (up to 12 KB) go
+ * through the ring of pinned buffers, each guarded by an event recorded after its copy.
+ *
+ * Errors follow the reference's handle (decode.cu:47-53,927-931): an argument out of range or a failed HIP call
+ * prints a message and aborts, so a caller that ignores return values never decodes from a cache it did not get.
+ * dec_create_v2 alone returns NULL (with nc_last_error) on a bad configuration.
  */
 #include <string.h>
 
@@ -32,6 +43,8 @@
 #define DEC_MAX_BATCH 1024 /* slots at most (decode.cu:28-29) */
 #define DEC_NARROW 256     /* the narrow graphs' slots (decode.cu:32-33) */
 #define DEC_ROWS 1024      /* prefill rows per dec_prefill (decode.cu:1037) */
+#define DEC_STAGES 4       /* pinned staging buffers of prefill rows in flight */
+#define DEC_ROW_BYTES 264  /* one position of one kv head in the prompt store (nc_kv_export_fp8's rows) */
 #define DEC_WORDS (DEC_MAX_BATCH / 64)
 #define DEC_GLOBAL_PTRS 4
 #define DEC_LAYER_PTRS 8
@@ -52,7 +65,7 @@ struct DecRows {
 };
 
 struct Decoder {
-    int L, C, F, vocab, vocab_pad, max_len, store_pages, lazy, H, Hkv, B, max_blocks, wte_fp32, mixes, words;
+    int L, C, F, vocab, vocab_pad, max_len, store_len, lazy, H, Hkv, B, max_blocks, wte_fp32, mixes, words;
     float softcap;
     const void *wte, *lm_head;
     const float *cos, *sin;
@@ -69,9 +82,12 @@ struct Decoder {
     uint32_t *allow;              /* [B][vocab / 32] */
     void *ws_dec, *ws_choose;
     long long ws_dec_bytes, ws_choose_bytes;
-    int32_t *host_tokens, *host_rows;
+    int32_t *host_tokens, *host_rows; /* host_rows: pinned [DEC_STAGES][3][DEC_ROWS] */
+    hipEvent_t staged[DEC_STAGES];    /* recorded after the copy out of host_rows' stage */
+    int stage;                        /* the next stage dec_prefill fills */
     uint32_t *host_allow;
-    uint8_t *store; /* pinned [L][store_pages][Hkv][4224] */
+    uint8_t *store;   /* pinned [L][store][Hkv][264] */
+    uint8_t *staging; /* device [L][max_len][Hkv][264]: a prompt's rows between the slot and the store */
     int narrow;     /* the next launches use the narrow graphs */
     hipGraphExec_t body[2], head[2];
     void *blocks[32]; /* device allocations, freed by dec_destroy */
@@ -241,6 +257,8 @@ extern "C" void dec_destroy(void *handle) {
         if (d->body[i]) (void)hipGraphExecDestroy(d->body[i]);
         if (d->head[i]) (void)hipGraphExecDestroy(d->head[i]);
     }
+    for (int i = 0; i < DEC_STAGES; i++)
+        if (d->staged[i]) (void)hipEventDestroy(d->staged[i]);
     for (int i = 0; i < d->nblocks; i++) (void)hipFree(d->blocks[i]);
     for (void *p : {(void *)d->host_tokens, (void *)d->host_rows, (void *)d->host_allow, (void *)d->store})
         if (p) (void)hipHostFree(p);
@@ -269,7 +287,7 @@ static int create(Decoder *d, const int *cfg, int ncfg, const uint64_t *ptrs, co
                d->Hkv);
     NC_REQUIRE(cfg[5] >= 0 && batch >= 0 && batch <= DEC_MAX_BATCH, "dec_create: store %d, batch %d", cfg[5], batch);
     d->max_blocks = (d->max_len + NC_PAGE - 1) / NC_PAGE;
-    d->store_pages = (cfg[5] + NC_PAGE - 1) / NC_PAGE;
+    d->store_len = cfg[5]; /* prompt-store positions */
     d->vocab_pad = (d->vocab + 31) / 32 * 32;
     d->wte = (const void *)ptrs[0];
     d->cos = (const float *)ptrs[1];
@@ -324,12 +342,19 @@ static int create(Decoder *d, const int *cfg, int ncfg, const uint64_t *ptrs, co
     NC_HIP_CHECK(hipMemsetD32Async((hipDeviceptr_t)d->d.pos, -1, d->B, d->stream)); /* every slot idle */
     NC_HIP_CHECK(hipMemsetD32Async((hipDeviceptr_t)d->top_p, 0x3f800000, d->B, d->stream)); /* top_p 1 */
     NC_HIP_CHECK(hipHostMalloc((void **)&d->host_tokens, 2 * (size_t)d->B * sizeof(int32_t), hipHostMallocDefault));
-    NC_HIP_CHECK(hipHostMalloc((void **)&d->host_rows, 3 * (size_t)DEC_ROWS * sizeof(int32_t), hipHostMallocDefault));
+    NC_HIP_CHECK(hipHostMalloc((void **)&d->host_rows, DEC_STAGES * 3 * (size_t)DEC_ROWS * sizeof(int32_t),
+                               hipHostMallocDefault));
+    for (int i = 0; i < DEC_STAGES; i++) { /* recorded once, so the first wait on each stage returns at once */
+        NC_HIP_CHECK(hipEventCreateWithFlags(&d->staged[i], hipEventDisableTiming));
+        NC_HIP_CHECK(hipEventRecord(d->staged[i], d->stream));
+    }
     NC_HIP_CHECK(hipHostMalloc((void **)&d->host_allow, (size_t)d->B * allow_words * 4, hipHostMallocDefault));
     memset(d->host_allow, 0, (size_t)d->B * allow_words * 4);
-    if (d->store_pages)
-        NC_HIP_CHECK(hipHostMalloc((void **)&d->store,
-                                   (size_t)d->L * d->store_pages * d->Hkv * NC_TILE_BYTES, hipHostMallocDefault));
+    if (d->store_len) {
+        const size_t position = (size_t)d->L * d->Hkv * DEC_ROW_BYTES;
+        NC_HIP_CHECK(hipHostMalloc((void **)&d->store, position * d->store_len, hipHostMallocDefault));
+        d->staging = (uint8_t *)dec_alloc(d, position * d->max_len);
+    }
     /* every launch path once eagerly (no slot active: nothing is written but scratch rows), then the graphs */
     const int widths[2] = {d->B, d->B > DEC_NARROW ? DEC_NARROW : 0};
     for (int g = 0; g < 2; g++) {
@@ -367,8 +392,14 @@ extern "C" void *dec_create_v2(const int *cfg, int ncfg, const uint64_t *ptrs, c
     return d;
 }
 
+/* The reference's entry point aborts where dec_create_v2 returns NULL: its caller does not check the handle. */
 extern "C" void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream) {
-    return dec_create_v2(cfg, 7, ptrs, scal, window, stream);
+    void *h = dec_create_v2(cfg, 7, ptrs, scal, window, stream);
+    if (!h) {
+        fprintf(stderr, "dec_create: %s\n", nc_last_error());
+        abort();
+    }
+    return h;
 }
 
 extern "C" int dec_batch(void *handle) { return ((Decoder *)handle)->B; }
@@ -396,46 +427,61 @@ extern "C" void dec_prefill(void *handle, int n, const int32_t *rows) {
         fprintf(stderr, "dec_prefill: %d rows exceed %d\n", n, DEC_ROWS);
         abort();
     }
-    NC_HIP_CHECK(hipStreamSynchronize(d->stream)); /* the staging rows of the previous call are consumed */
-    for (int k = 0; k < 3; k++) memcpy(d->host_rows + k * DEC_ROWS, rows + (size_t)k * n, n * sizeof(int32_t));
-    NC_HIP_CHECK(hipMemcpyAsync(d->r.tok, d->host_rows, 3 * (size_t)DEC_ROWS * sizeof(int32_t),
-                                hipMemcpyHostToDevice, d->stream));
+    /* the stage's previous copy (DEC_STAGES calls ago) has read its buffer: usually long done, so no wait */
+    const int k = d->stage;
+    d->stage = (k + 1) % DEC_STAGES;
+    NC_HIP_CHECK(hipEventSynchronize(d->staged[k]));
+    int32_t *host = d->host_rows + (size_t)k * 3 * DEC_ROWS;
+    for (int c = 0; c < 3; c++) memcpy(host + c * DEC_ROWS, rows + (size_t)c * n, n * sizeof(int32_t));
+    NC_HIP_CHECK(hipMemcpyAsync(d->r.tok, host, 3 * (size_t)DEC_ROWS * sizeof(int32_t), hipMemcpyHostToDevice,
+                                d->stream));
+    NC_HIP_CHECK(hipEventRecord(d->staged[k], d->stream));
     if (enqueue_prefill(d, n) < 0) {
         fprintf(stderr, "dec_prefill: %s\n", nc_last_error());
         abort();
     }
 }
 
-/* Slot b's cache pages holding positions [at, at + n) to or from the store's pages from store_at: page-granular (a
- * page's codes interleave its 16 positions), so at and store_at are multiples of 16 and whole pages move. */
-static int prompt_copy(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
-    NC_REQUIRE(b >= 0 && b < d->B && n >= 0, "prompt copy: slot %d, %d positions", b, n);
-    NC_REQUIRE(at % NC_PAGE == 0 && store_at % NC_PAGE == 0, "prompt copy: at %d and store_at %d must be multiples of %d",
-               at, store_at, NC_PAGE);
-    const int pages = (n + NC_PAGE - 1) / NC_PAGE, p0 = at / NC_PAGE, s0 = store_at / NC_PAGE;
-    NC_REQUIRE(p0 + pages <= d->max_blocks && s0 + pages <= d->store_pages,
-               "prompt copy: pages [%d, %d) of the slot, [%d, %d) of the store (%d pages)", p0, p0 + pages, s0,
-               s0 + pages, d->store_pages);
-    if (!pages) return 0;
-    const size_t tile = (size_t)d->Hkv * NC_TILE_BYTES, width = pages * tile;
-    uint8_t *slot = d->cache + ((size_t)b * d->max_blocks + p0) * tile;
-    uint8_t *store = d->store + (size_t)s0 * tile;
-    const size_t slot_pitch = d->pool_bytes, store_pitch = (size_t)d->store_pages * tile;
-    if (to_store)
-        NC_HIP_CHECK(hipMemcpy2DAsync(store, store_pitch, slot, slot_pitch, width, d->L, hipMemcpyDeviceToHost,
+/* Slot b's positions [at, at + n), every layer, to or from the store's positions [store_at, store_at + n): the
+ * slot's pages <-> the staging rows by nc_kv_export_fp8 / nc_kv_import_fp8, the staging rows <-> the store by one
+ * 2-D copy (L rows of n positions; the store's pitch is its whole layer). Out-of-range arguments abort. */
+static void prompt_copy(Decoder *d, const char *name, int b, int at, int store_at, int n, bool to_store) {
+    if (b < 0 || b >= d->B || at < 0 || n < 0 || store_at < 0 || (long long)at + n > d->max_len ||
+        (long long)store_at + n > d->store_len) {
+        fprintf(stderr, "%s: slot %d (of %d), positions [%d, %lld) (of %d), store positions [%d, %lld) (of %d)\n",
+                name, b, d->B, at, (long long)at + n, d->max_len, store_at, (long long)store_at + n, d->store_len);
+        abort();
+    }
+    if (n == 0) return;
+    const size_t position = (size_t)d->Hkv * DEC_ROW_BYTES, width = (size_t)n * position;
+    uint8_t *store = d->store + (size_t)store_at * position;
+    const size_t store_pitch = (size_t)d->store_len * position;
+    const int num_blocks = d->B * d->max_blocks;
+    int rc = 0;
+    if (to_store) {
+        rc = nc_kv_export_fp8(d->cache, (long long)d->pool_bytes, d->L, nullptr, d->max_blocks, num_blocks, d->B, b,
+                              at, n, d->Hkv, d->staging, d->stream);
+        if (rc == 0)
+            NC_HIP_CHECK(hipMemcpy2DAsync(store, store_pitch, d->staging, width, width, d->L, hipMemcpyDeviceToHost,
+                                          d->stream));
+    } else {
+        NC_HIP_CHECK(hipMemcpy2DAsync(d->staging, width, store, store_pitch, width, d->L, hipMemcpyHostToDevice,
                                       d->stream));
-    else
-        NC_HIP_CHECK(hipMemcpy2DAsync(slot, slot_pitch, store, store_pitch, width, d->L, hipMemcpyHostToDevice,
-                                      d->stream));
-    return 0;
+        rc = nc_kv_import_fp8(d->staging, d->L, d->cache, (long long)d->pool_bytes, nullptr, d->max_blocks, num_blocks,
+                              d->B, b, at, n, d->Hkv, d->stream);
+    }
+    if (rc < 0) {
+        fprintf(stderr, "%s: %s\n", name, nc_last_error());
+        abort();
+    }
 }
 
-extern "C" int dec_save_prompt(void *handle, int b, int at, int store_at, int n) {
-    return prompt_copy((Decoder *)handle, b, at, store_at, n, true);
+extern "C" void dec_save_prompt(void *handle, int b, int at, int store_at, int n) {
+    prompt_copy((Decoder *)handle, "dec_save_prompt", b, at, store_at, n, true);
 }
 
-extern "C" int dec_load_prompt(void *handle, int b, int at, int store_at, int n) {
-    return prompt_copy((Decoder *)handle, b, at, store_at, n, false);
+extern "C" void dec_load_prompt(void *handle, int b, int at, int store_at, int n) {
+    prompt_copy((Decoder *)handle, "dec_load_prompt", b, at, store_at, n, false);
 }
 
 extern "C" void dec_set_active(void *handle, const unsigned long long *slots) {
@@ -485,6 +531,10 @@ extern "C" void dec_tokens(void *handle, int32_t *out) {
 
 extern "C" void dec_take_alt(void *handle, int b) {
     Decoder *d = (Decoder *)handle;
+    if (b < 0 || b >= d->B) {
+        fprintf(stderr, "dec_take_alt: slot %d outside [0, %d)\n", b, d->B);
+        abort();
+    }
     hipLaunchKernelGGL(k_take_alt, dim3(1), dim3(1), 0, d->stream, d->d.tok, d->alt, b);
     NC_LAUNCH_CHECK();
 }

@@ -24,6 +24,7 @@ from nanochat_amd.native import check, hip_library, pointer, stream
 PAGE = 16
 HEAD_DIM = 128
 TILE_BYTES = 4224
+ROW_BYTES = 264  # one position of one kv head as a row: K codes, V codes, K scale, V scale
 
 
 def _require(t: Tensor, name: str, dtype: torch.dtype, dim: int | None = None) -> None:
@@ -148,3 +149,25 @@ class Fp8KVCache:
         check(hip_library().nc_kv_gather_fp8(*args, pointer(ctx_len), B, self.hkv, max_ctx, pointer(k), pointer(v),
                                              pointer(ks), pointer(vs), stream()))
         return k, v, ks, vs
+
+    def export_rows(self, seq: int, at: int, n: int, out: Tensor | None = None) -> Tensor:
+        """Positions [at, at + n) of sequence seq (any at, any n) as rows uint8 [n][hkv][264]: K codes, V codes in
+        dim order, K scale and V scale (fp32 bytes). A position whose block is missing gives a zero row."""
+        if out is None:
+            out = torch.empty((n, self.hkv, ROW_BYTES), dtype=torch.uint8, device=self.pages.device)
+        elif out.shape != (n, self.hkv, ROW_BYTES) or out.dtype != torch.uint8 or not out.is_contiguous():
+            raise ValueError(f"out must be contiguous uint8 [{n}][{self.hkv}][{ROW_BYTES}]")
+        pages, table, mb, nb, ns = self._cache_args()
+        check(hip_library().nc_kv_export_fp8(pages, 0, 1, table, mb, nb, ns, seq, at, n, self.hkv, pointer(out),
+                                             stream()))
+        return out
+
+    def import_rows(self, rows: Tensor, seq: int, at: int) -> None:
+        """export_rows' inverse: rows uint8 [n][hkv][264] into positions [at, at + n) of sequence seq; only those
+        positions' bytes change."""
+        _require(rows, "rows", torch.uint8, 3)
+        if rows.shape[1:] != (self.hkv, ROW_BYTES):
+            raise ValueError(f"rows {tuple(rows.shape)} must be [n][{self.hkv}][{ROW_BYTES}]")
+        pages, table, mb, nb, ns = self._cache_args()
+        check(hip_library().nc_kv_import_fp8(pointer(rows), 1, pages, 0, table, mb, nb, ns, seq, at, rows.shape[0],
+                                             self.hkv, stream()))

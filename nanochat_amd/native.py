@@ -26,6 +26,8 @@ SIGNATURES: dict[str, tuple] = {
     "nc_kv_append_fp8": (I32, [P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P, P, P, I32, I32, I32, P, P]),
     "nc_kv_store_fp8": (I32, [P, P, I64, I32, P, P, I32, P, P, I32, I32, I32, P]),
     "nc_kv_gather_fp8": (I32, [P, P, I32, I32, P, I32, I32, I32, P, P, P, P, P]),
+    "nc_kv_export_fp8": (I32, [P, I64, I32, P, I32, I32, I32, I32, I32, I32, I32, P, P]),
+    "nc_kv_import_fp8": (I32, [P, I32, P, I64, P, I32, I32, I32, I32, I32, I32, I32, P]),
     "nc_decode_workspace_bytes": (I64, [I32, I32, I32, I32]),
     "nc_decode_attn_fp8": (I32, [P, P, P, I32, I32, P, I32, I32, I32, I32, I32, F32, P, P, I64, P]),
     "nc_decode_step_fp8": (I32, [P, I64, P, P, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P,
@@ -47,8 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "dec_prefill_rows": (I32, [P]),
     "dec_set_prompt": (None, [P, I32, ctypes.c_int32, ctypes.c_int32, F32, F32, ctypes.c_ulonglong]),
     "dec_prefill": (None, [P, I32, P]),
-    "dec_save_prompt": (I32, [P, I32, I32, I32, I32]),
-    "dec_load_prompt": (I32, [P, I32, I32, I32, I32]),
+    "dec_save_prompt": (None, [P, I32, I32, I32, I32]),
+    "dec_load_prompt": (None, [P, I32, I32, I32, I32]),
     "dec_masks": (P, [P]),
     "dec_set_active": (None, [P, P]),
     "dec_launch_body": (None, [P]),
@@ -64,17 +66,10 @@ class HipLibraryError(RuntimeError):
 
 @functools.cache
 def hip_library() -> ctypes.CDLL:
-    """The loaded library with every entry point's argtypes set; built in-tree first if missing or stale.
-    NC_LIBRARY=<path> loads another build of the same sources instead (A/B timing of build variants)."""
-    import os
-
-    override = os.environ.get("NC_LIBRARY")
-    if override:
-        lib = ctypes.CDLL(override)
-    else:
-        if not _build.is_current():
-            _build.build()
-        lib = ctypes.CDLL(str(_build.LIBRARY))
+    """The loaded library with every entry point's argtypes set; built in-tree first if missing or stale."""
+    if not _build.is_current():
+        _build.build()
+    lib = ctypes.CDLL(str(_build.LIBRARY))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = res, args

@@ -214,6 +214,48 @@ def gather(cache: PagedCache, block_table: np.ndarray | None, max_blocks: int, c
     return k, v, ks, vs
 
 
+ROW_BYTES = 2 * HEAD_DIM + 8  # a position of a kv head as a row: K codes, V codes, K scale, V scale
+
+
+def export_rows(cache: PagedCache, block_table: np.ndarray | None, max_blocks: int, seq: int, at: int,
+                n: int) -> np.ndarray:
+    """Positions [at, at + n) of sequence seq as rows uint8 [n][Hkv][264]: K codes, V codes in dim order, then the K
+    and V scales' fp32 bytes; a position whose block is missing (< 0 or past the pool) gives a zero row. The prompt
+    store's unit: the reference copies a slot's positions [at, at + n) to the store position by position
+    (model/kernels/decode.cu:1053-1075, bf16 K and V rows there)."""
+    rows = np.zeros((n, cache.hkv, ROW_BYTES), np.uint8)
+    for i in range(n):
+        blk = _block_or_missing(cache, block_table, max_blocks, seq, at + i)
+        if blk < 0:
+            continue
+        for h in range(cache.hkv):
+            kc, vc, ks, vs = cache.read(blk, h, (at + i) % PAGE)
+            rows[i, h] = np.concatenate([kc, vc, np.array([ks, vs], np.float32).view(np.uint8)])
+    return rows
+
+
+def import_rows(cache: PagedCache, rows: np.ndarray, block_table: np.ndarray | None, max_blocks: int, seq: int,
+                at: int) -> None:
+    """export_rows' inverse (the store-to-slot direction of decode.cu:1053-1075): rows [n][Hkv][264] into positions
+    [at, at + n) of sequence seq; a position whose block is missing is not written."""
+    for i in range(rows.shape[0]):
+        blk = _block_or_missing(cache, block_table, max_blocks, seq, at + i)
+        if blk < 0:
+            continue
+        for h in range(cache.hkv):
+            r = rows[i, h]
+            sc = r[2 * HEAD_DIM:].view(np.float32)
+            cache.write(blk, h, (at + i) % PAGE, r[:HEAD_DIM], sc[0], r[HEAD_DIM:2 * HEAD_DIM], sc[1])
+
+
+def _block_or_missing(cache: PagedCache, block_table, max_blocks: int, seq: int, pos: int) -> int:
+    page = pos // PAGE
+    if page >= max_blocks:
+        return -1
+    blk = int(PagedCache.block_of(seq, pos, block_table, max_blocks))
+    return blk if 0 <= blk < cache.num_blocks else -1
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # attention (fp64 over the dequantised cache)
 # ---------------------------------------------------------------------------------------------------------------

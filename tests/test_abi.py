@@ -285,3 +285,59 @@ def test_a_c_caller_compiles_links_and_runs(tmp_path):
     assert out[0] == "1"
     assert int(out[1]) == native.hip_library().nc_decode_workspace_bytes(64, 16, 4, 8192)
     assert int(out[2]) == native.hip_library().nc_choose_workspace_bytes(8, 1000)
+
+
+def test_reference_entry_dec_create_aborts_on_a_bad_configuration(tmp_path):
+    """The reference's dec_create aborts with a message (decode.cu:927-931): its caller never checks the handle. A C
+    program passes a hidden size that is not a multiple of 128; the check runs before any device call, so no GPU is
+    needed, and the process ends by SIGABRT naming the problem."""
+    import shutil
+    import signal
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    lib = Path(native.hip_library()._name)
+    src = tmp_path / "create.c"
+    src.write_text('#include "nanochat_amd.h"\n#include <stdio.h>\n'
+                   'int main(void) {\n'
+                   '    int cfg[7] = {1, 200, 1024, 1000, 48, 0, 7};\n'
+                   '    uint64_t ptrs[12] = {0};\n'
+                   '    float scal[3] = {1, 0, 15};\n'
+                   '    int window[1] = {-1};\n'
+                   '    void *h = dec_create(cfg, ptrs, scal, window, 0);\n'
+                   '    printf("returned %p\\n", h);\n'
+                   '    return 0;\n'
+                   '}\n')
+    exe = tmp_path / "create"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{HEADER.parent}", str(src), f"-L{lib.parent}",
+                    "-lnanochat_amd", f"-Wl,-rpath,{lib.parent}", "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == -signal.SIGABRT, (r.returncode, r.stdout, r.stderr)
+    assert "dec_create: " in r.stderr and "C 200" in r.stderr, r.stderr
+    assert "returned" not in r.stdout
+
+
+def test_position_rows_reject_bad_arguments():
+    lib = native.hip_library()
+    #          cache pool layers table max_b blocks seqs seq at n  hkv rows  stream
+    base = [FAKE, 0, 1, NULL, 10, 40, 4, 1, 5, 20, 2, FAKE, NULL]
+
+    def rejects(i, value, message):
+        args = list(base)
+        args[i] = value
+        assert lib.nc_kv_export_fp8(*args) < 0, (i, value)
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error()
+
+    rejects(7, 4, "sequence 4")         # past the 4 sequences
+    rejects(8, 150, "positions")        # 150 + 20 > 10 pages of 16
+    rejects(9, -1, "n -1")
+    rejects(5, 30, "contiguous")        # 4 sequences x 10 blocks need 40
+    rejects(2, 3, "pool_bytes")         # several layers need the pool stride
+    rejects(0, NULL, "null")
+    args = list(base)
+    args[9] = 0
+    assert lib.nc_kv_export_fp8(*args) == 0  # nothing to move: no launch
+    # import takes the same checks (rows first, then the cache arguments)
+    assert lib.nc_kv_import_fp8(FAKE, 1, FAKE, 0, NULL, 10, 40, 4, 9, 0, 3, 2, NULL) < 0
+    assert "sequence 9" in lib.nc_last_error().decode()

@@ -144,3 +144,66 @@ def test_gather_bit_exact(gpu, layout):
     want = G.gather(oracle_cache(cache), table(cache), cache.max_blocks, ctx.cpu().numpy(), 100)
     for got, w in zip((k, v, ks, vs), want):
         np.testing.assert_array_equal(got.cpu().numpy(), w)
+
+
+ROW_CASES = [
+    # layout, hkv, sequence, at, n: unaligned starts and lengths, whole pages, a single position, none
+    ("paged", 4, 2, 37, 50),
+    ("contiguous", 13, 1, 0, 2047 % 64),
+    ("paged", 2, 0, 16, 32),
+    ("contiguous", 3, 3, 99, 1),
+    ("paged", 1, 1, 5, 0),
+]
+
+
+@pytest.mark.parametrize("layout, hkv, s, at, n", ROW_CASES)
+def test_position_rows_bit_exact(gpu, layout, hkv, s, at, n):
+    """nc_kv_export_fp8 equals the oracle's rows; nc_kv_import_fp8 of those rows into another sequence at another
+    unaligned start changes exactly the bytes the oracle's import changes (the whole pool compared)."""
+    print(f"position rows {layout} hkv {hkv} seq {s} [{at}, {at + n})", flush=True)
+    dev = gpu
+    cache = make_cache(layout, 4, 160, hkv, dev, seed=61)
+    random_bytes(cache, 62)
+    ref = oracle_cache(cache)
+    rows = cache.export_rows(s, at, n)
+    torch.cuda.synchronize()
+    want = G.export_rows(ref, table(cache), cache.max_blocks, s, at, n)
+    np.testing.assert_array_equal(rows.cpu().numpy(), want)
+    dst_seq, dst_at = (s + 1) % 4, 160 - n - 3 if n else 7
+    cache.import_rows(rows, dst_seq, dst_at)
+    torch.cuda.synchronize()
+    G.import_rows(ref, want, table(cache), cache.max_blocks, dst_seq, dst_at)
+    assert_same_cache(cache, ref)
+
+
+def test_position_rows_of_several_layers(gpu):
+    """The decoder's form: layers pools spaced pool_bytes apart in one allocation, exported and imported in one
+    call each, against the oracle layer by layer."""
+    from nanochat_amd.native import check, hip_library, pointer, stream
+
+    dev = gpu
+    L, hkv, B, cap = 3, 2, 2, 64
+    caches = [make_cache("contiguous", B, cap, hkv, dev, seed=70 + l) for l in range(L)]
+    pool = torch.stack([c.pages for c in caches])  # [L][blocks][hkv][4224]
+    g = torch.Generator().manual_seed(73)
+    pool.copy_(torch.randint(0, 256, pool.shape, generator=g, dtype=torch.uint8))
+    refs = []
+    for l in range(L):
+        r = G.PagedCache(caches[l].num_blocks, hkv)
+        r.pages[...] = pool[l].cpu().numpy()
+        refs.append(r)
+    mb, nb = caches[0].max_blocks, caches[0].num_blocks
+    pool_bytes = pool[0].numel()
+    rows = torch.empty((L, 21, hkv, 264), dtype=torch.uint8, device=dev)
+    lib = hip_library()
+    check(lib.nc_kv_export_fp8(pointer(pool), pool_bytes, L, None, mb, nb, B, 1, 11, 21, hkv, pointer(rows),
+                               stream()))
+    torch.cuda.synchronize()
+    want = np.stack([G.export_rows(r, None, mb, 1, 11, 21) for r in refs])
+    np.testing.assert_array_equal(rows.cpu().numpy(), want)
+    check(lib.nc_kv_import_fp8(pointer(rows), L, pointer(pool), pool_bytes, None, mb, nb, B, 0, 40, 21, hkv,
+                               stream()))
+    torch.cuda.synchronize()
+    for l in range(L):
+        G.import_rows(refs[l], want[l], None, mb, 0, 40)
+        np.testing.assert_array_equal(pool[l].cpu().numpy(), refs[l].pages)

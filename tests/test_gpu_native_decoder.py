@@ -109,3 +109,46 @@ def test_native_rejected_bos_takes_the_alternative(gpu):
     for k in range(6):
         assert out[k] == [100 + 37 * k] * 4, (k, out[k])
     assert dec.alts_taken > 0
+
+
+def test_native_store_at_unaligned_positions_decodes_as_prefilled(gpu):
+    """The reference's store protocol (inference/decoder.py:202-232): each new prompt of n cached positions is saved at
+    the store position where the previous one ended (0, 5, 23, 55: page boundaries neither at the starts nor the ends
+    but the first; the fifth prompt's 20 positions from 66 do not fit the 80), and a repeated prompt is loaded from
+    there instead of prefilled. One slot, so every run of a prompt has the same schedule: the loaded runs
+    must give exactly the prefilled runs' tokens (greedy and seeded sampling), and the first runs match the CPU
+    model."""
+    print("native decoder: unaligned prompt store", flush=True)
+    model = RandomModel(TINY, gpu, seed=81)
+    rng = np.random.default_rng(82)
+    prompts = [[BOS] + rng.integers(8, TINY.vocab, n).tolist() for n in (5, 18, 32, 11, 20)]
+    reqs = [Request(input_ids=ids, max_new_tokens=6, temperature=0.0 if k % 2 == 0 else 0.9, seed=90 + k)
+            for k, ids in enumerate(prompts)]
+    dec = NativeDecoder(model, bos=BOS, max_length=48, prompt_store=80, batch=1)
+    first = dict(dec.generate(reqs))
+    assert dec.loads == 0
+    assert dec.stored == {tuple(p): at for p, at in zip(prompts[:4], (0, 5, 23, 55))}  # the fifth does not fit
+    again = dict(dec.generate(list(reversed(reqs))))
+    assert dec.loads == 4
+    for k in range(5):
+        assert again[4 - k] == first[k], (k, first[k], again[4 - k])
+    checked = sum(check_alone(model, k, r, first[k]) for k, r in enumerate(reqs))
+    assert checked >= 12, checked
+
+
+def test_torch_server_store_at_unaligned_positions(gpu):
+    """The torch-driven server's store is position-granular too (the same PromptStore offsets, rows moved by
+    nc_kv_export_fp8 / nc_kv_import_fp8): loaded runs equal prefilled runs."""
+    from nanochat_amd.serving import Server
+
+    print("torch server: unaligned prompt store", flush=True)
+    model = RandomModel(TINY, gpu, seed=83)
+    rng = np.random.default_rng(84)
+    prompts = [[BOS] + rng.integers(8, TINY.vocab, n).tolist() for n in (9, 26, 3)]
+    reqs = [Request(input_ids=ids, max_new_tokens=5) for ids in prompts]
+    server = Server(model, batch=1, max_len=48, device=gpu, bos=BOS, prompt_store=40)
+    first = dict(server.generate(reqs))
+    assert server.stored == {tuple(prompts[0]): 0, tuple(prompts[1]): 9, tuple(prompts[2]): 35}
+    again = dict(server.generate(reqs))
+    assert server.loads == 3
+    assert again == first

@@ -250,6 +250,64 @@ def test_append_then_gather_paged_equals_contiguous():
     assert np.all(a[0][2, :, 5:] == 0)
 
 
+def test_export_rows_reads_the_tile_bytes_and_matches_gather():
+    """A position's row is its K codes, V codes (dim order) and the two scales' bytes, read from the tile offsets of
+    the layout formula (planted in the raw pool, not through the oracle's views), for any start and length; rows of
+    a paged sequence equal gather's canonical rows at the same positions; a missing block gives a zero row."""
+    hkv, max_blocks = 2, 5
+    c = G.PagedCache(12, hkv)
+    rng = np.random.default_rng(11)
+    c.pages[...] = rng.integers(0, 256, c.pages.shape, dtype=np.uint8)
+    table = np.array([[7, 3, 11, 0, -1], [1, 2, 4, 5, 6]], np.int32)
+    flat = c.pages.reshape(-1)
+    pos, h = 37, 1  # sequence 0, page 2 (block 11), token 5
+    tile = (11 * hkv + h) * 4224
+    rows = G.export_rows(c, table, max_blocks, 0, 30, 20)  # positions 30..49, unaligned both ends
+    row = rows[pos - 30, h]
+    np.testing.assert_array_equal(row[:128], flat[tile + 5 * 128: tile + 6 * 128])
+    np.testing.assert_array_equal(row[128:256], [flat[tile + 2048 + (5 // 4) * 512 + d * 4 + 5 % 4] for d in range(128)])
+    np.testing.assert_array_equal(row[256:260], flat[tile + 4096 + 20: tile + 4096 + 24])
+    np.testing.assert_array_equal(row[260:264], flat[tile + 4160 + 20: tile + 4160 + 24])
+    k, v, ks, vs = G.gather(c, table, max_blocks, np.array([64, 64]), 64)
+    for i in range(20):
+        if (30 + i) // 16 == 4:  # the missing block
+            assert not rows[i].any()
+            continue
+        for hh in range(hkv):
+            np.testing.assert_array_equal(rows[i, hh, :128], k[0, hh, 30 + i])
+            np.testing.assert_array_equal(rows[i, hh, 128:256], v[0, hh, 30 + i])
+            np.testing.assert_array_equal(rows[i, hh, 256:].view(np.float32), [ks[0, hh, 30 + i], vs[0, hh, 30 + i]])
+
+
+def test_import_rows_moves_positions_and_nothing_else():
+    """Rows exported from one sequence and imported at another start of another sequence land exactly there (the
+    moved positions gather equal), every other byte of the pool is unchanged, and a missing block is not written."""
+    hkv, max_blocks = 3, 4
+    src = G.PagedCache(8, hkv)
+    rng = np.random.default_rng(12)
+    src.pages[...] = rng.integers(0, 256, src.pages.shape, dtype=np.uint8)
+    rows = G.export_rows(src, None, max_blocks, 1, 3, 29)  # sequence 1 (blocks 4..7), positions 3..31
+    dst = G.PagedCache(8, hkv)
+    dst.pages[...] = rng.integers(0, 256, dst.pages.shape, dtype=np.uint8)
+    before = dst.pages.copy()
+    table = np.array([[2, 0, 6, -1], [1, 3, 4, 5]], np.int32)
+    G.import_rows(dst, rows, table, max_blocks, 0, 21)  # positions 21..49 of sequence 0: blocks 0, 6, then missing
+    a = G.gather(src, None, max_blocks, np.array([0, 32]), 32)
+    b = G.gather(dst, table, max_blocks, np.array([48, 0]), 48)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x[1, :, 3:30], y[0, :, 21:48])
+    changed = np.flatnonzero((dst.pages != before).any(axis=(1, 2)))
+    assert set(changed) <= {0, 6}, changed  # only the blocks of pages 1 and 2 of sequence 0
+    untouched = G.export_rows(dst, table, max_blocks, 0, 0, 21)  # positions before `at` keep their bytes
+    np.testing.assert_array_equal(untouched, G.export_rows(_with(before, hkv), table, max_blocks, 0, 0, 21))
+
+
+def _with(pages, hkv):
+    c = G.PagedCache(pages.shape[0], hkv)
+    c.pages[...] = pages
+    return c
+
+
 # ----------------------------------------------------------------------------------------------- attention
 
 def make_cache(ctx, hkv, seed, table=False):
