@@ -123,6 +123,20 @@ int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos
                        int hq, int hkv, int max_ctx, float sm_scale, void *out, void *workspace,
                        long long workspace_bytes, void *stream);
 
+/* nc_decode_step_fp8 without the workspace: the partial results between its two kernels live in a static device
+ * array of 64 MiB (67108864 bytes) that the library holds on every device it runs on until the process ends, so the
+ * call allocates nothing. A shape whose workspace (nc_decode_workspace_bytes) exceeds 64 MiB is rejected with an
+ * error (config 3's B 64, 16 / 4 heads need 21.5 MB; B 128 of 13 MHA heads 11.9 MB). Every call on a device shares
+ * its array: calls in one stream are ordered, calls that may overlap on one device (two streams) race. Outputs, cache
+ * bytes and pos_out are bit-identical to nc_decode_step_fp8's.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). */
+int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                               const float *q_gain, const float *k_gain, const float *cos, const float *sin,
+                               int rope_len, uint8_t *cache, const int32_t *block_table, int max_blocks,
+                               int num_blocks, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
+                               void *out, void *stream);
+
 /* Chunked-prefill attention: row r (bf16 q [n][Hq][128], normed and rotated, e.g. nc_kv_append_fp8's q_out) at
  * position pos[r] of sequence seq[r] attends keys [max(pos - window, 0), pos] of that sequence in the cache
  * (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores times sm_scale, fp32 softmax, bf16 out

@@ -41,6 +41,8 @@
  *
  * Roofline: HBM. Per (token, kv head) the kernel reads 128 B of K, 128 B of V and two fp32 scales: 264 B.
  */
+#include <mutex>
+
 #include "layout.h"
 #include "qk_row.h"
 
@@ -807,4 +809,54 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const i
     return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
                        max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, workspace, workspace_bytes,
                        stream);
+}
+
+/* ------------------------------------------------------------------------------------------------------------
+ * The fused step without a workspace argument, for callers that cannot allocate (code under graph capture, tight
+ * serving loops): the partial results between k_decode and k_merge live in `scratch`, a static device array of
+ * NC_DECODE_SCRATCH_BYTES that every device running this library holds until the process ends. Its device address
+ * is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernels like the
+ * workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. No cell of it needs
+ * to start at zero: every segment's descriptor is written before k_merge reads it, and only the slots of pieces
+ * that exist are folded. Calls share their device's array, so two calls that may overlap on one device (two streams)
+ * race; calls in one stream do not. */
+#define NC_DECODE_SCRATCH_BYTES (64ll << 20)
+#define NC_MAX_DEVICES 64
+
+static __device__ __align__(256) unsigned char scratch[NC_DECODE_SCRATCH_BYTES];
+
+static void *scratch_address() {
+    static void *address[NC_MAX_DEVICES];
+    static std::mutex lock;
+    int dev = 0;
+    NC_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NC_MAX_DEVICES) {
+        fprintf(stderr, "decode_attn.hip: device %d past the %d the scratch table holds\n", dev, NC_MAX_DEVICES);
+        abort();
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    if (!address[dev]) {
+        void *p = nullptr;
+        NC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        address[dev] = p;
+    }
+    return address[dev];
+}
+
+extern "C" int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride, const int32_t *pos,
+                                          int32_t *pos_out, const float *q_gain, const float *k_gain,
+                                          const float *cos, const float *sin, int rope_len, uint8_t *cache,
+                                          const int32_t *block_table, int max_blocks, int num_blocks, int window,
+                                          int B, int hq, int hkv, int max_ctx, float sm_scale, void *out,
+                                          void *stream) {
+    const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
+    NC_REQUIRE(need <= NC_DECODE_SCRATCH_BYTES,
+               "%d sequences of %d / %d heads need %lld bytes of partial results, the static scratch holds %lld", B,
+               hq, hkv, need, NC_DECODE_SCRATCH_BYTES);
+    if (B <= 0 || need == 0) /* nothing to launch: the shared checks report a bad B or head count */
+        return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
+                           max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, nullptr, 0, stream);
+    return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, scratch_address(),
+                       NC_DECODE_SCRATCH_BYTES, stream);
 }
