@@ -13,7 +13,12 @@ HBM); roofline = the step's attention call (k_decode, then k_merge): the timed s
 nc_decode_step_fp8 call each), or with --unfused the attention call alone at the last step's context, timed over
 graph replays of 10 back-to-back calls, with HIP events on their stream; attention_only = that attention call
 alone in either mode (the decode kernel and the split-K merge without the append, the kernels the metric counts);
-cpu_baseline = the numpy oracle over a bounded sample of the same sequences on this host's cores.
+cpu_baseline = the numpy oracle over a bounded sample of the same sequences on this host's cores; the config 2, 4
+and 5 objects carry their own cpu_baseline (config 5's: the oracle's CPU model on one sequence, extrapolated to the
+whole run and labelled so), each with the host's CPU model, thread count and torch version.
+
+Profiling helpers (no measurement): --pmc-summary turns rocprofv3 --pmc output into per-kernel bytes and MFMA
+figures, --stats-summary prints a rocprofv3 --stats kernel table; profiles/ holds their output.
 """
 
 from __future__ import annotations
@@ -53,6 +58,14 @@ def parse():
                          "fused nc_decode_step_fp8")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the measurement, copy a 1 GiB buffer 3 times (the byte-counter calibration kernel)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="no measurement: summarise rocprofv3 --pmc output directories (counter_collection.csv) "
+                         "per kernel of --kernels, as JSON")
+    ap.add_argument("--kernels", default="k_decode<true>,k_merge",
+                    help="--pmc-summary: the kernels (short names) whose last --last dispatches are averaged")
+    ap.add_argument("--last", type=int, default=20, help="--pmc-summary: dispatches per kernel averaged")
+    ap.add_argument("--stats-summary", metavar="DIR",
+                    help="no measurement: print the kernel table of a rocprofv3 --kernel-trace --stats directory")
     return ap.parse_args()
 
 
@@ -70,25 +83,126 @@ def replay_ms(graph, n: int, stream) -> float:
     return start.elapsed_time(end) / n
 
 
+CALL_KERNELS = {"nc_decode_step_fp8": ("k_decode<true>", "k_merge"),
+                "nc_decode_attn_fp8": ("k_decode<false>", "k_merge")}
+
+
 def traffic_bytes(call: str):
-    """HBM bytes per `call` (nc_decode_step_fp8 or nc_decode_attn_fp8) from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-    passes, each scaled by what the counter reads for a plain 1 GiB copy (TRAFFIC_FILE, written from the profiling
-    runs); None if absent."""
+    """Memory bytes per `call` (nc_decode_step_fp8 or nc_decode_attn_fp8): its kernels' read bytes (TCC_EA0_RDREQ
+    by request size) plus write bytes (WRITE_SIZE's expression), per dispatch, from the rocprofv3 --pmc passes
+    summarised in TRAFFIC_FILE (bench.py --pmc-summary); None if absent."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f)[call]["bytes_per_call"]
+            summary = json.load(f)[call]["summary"]
+        return int(sum(summary[k]["read_bytes"] + summary[k]["write_bytes"] for k in CALL_KERNELS[call]))
     except (OSError, KeyError, ValueError):
         return None
 
 
+def traffic_algorithmic() -> int | None:
+    """The algorithmic bytes per call of the profiled run TRAFFIC_FILE summarises (its traffic is compared with
+    those, not with this run's)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return int(json.load(f)["algorithmic_bytes_per_call"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+COPY_PROBE_BYTES = 1 << 30  # read and written by each dispatch of the copy probe
+
+
 def copy_probe(dev) -> None:
+    """Three dispatches of an elementwise kernel that reads 1 GiB and writes 1 GiB (torch.neg, kernel name
+    containing "neg"): the byte counters' calibration."""
     import torch
 
-    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
-        dst.copy_(src)
+        torch.neg(src, out=dst)
     torch.cuda.synchronize()
+
+
+def stats_summary(d: str, rows: int = 20) -> str:
+    """The rocprofv3 --stats kernel table (kernel_stats.csv under d): calls, average / min / max duration, share."""
+    import csv
+    import glob
+
+    f = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)[0]
+    lines = [f"{'kernel':60s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'pct':>6s}"]
+    with open(f) as fh:
+        for r in list(csv.DictReader(fh))[:rows]:
+            n = r["Name"] if len(r["Name"]) < 60 else r["Name"][:57] + "..."
+            lines.append(f"{n:60s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.3f} "
+                         f"{float(r['MinNs']) / 1e3:9.3f} {float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}")
+    return "\n".join(lines)
+
+
+SIMDS = 1024  # MI355X: 256 CUs x 4 SIMDs (SQ_VALU_MFMA_BUSY_CYCLES is summed over SIMDs)
+XCDS = 8
+
+
+def pmc_summary(dirs: list[str], kernels: list[str], last: int) -> dict:
+    """Per-dispatch averages of every counter in rocprofv3 --pmc output directories for the named kernels (their
+    last `last` dispatches) and for the copy probe, and the figures derived from them:
+      read_bytes  = 32 RDREQ_32B + 64 RDREQ_64B + 128 RDREQ_128B   (TCC_EA0_* sums: requests from L2 to memory)
+      fetch_bytes = FETCH_SIZE's own expression x 1024 (BUBBLE, RDREQ, RDREQ_32B)
+      write_bytes = 32 (WRREQ - WRREQ_64B) + 64 WRREQ_64B            (WRITE_SIZE's expression x 1024)
+      mfma_busy   = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs)  (GRBM_GUI_ACTIVE as collected
+                    is the sum of the 8 XCDs' busy cycles; the busy cycles are summed over every SIMD)
+    and for the copy probe each byte figure over the bytes it moves (1 GiB each way: the counters' calibration)."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    per = defaultdict(list)
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    name = r["Kernel_Name"].split("(")[0]
+                    name = name[5:] if name.startswith("void ") else name
+                    if name not in kernels:
+                        name = "copy_probe" if "neg" in r["Kernel_Name"] else None
+                    if name:
+                        per[(name, r["Counter_Name"])].append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    out = {}
+    for name in list(kernels) + ["copy_probe"]:
+        c = {}
+        for (k, counter), v in per.items():
+            if k == name:
+                v.sort()
+                vals = [x for _, x in v[-(3 if name == "copy_probe" else last):]]
+                c[counter] = sum(vals) / len(vals)
+        if not c:
+            continue
+        d = {"dispatches_averaged": 3 if name == "copy_probe" else last, "counters": c}
+        g = lambda n: c.get(n + "_sum", c.get(n))
+        if all(g(n) is not None for n in ("TCC_EA0_RDREQ_32B", "TCC_EA0_RDREQ_64B", "TCC_EA0_RDREQ_128B")):
+            d["read_bytes"] = 32 * g("TCC_EA0_RDREQ_32B") + 64 * g("TCC_EA0_RDREQ_64B") + 128 * g("TCC_EA0_RDREQ_128B")
+        if all(g(n) is not None for n in ("TCC_BUBBLE", "TCC_EA0_RDREQ", "TCC_EA0_RDREQ_32B")):
+            d["fetch_bytes"] = (128 * g("TCC_BUBBLE") + 64 * (g("TCC_EA0_RDREQ") - g("TCC_BUBBLE") -
+                                                             g("TCC_EA0_RDREQ_32B")) + 32 * g("TCC_EA0_RDREQ_32B"))
+        if all(g(n) is not None for n in ("TCC_EA0_WRREQ", "TCC_EA0_WRREQ_64B")):
+            d["write_bytes"] = 32 * (g("TCC_EA0_WRREQ") - g("TCC_EA0_WRREQ_64B")) + 64 * g("TCC_EA0_WRREQ_64B")
+        if g("SQ_VALU_MFMA_BUSY_CYCLES") is not None and g("GRBM_GUI_ACTIVE"):
+            d["mfma_busy"] = g("SQ_VALU_MFMA_BUSY_CYCLES") / (g("GRBM_GUI_ACTIVE") / XCDS * SIMDS)
+            d["gpu_cycles"] = g("GRBM_GUI_ACTIVE") / XCDS
+        if g("SQ_VALU_MFMA_COEXEC_CYCLES") is not None and g("SQ_VALU_MFMA_BUSY_CYCLES"):
+            d["coexec_of_mfma_busy"] = g("SQ_VALU_MFMA_COEXEC_CYCLES") / g("SQ_VALU_MFMA_BUSY_CYCLES")
+        if g("SQ_INSTS_VALU") is not None and g("SQ_INSTS_MFMA"):
+            d["valu_per_mfma"] = g("SQ_INSTS_VALU") / g("SQ_INSTS_MFMA")
+        mops = [g(n) for n in ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                               "SQ_INSTS_VALU_MFMA_MOPS_F8") if g(n) is not None]
+        if mops:
+            d["mfma_flops"] = 512 * sum(mops)
+        if name == "copy_probe":
+            for key in ("read_bytes", "fetch_bytes", "write_bytes"):
+                if key in d:
+                    d[key.replace("_bytes", "_over_moved")] = d[key] / COPY_PROBE_BYTES
+        out[name] = d
+    return out
 
 
 def time_calls(fn, calls: int, replays: int, stream) -> float:
@@ -107,8 +221,9 @@ def time_calls(fn, calls: int, replays: int, stream) -> float:
     return replay_ms(graph, replays, stream) / calls
 
 
-def extra_decode_cfg2(dev, stream) -> dict:
-    """Config 2 (B 32, 10/10 heads, ctx 4096 contiguous): one decode-attention call after the step's append."""
+def extra_decode_cfg2(dev, stream, cpu_s: float | None = None) -> dict:
+    """Config 2 (B 32, 10/10 heads, ctx 4096 contiguous): one decode-attention call after the step's append; with
+    cpu_s, the oracle's CPU leg on a bounded sample of the same sequences."""
     from nanochat_amd.attention import decode_attention, decode_workspace
     from nanochat_amd.workloads import CONFIG2, build_decode_case, decode_bytes
 
@@ -123,13 +238,17 @@ def extra_decode_cfg2(dev, stream) -> dict:
                     ATTN_REPS, 20, stream)
     nbytes = decode_bytes(case.ctx + 1, cfg.hkv, cfg.window)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "bytes": int(nbytes), "GB_s": round(gbs, 2),
-            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    res = {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "bytes": int(nbytes), "GB_s": round(gbs, 2),
+           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    if cpu_s:
+        res["cpu_baseline"] = cpu_decode(case, case.ctx + 1, q, cpu_s, gbs)
+    return res
 
 
-def extra_prefill_cfg4(dev, stream) -> dict:
+def extra_prefill_cfg4(dev, stream, cpu_s: float | None = None) -> dict:
     """Config 4 (B 8, 16/4 heads, 3584 cached + 512-token chunk): the chunk's append, then prefill attention; the
-    attention call timed alone (MFMA-bound: algorithmic flops over time against the dense bf16 peak)."""
+    attention call timed alone (MFMA-bound: algorithmic flops over time against the dense bf16 peak); with cpu_s,
+    the oracle's CPU leg on a bounded sample of the same rows."""
     from nanochat_amd.attention import prefill_attention
     from nanochat_amd.workloads import CONFIG4, build_prefill_case, prefill_flops
 
@@ -142,15 +261,19 @@ def extra_prefill_cfg4(dev, stream) -> dict:
                                                      case.sin, cfg.hq), ATTN_REPS, 10, stream)
     flops = prefill_flops(case.pos.cpu().numpy(), cfg.hq, cfg.window)
     tfs = flops / (ms * 1e-3) / 1e12
-    return {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "append_us": round(append_ms * 1e3, 3),
-            "flops": flops, "TFLOP_s": round(tfs, 1), "bound": "mfma", "peak_TFLOP_s": MFMA_PEAK_TFS,
-            "frac_of_mfma_peak": round(tfs / MFMA_PEAK_TFS, 4)}
+    res = {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "append_us": round(append_ms * 1e3, 3),
+           "flops": flops, "TFLOP_s": round(tfs, 1), "bound": "mfma", "peak_TFLOP_s": MFMA_PEAK_TFS,
+           "frac_of_mfma_peak": round(tfs / MFMA_PEAK_TFS, 4)}
+    if cpu_s:
+        res["cpu_baseline"] = cpu_prefill(case, q, cpu_s, tfs)
+    return res
 
 
-def extra_e2e_cfg5(dev, steps: int | None = None) -> dict:
+def extra_e2e_cfg5(dev, steps: int | None = None, cpu_s: float | None = None) -> dict:
     """Config 5: random-init 26-layer d1664 model, 128 random 2048-token prompts prefilled into the fp8 cache, then
     512 greedy decode steps replayed from one captured graph; tokens/s and the decode steps' algorithmic HBM bytes
-    (bf16 weights once + 264 B per cached (token, head, layer))."""
+    (bf16 weights once + 264 B per cached (token, head, layer)); with cpu_s, the oracle's CPU model on one sequence,
+    extrapolated to the whole run."""
     import torch
 
     from nanochat_amd.decoder import CONFIG5, generate
@@ -160,21 +283,26 @@ def extra_e2e_cfg5(dev, steps: int | None = None) -> dict:
         from dataclasses import replace
 
         cfg = replace(cfg, steps=steps, name=cfg.name.replace(f"steps{cfg.steps}", f"steps{steps}"))
-    toks, info, keep = generate(cfg, dev)
-    del keep
+    toks, info, (model, dec, prompts) = generate(cfg, dev)
+    del dec
     torch.cuda.empty_cache()
     m, B, steps = cfg.model, cfg.batch, cfg.steps
     kv = sum((cfg.prompt - 1 + i + 1) * B * m.kv_heads * 264 * m.layers for i in range(steps))
     step_bytes = (kv + steps * info["weight_bytes"]) / steps
     dec_s, pre_s = info["decode_ms"] * 1e-3, info["prefill_ms"] * 1e-3
     gbs = step_bytes / (dec_s / steps) / 1e9
-    return {"workload": cfg.name, "prefill_s": round(pre_s, 4), "decode_s": round(dec_s, 4),
-            "decode_ms_per_step": round(info["decode_ms_per_step"], 4),
-            "decode_tokens_per_s": round(B * steps / dec_s, 1),
-            "e2e_tokens_per_s": round(B * steps / (pre_s + dec_s), 1),
-            "decode_step_bytes": int(step_bytes), "decode_GB_s": round(gbs, 1),
-            "decode_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "check": {"first_tokens": toks[0, :4].tolist(), "distinct_tokens": int(toks.unique().numel())}}
+    import hashlib
+
+    res = {"workload": cfg.name, "prefill_s": round(pre_s, 4), "decode_s": round(dec_s, 4),
+           "decode_ms_per_step": round(info["decode_ms_per_step"], 4),
+           "decode_tokens_per_s": round(B * steps / dec_s, 1),
+           "e2e_tokens_per_s": round(B * steps / (pre_s + dec_s), 1),
+           "decode_step_bytes": int(step_bytes), "decode_GB_s": round(gbs, 1),
+           "decode_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "tokens_sha256": hashlib.sha256(toks.cpu().numpy().astype("<i4").tobytes()).hexdigest()[:16]}
+    if cpu_s:
+        res["cpu_baseline"] = cpu_e2e(model, prompts, cfg, 2 * cpu_s, res)
+    return res
 
 
 def torch_empty_like(t):
@@ -183,7 +311,39 @@ def torch_empty_like(t):
     return torch.empty_like(t)
 
 
-def cpu_baseline(case, final_ctx: np.ndarray, q, budget_s: float) -> dict:
+def host_info() -> dict:
+    """The host the CPU legs run on: CPU model, the threads used, torch and numpy versions."""
+    import torch
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "threads": len(os.sched_getaffinity(0)), "torch": torch.__version__,
+            "numpy": np.__version__}
+
+
+def _q_bits(q) -> np.ndarray:
+    import torch
+
+    return q.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _host_cache(cache):
+    from oracle import golden as G
+
+    host = G.PagedCache(cache.num_blocks, cache.hkv)
+    host.pages[...] = cache.pages.cpu().numpy()
+    table = cache.block_table.cpu().numpy() if cache.block_table is not None else None
+    return host, table
+
+
+def cpu_decode(case, final_ctx: np.ndarray, q, budget_s: float, gpu_gbs: float) -> dict:
     """The oracle's decode attention (numpy, fp64 over the dequantised cache) on whole sequences of the same cache,
     in order, until budget_s of work; GB/s over the same algorithmic bytes as the GPU figure."""
     import math
@@ -195,10 +355,8 @@ def cpu_baseline(case, final_ctx: np.ndarray, q, budget_s: float) -> dict:
 
     cores = len(os.sched_getaffinity(0))
     cache = case.cache
-    host = G.PagedCache(cache.num_blocks, cache.hkv)
-    host.pages[...] = cache.pages.cpu().numpy()
-    table = cache.block_table.cpu().numpy() if cache.block_table is not None else None
-    qb = q.contiguous().cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    host, table = _host_cache(cache)
+    qb = _q_bits(q)
     cfg = case.cfg
     done, t_total = 0, 0.0
     with threadpool_limits(limits=cores):
@@ -210,14 +368,93 @@ def cpu_baseline(case, final_ctx: np.ndarray, q, budget_s: float) -> dict:
             t_total += time.perf_counter() - t0
             done += 1
     nbytes = decode_bytes(final_ctx[:done], cfg.hkv, cfg.window)
-    return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    value = nbytes / t_total / 1e9
+    return {"value": round(value, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"oracle decode attention (numpy fp64 over dequantised fp8) of the first {done} of "
                       f"{cfg.batch} sequences ({int(final_ctx[:done].sum())} keys x {cfg.hkv} kv heads), "
-                      f"{t_total:.1f} s"}
+                      f"{t_total:.1f} s",
+            "speedup_gpu_over_cpu": round(gpu_gbs / value, 1), "host": host_info()}
+
+
+def cpu_prefill(case, q, budget_s: float, gpu_tfs: float) -> dict:
+    """The oracle's prefill attention (numpy fp64 over the dequantised cache) on the rows of whole sequences of the
+    same chunk, in order, until budget_s of work; TFLOP/s over the same algorithmic flops as the GPU figure."""
+    import math
+
+    from threadpoolctl import threadpool_limits
+
+    from nanochat_amd.workloads import prefill_flops
+    from oracle import golden as G
+
+    cores = len(os.sched_getaffinity(0))
+    cfg = case.cfg
+    host, table = _host_cache(case.cache)
+    qb = _q_bits(q)
+    pos, seq = case.pos.cpu().numpy(), case.seq.cpu().numpy()
+    done, t_total, flops = 0, 0.0, 0
+    with threadpool_limits(limits=cores):
+        while done < cfg.batch and t_total < budget_s:
+            rows = np.nonzero(seq == done)[0]
+            t0 = time.perf_counter()
+            G.rows_attention(qb[rows], pos[rows], seq[rows], host, table, case.cache.max_blocks, cfg.batch,
+                             cfg.window, cfg.hq, cfg.hkv, 1 / math.sqrt(128))
+            t_total += time.perf_counter() - t0
+            flops += prefill_flops(pos[rows], cfg.hq, cfg.window)
+            done += 1
+    value = flops / t_total / 1e12
+    return {"value": round(value, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"oracle prefill attention (numpy fp64 over dequantised fp8) of the chunk rows of the first "
+                      f"{done} of {cfg.batch} sequences ({flops:.3e} flop), {t_total:.1f} s",
+            "speedup_gpu_over_cpu": round(gpu_tfs / value, 1), "host": host_info()}
+
+
+def cpu_e2e(model, prompts, cfg, budget_s: float, gpu: dict) -> dict:
+    """The oracle's CPU model (oracle/model.py: torch-CPU bf16 GEMMs, numpy append and fp64 attention) on one
+    sequence of the same model and prompts: its prompt prefilled in 256-row chunks until done or 2/3 of budget_s,
+    then 8 greedy decode steps at batch 1. The whole workload's time is extrapolated from it (labelled): every
+    sequence one after another, prefill scaled by rows, 512 steps at the measured step time."""
+    import torch
+
+    from oracle.model import CpuModel
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n_prompt, steps = cfg.prompt - 1, 8
+    cpu = CpuModel(model, 1, cfg.prompt + steps)
+    ids = prompts[0].cpu().numpy().astype(np.int64)
+    done, t0 = 0, time.perf_counter()
+    while done < n_prompt and time.perf_counter() - t0 < budget_s * 2 / 3:
+        n = min(256, n_prompt - done)
+        cpu.prefill_rows(ids[done:done + n], np.arange(done, done + n), np.zeros(n, np.int64))
+        done += n
+    prefill_s = time.perf_counter() - t0
+    tok = ids[n_prompt:n_prompt + 1] if done == n_prompt else ids[done:done + 1]
+    t1 = time.perf_counter()
+    for i in range(steps):
+        tok = cpu.step(tok, done + i).argmax(1)
+    step_s = (time.perf_counter() - t1) / steps
+    per_seq = prefill_s * n_prompt / done + cfg.steps * step_s
+    total_s = cfg.batch * per_seq
+    value = cfg.batch * cfg.steps / total_s
+    return {"value": round(value, 3), "unit": "tokens/s", "cores": cores, "kind": "port", "extrapolated": True,
+            "sample": f"oracle CPU model, sequence 0 only: {done} of its {n_prompt} prompt positions prefilled in "
+                      f"{prefill_s:.1f} s, then {steps} greedy steps at batch 1 ({step_s:.2f} s each); the full run "
+                      f"extrapolated as {cfg.batch} sequences one after another, prefill scaled to {n_prompt} rows "
+                      f"and {cfg.steps} steps each: {total_s:.0f} s",
+            "decode_tokens_per_s_batch1": round(1 / step_s, 3),
+            "prefill_tokens_per_s": round(done / prefill_s, 2),
+            "speedup_gpu_over_cpu": round(gpu["e2e_tokens_per_s"] / value, 1), "host": host_info()}
 
 
 def main():
     args = parse()
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary))
+        return
+    if args.pmc_summary:
+        print(json.dumps({"dirs": args.pmc_summary, "summary": pmc_summary(args.pmc_summary, args.kernels.split(","),
+                                                                            args.last)}, indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the decode path shards by "
               "(sequence, kv head) with no exchange, see DESIGN.md", file=sys.stderr)
@@ -230,8 +467,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.only:
         s = torch.cuda.Stream(dev)
-        run = {"decode2": lambda: extra_decode_cfg2(dev, s), "prefill4": lambda: extra_prefill_cfg4(dev, s),
-               "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps)}[args.only]
+        cpu_s = None if args.no_cpu else args.cpu_seconds
+        run = {"decode2": lambda: extra_decode_cfg2(dev, s, cpu_s), "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
+               "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s)}[args.only]
         print(json.dumps(run()), flush=True)
         return
     cfg = CONFIG3
@@ -348,16 +586,18 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes("nc_decode_attn_fp8" if args.unfused else "nc_decode_step_fp8"),
+                     "traffic_run_algorithmic_bytes": traffic_algorithmic(),
                      "kernel": call_kernel, "bytes_per_launch": int(call_bytes)},
     }
+    cpu_s = None if args.no_cpu else args.cpu_seconds
     if not args.no_extra:
-        result["decode_cfg2"] = extra_decode_cfg2(dev, stream)
-        result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream)
-        result["e2e_cfg5"] = extra_e2e_cfg5(dev, args.e2e_steps)
+        result["decode_cfg2"] = extra_decode_cfg2(dev, stream, cpu_s)
+        result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream, cpu_s)
+        result["e2e_cfg5"] = extra_e2e_cfg5(dev, args.e2e_steps, cpu_s)
     if args.copy_probe:
         copy_probe(dev)
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(case, final_ctx, q, args.cpu_seconds)
+    if cpu_s:
+        result["cpu_baseline"] = cpu_decode(case, final_ctx, q, cpu_s, value)
     print(json.dumps(result), flush=True)
 
 

@@ -6,7 +6,11 @@ fallback: it fails loudly when its HIP library is missing.
 
 Modules:
   golden   numpy restatement: rotary tables, QK-norm + RoPE row math, bf16/fp8 rounding, per-(token, kv head)
-           fp8 quantisation, the paged cache layout, append, gather, decode and chunked-prefill attention (fp64).
+           fp8 quantisation, the paged cache layout, append, gather, position rows, decode and chunked-prefill
+           attention (fp64).
+  sampling the token choice: Philox4x32-10, Gumbel-max, nucleus, masks and the commit.
+  model    the decoder on the CPU (torch bf16 GEMMs over golden's append and attention): the end-to-end checker
+           and the config 5 CPU baseline.
 
 Parity pins (tests/test_oracle.py): every function is checked against a closed form, an exhaustive table, torch's
 own float8_e4m3fn / bfloat16 casts (library routines), or brute force on tiny inputs. The reference ships no

@@ -1,5 +1,6 @@
 """GPU end-to-end decoder (prefill + greedy decode over the fp8 cache) against a CPU restatement of the same model:
-torch bf16 GEMMs on the CPU and the oracle's append and fp64 attention over bit-identical cache bytes. Logits
+oracle/model.py's CpuModel, torch bf16 GEMMs on the CPU and the oracle's append and fp64 attention over
+bit-identical cache bytes. Logits
 within tolerance at every step (the two sides feed the same tokens), the greedy choice equal wherever the CPU
 logits' top-two margin exceeds the tolerance, and the captured graph's replays equal to eager steps."""
 
@@ -8,77 +9,13 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from helpers import bits
-from nanochat_amd.decoder import EPS, Fp8Decoder, ModelConfig, RandomModel, argmax_rows
-from oracle import golden as G
+from nanochat_amd.decoder import Fp8Decoder, ModelConfig, RandomModel, argmax_rows
+from oracle.model import CpuModel
 
 pytestmark = pytest.mark.gpu
 
 TINY = ModelConfig(layers=2, d_model=256, heads=2, vocab=1000)
 LOGIT_ATOL = 2e-2
-
-
-def cpu_norm(x):
-    return F.rms_norm(x.float(), (x.shape[-1],), eps=EPS).to(torch.bfloat16)
-
-
-class CpuModel:
-    """The decoder's math on the CPU: bf16 tensors and torch bf16 GEMMs; the oracle's append, rows_attention and
-    decode_attention on a host copy of the cache layout."""
-
-    def __init__(self, model, batch: int, max_len: int):
-        cfg = model.cfg
-        self.cfg, self.batch = cfg, batch
-        self.w = [{k: v.cpu() for k, v in lw.items()} for lw in model.layers]
-        self.wte, self.lm_head = model.wte.cpu(), model.lm_head.cpu()
-        self.lr, self.l0 = model.resid_lambdas.cpu(), model.x0_lambdas.cpu()
-        self.max_blocks = -(-max_len // G.PAGE)
-        self.caches = [G.PagedCache(batch * self.max_blocks, cfg.kv_heads) for _ in range(cfg.layers)]
-        self.cos, self.sin = G.rotary_tables(max_len, cfg.theta)
-
-    def _mix(self, l, x, x0):
-        """inference/modeling_nanochat.py:170-171: bf16(resid h + x0 x0) in fp32."""
-        return (self.lr[l] * x.float() + self.l0[l] * x0.float()).to(torch.bfloat16)
-
-    def _layer(self, l, x, pos, seq, tok, attend):
-        lw, cfg = self.w[l], self.cfg
-        n = cpu_norm(x)
-        qkv = n @ lw["wqkv"].t()
-        if "ve" in lw:  # inference/modeling_nanochat.py:85-88
-            H = cfg.kv_heads
-            gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))
-            v = qkv[:, (cfg.heads + H) * 128:].reshape(-1, H, 128)
-            ve = lw["ve"][torch.from_numpy(np.asarray(tok, np.int64))].reshape(-1, H, 128)
-            qkv[:, (cfg.heads + H) * 128:] = (v.float() + gate[..., None] * ve.float()).to(torch.bfloat16).flatten(1)
-        q = G.append(self.caches[l], bits(qkv), pos, seq, lw["q_gain"].numpy(), lw["k_gain"].numpy(), self.cos,
-                     self.sin, cfg.heads, cfg.kv_heads, None, self.max_blocks)
-        o = torch.from_numpy(attend(q, self.caches[l]).astype(np.float32)).to(torch.bfloat16)
-        x = x + o.reshape(o.shape[0], -1) @ lw["wo"].t()
-        u = (cpu_norm(x) @ lw["wup"].t()).float().relu().square().to(torch.bfloat16)
-        return x + u @ lw["wdown"].t()
-
-    def prefill(self, prompts):
-        B, T = prompts.shape
-        pos = np.tile(np.arange(T - 1), B)
-        seq = np.repeat(np.arange(B), T - 1)
-        tok = prompts[:, :-1].reshape(-1)
-        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
-        scale = 128 ** -0.5
-        for l in range(self.cfg.layers):
-            w = self.cfg.window(l)
-            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.rows_attention(
-                q, pos, seq, c, None, self.max_blocks, B, w, self.cfg.heads, self.cfg.kv_heads, scale))
-
-    def step(self, tok, position):
-        B = self.batch
-        pos, seq = np.full(B, position), np.arange(B)
-        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
-        scale = 128 ** -0.5
-        for l in range(self.cfg.layers):
-            w = self.cfg.window(l)
-            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.decode_attention(
-                q, c, None, self.max_blocks, pos + 1, w, self.cfg.heads, self.cfg.kv_heads, scale))
-        return (cpu_norm(x).float() @ self.lm_head.float().t()).numpy()
 
 
 def test_argmax_lowest_index_on_ties(gpu):

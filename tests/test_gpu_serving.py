@@ -10,7 +10,8 @@ import pytest
 from nanochat_amd.decoder import RandomModel
 from nanochat_amd.serving import Request, Server
 from oracle import sampling as S
-from test_gpu_decoder import LOGIT_ATOL, TINY, CpuModel
+from oracle.model import CpuModel
+from test_gpu_decoder import LOGIT_ATOL, TINY
 
 pytestmark = pytest.mark.gpu
 
@@ -96,13 +97,13 @@ def test_prompt_store_loads_instead_of_prefilling(gpu):
     prefilled each time."""
     model = RandomModel(TINY, gpu, seed=31)
     rng = np.random.default_rng(32)
-    a = [BOS] + rng.integers(8, TINY.vocab, 37).tolist()   # 38 tokens: 3 pages of prompt positions
+    a = [BOS] + rng.integers(8, TINY.vocab, 37).tolist()   # 38 tokens: 37 cached prompt positions
     b = [BOS] + rng.integers(8, TINY.vocab, 20).tolist()
     big = [BOS] + rng.integers(8, TINY.vocab, 40).tolist()
     reqs = [Request(input_ids=ids, max_new_tokens=5) for ids in (a, b, a, big, a, big)]
     server = Server(model, batch=1, max_len=48, device=gpu, bos=BOS, prompt_store=5 * 16)
     out = dict(server.generate(reqs))
-    assert server.loads == 2          # a twice; b stored too (2 pages), big (3 pages) no longer fits
+    assert server.loads == 2          # a twice; b stored too (positions 37..56), big (40) no longer fits in 80
     assert set(server.stored) == {tuple(a), tuple(b)}
     assert out[0] == out[2] == out[4]
     assert out[3] == out[5]
