@@ -16,6 +16,11 @@ pytestmark = pytest.mark.gpu
 
 TINY = ModelConfig(layers=2, d_model=256, heads=2, vocab=1000)
 LOGIT_ATOL = 2e-2
+# 26 layers of bf16 residual roundings move the logits (std 0.82) more than two layers do: at this shape the CPU model
+# itself differs from the same model with fp32 activations (only the cache rows rounded to bf16) by max 0.065 and
+# mean 0.011, so the GPU is held to about twice that
+CFG5_LOGIT_ATOL = 1.5e-1
+CFG5_LOGIT_MEAN = 2.5e-2
 
 
 def test_argmax_lowest_index_on_ties(gpu):
@@ -57,28 +62,35 @@ def test_loaded_checkpoint_matches_cpu_model(gpu, tmp_path):
     check_against_cpu(gpu, loaded)
 
 
-def check_against_cpu(gpu, model):
+def check_against_cpu(gpu, model, B=3, T=40, steps=6, atol=LOGIT_ATOL, mean_tol=LOGIT_ATOL / 10, row_chunk=32):
+    """Prefill B random prompts of T tokens (in chunks of row_chunk rows: several of them), then `steps` greedy
+    steps on the GPU decoder and the CPU model fed the same tokens; returns the largest logit difference."""
     dev = gpu
-    B, T, steps = 3, 40, 6
     prompts = np.random.default_rng(8).integers(0, model.cfg.vocab, (B, T)).astype(np.int32)
-    dec = Fp8Decoder(model, B, T - 1 + steps, dev, row_chunk=32)  # several row chunks in the prefill
+    dec = Fp8Decoder(model, B, T - 1 + steps, dev, row_chunk=row_chunk)
     cpu = CpuModel(model, B, T - 1 + steps)
     dec.prefill(torch.from_numpy(prompts).to(dev))
     cpu.prefill(prompts)
     tok = prompts[:, -1].copy()
     out = torch.empty(B, dtype=torch.int32, device=dev)
+    worst = 0.0
     for s in range(steps):
         p = T - 1 + s
         logits = dec._step(torch.from_numpy(tok).to(dev), torch.full((B,), p, dtype=torch.int32, device=dev), out)
         want = cpu.step(tok, p)
         got = logits.cpu().numpy()
-        err = np.abs(got - want).max()
-        assert err <= LOGIT_ATOL, (s, err)
+        diff = np.abs(got - want)
+        err = diff.max()
+        print(f"step {s}: logit difference max {err:.3e} mean {diff.mean():.3e}, logits std {want.std():.3f}",
+              flush=True)
+        assert err <= atol and diff.mean() <= mean_tol, (s, err, diff.mean())
+        worst = max(worst, err)
         chosen = out.cpu().numpy()
         top2 = np.sort(want, axis=1)[:, -2:]
-        sure = top2[:, 1] - top2[:, 0] > 2 * LOGIT_ATOL
+        sure = top2[:, 1] - top2[:, 0] > 2 * atol
         np.testing.assert_array_equal(chosen[sure], want.argmax(1)[sure])
         tok = chosen  # both sides continue from the GPU's choice
+    return worst
 
 
 def test_graph_replays_equal_eager_steps(gpu):
@@ -140,3 +152,17 @@ def test_sampled_decoding_follows_the_choice_rules(gpu):
         graphed.run(1)
         torch.cuda.synchronize()
     torch.testing.assert_close(graphed.tokens(steps).cpu(), torch.stack(outs, 1).cpu())
+
+
+CFG5_SHAPE = ModelConfig(layers=26, d_model=1664, heads=13, vocab=65536)  # BASELINE config 5's architecture
+
+
+def test_config5_architecture_matches_cpu_model(gpu):
+    """The full config-5 model (26 layers, d 1664, 13 heads, vocab 65536, random init) at a size the CPU model covers:
+    4 sequences of 256-token prompts, then 4 greedy steps. Every step's logits within CFG5_LOGIT_ATOL (max) and
+    CFG5_LOGIT_MEAN (mean) of the CPU model's (torch bf16 GEMMs on the CPU, the oracle's append and fp64 attention),
+    greedy tokens equal wherever the CPU logits' top-two margin exceeds twice the tolerance."""
+    print("config 5 architecture: 4 x 256-token prompts, 4 steps", flush=True)
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    check_against_cpu(gpu, RandomModel(CFG5_SHAPE, gpu, seed=5), B=4, T=256, steps=4, atol=CFG5_LOGIT_ATOL,
+                      mean_tol=CFG5_LOGIT_MEAN, row_chunk=1024)
