@@ -261,7 +261,8 @@ void dec_destroy(void *handle);
 /* The handle's slot count. Replaces: dec_batch, decode.cu:948. */
 int dec_batch(void *handle);
 
-/* Rows per dec_prefill call (1024). Replaces: dec_prefill_rows, decode.cu:1037. */
+/* Rows per dec_prefill call (16384; the reference's 1024: its caller chunks by this value). Replaces:
+ * dec_prefill_rows, decode.cu:1037. */
 int dec_prefill_rows(void *handle);
 
 /* Slot b starts at its prompt's last token `token`, position `last` (earlier positions cached or queued for

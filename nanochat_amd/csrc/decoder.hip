@@ -42,7 +42,8 @@
 
 #define DEC_MAX_BATCH 1024 /* slots at most (decode.cu:28-29) */
 #define DEC_NARROW 256     /* the narrow graphs' slots (decode.cu:32-33) */
-#define DEC_ROWS 1024      /* prefill rows per dec_prefill (decode.cu:1037) */
+#define DEC_ROWS 16384     /* prefill rows per dec_prefill (the reference runs 1024, decode.cu:1037; its caller chunks by
+                              dec_prefill_rows, so more rows a call keep the GEMMs on their many-rows tile) */
 #define DEC_STAGES 4       /* pinned staging buffers of prefill rows in flight */
 #define DEC_ROW_BYTES 264  /* one position of one kv head in the prompt store (nc_kv_export_fp8's rows) */
 #define DEC_WORDS (DEC_MAX_BATCH / 64)

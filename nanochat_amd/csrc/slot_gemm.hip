@@ -283,6 +283,220 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
     }
 }
 
+/* ------------------------------------------------------------------------------------------------ large M */
+
+/*
+ * The same GEMM for many rows (prefill chunks: M in the thousands), where it is MFMA-bound instead of a stream of W:
+ * a workgroup of 8 waves owns a 256 x-row x 256 W-row output tile over the full K (complete sums, deterministic), and
+ * each wave a 128 x-row x 64 W-row part of it. Every output element is computed by the same instruction
+ * (v_mfma_f32_16x16x32_bf16, A = 16 W rows, B = 16 x rows), in the same order of 32-column K steps, as
+ * k_slot_gemm computes it, and the norm's Σ x² the same way (x·xᵀ's diagonal over the same steps): the result of a
+ * row does not depend on M, on the tile, or on which of the two kernels ran.
+ *
+ * K is walked in 64-column chunks through a 2-slot LDS ring (64 KB a slot: the tile's 256 W rows and 256 x rows of
+ * 128 bytes, the swizzled layout and DMA of k_slot_gemm): at the start of chunk c the DMAs of chunk c + 1 are issued
+ * into the slot chunk c - 1 used (every wave is past its reads, one barrier), then chunk c's fragments are read in
+ * two halves, the second half's reads in flight while the first half's MFMAs run. Two waves per SIMD overlap one's
+ * LDS reads with the other's MFMAs. Rows past m or n read the last row (clamped) and are not stored.
+ *
+ * Tiles are ordered XCD-aware (workgroup b on XCD b % 8 takes a contiguous range) and, within it, in groups of
+ * RG_GROUP x-row tiles that sweep the W tiles, so neighbouring workgroups share x and W rows in L2.
+ */
+#define RG_THREADS 512
+#define RG_WAVES 8
+#define RG_BM 256 /* x rows per tile */
+#define RG_BN 256 /* W rows per tile */
+#define RG_GROUP 4
+#define RG_MIN_M 512 /* nc_slot_gemm_bf16 takes this kernel from this many rows on (automatic tile) */
+
+struct RowsGemmArgs {
+    const bf16_t *w, *x;
+    void *out;
+    const bf16_t *res;
+    int n, k, m;
+    int n_tiles, m_tiles, units_per_xcd;
+};
+
+/* 16 bytes of LDS at addr + OFF (an immediate: tile offsets need no registers of their own). */
+template <int OFF> __device__ __forceinline__ bf16x8 rg_ds_read(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+/* This wave's DMA instructions of a chunk: instruction wv + RG_WAVES d lands at dst + 1024 (wv + RG_WAVES d). */
+template <int DPW>
+__device__ __forceinline__ void rg_dma(const unsigned char *const *src, size_t off, unsigned char *dst, int wv) {
+#pragma unroll
+    for (int d = 0; d < DPW; d++)
+        __builtin_amdgcn_global_load_lds(src[d] + off, dst + 1024 * (wv + RG_WAVES * d), 16, 0, 0);
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
+    constexpr int ROWS = RG_BN + RG_BM, SLOT = ROWS * 128, DPW = ROWS / 8 / RG_WAVES; /* 8 DMAs per wave a chunk */
+    constexpr int WM = 2, WN = 4;                                  /* waves over x rows x W rows */
+    constexpr int TM = RG_BM / 16 / WM, TN = RG_BN / 16 / WN;     /* 8 x tiles, 4 W tiles per wave */
+    constexpr int TSQ = TM / WN;                                   /* x tiles whose Σ x² this wave computes */
+    constexpr bool NORM = EPI == SG_NORM_STORE || EPI == SG_RELU2_NORM || EPI == SG_NORM_F32;
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[2 * SLOT];
+
+    const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
+    if (unit >= a.n_tiles * a.m_tiles) return;
+    const int per_group = RG_GROUP * a.n_tiles, group = unit / per_group, first_m = group * RG_GROUP;
+    const int gsz = min(a.m_tiles - first_m, RG_GROUP), in_group = unit % per_group;
+    const int mt = first_m + in_group % gsz, ntl = in_group / gsz;
+    const int row0 = ntl * RG_BN, m0 = mt * RG_BM;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int j = lane >> 4, n = lane & 15;
+    const int wn = wv % WN, wm = wv / WN;
+    const int chunks = a.k / SG_CHUNK;
+    const size_t ld = (size_t)a.k;
+
+    /* DMA instruction i = wv + RG_WAVES d of a chunk moves slot rows 8i..8i+7 (W rows first, then x rows) */
+    const unsigned char *src[DPW];
+#pragma unroll
+    for (int d = 0; d < DPW; d++) {
+        const int r = 8 * (wv + RG_WAVES * d) + (lane >> 3);
+        const int piece = (lane & 7) ^ (r & 7);
+        const bf16_t *row = r < RG_BN ? a.w + (size_t)min(row0 + r, a.n - 1) * ld
+                                      : a.x + (size_t)min(m0 + r - RG_BN, a.m - 1) * ld;
+        src[d] = reinterpret_cast<const unsigned char *>(row) + 16 * piece;
+    }
+    auto dma = [&](int c, int slot) {
+        rg_dma<DPW>(src, (size_t)min(c, chunks - 1) * (SG_CHUNK * 2), ring + slot * SLOT, wv);
+    };
+
+    /* fragment rows: W tile t row 16 (wn TN + t) + n, x tile u row RG_BN + 16 (wm TM + u) + n; a row's swizzle
+     * (piece ^ (row & 7)) is n & 7 for every tile, so one base address per half and operand, tiles 2048 B apart */
+    uint32_t bw[2], bx[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t swz = 16 * ((4 * h + j) ^ (n & 7));
+        bw[h] = sg_lds_addr(ring) + 128 * (16 * wn * TN + n) + swz;
+        bx[h] = sg_lds_addr(ring) + 128 * (RG_BN + 16 * wm * TM + n) + swz;
+    }
+
+    f32x4 acc[TN][TM];
+    f32x4 sq[TSQ];
+#pragma unroll
+    for (int t = 0; t < TN; t++)
+#pragma unroll
+        for (int u = 0; u < TM; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < TSQ; q++) sq[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    /* half h of chunk c's fragments (completed by the next sg_ds_wait) */
+    auto read = [&](int c, int h, bf16x8 (&wf)[TN], bf16x8 (&xf)[TM]) {
+        const uint32_t so = (uint32_t)((c & 1) * SLOT), aw = bw[h] + so, ax = bx[h] + so;
+        static_assert(TN == 4 && TM == 8, "the reads below are unrolled for 4 W and 8 x tiles");
+        wf[0] = rg_ds_read<0>(aw);
+        wf[1] = rg_ds_read<2048>(aw);
+        wf[2] = rg_ds_read<4096>(aw);
+        wf[3] = rg_ds_read<6144>(aw);
+        xf[0] = rg_ds_read<0>(ax);
+        xf[1] = rg_ds_read<2048>(ax);
+        xf[2] = rg_ds_read<4096>(ax);
+        xf[3] = rg_ds_read<6144>(ax);
+        xf[4] = rg_ds_read<8192>(ax);
+        xf[5] = rg_ds_read<10240>(ax);
+        xf[6] = rg_ds_read<12288>(ax);
+        xf[7] = rg_ds_read<14336>(ax);
+    };
+    auto settle = [&](bf16x8 (&wf)[TN], bf16x8 (&xf)[TM]) {
+        sg_ds_wait();
+#pragma unroll
+        for (int t = 0; t < TN; t++) sg_after_wait(wf[t]);
+#pragma unroll
+        for (int u = 0; u < TM; u++) sg_after_wait(xf[u]);
+    };
+    auto multiply = [&](const bf16x8 (&wf)[TN], const bf16x8 (&xf)[TM]) {
+#pragma unroll
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int u = 0; u < TM; u++)
+                acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[t], xf[u], acc[t][u], 0, 0, 0);
+        if constexpr (NORM) {
+#pragma unroll
+            for (int q = 0; q < TSQ; q++) { /* x tile q WN + wn, picked by selects (wn is wave-uniform) */
+                bf16x8 v = xf[q * WN];
+#pragma unroll
+                for (int w = 1; w < WN; w++) v = wn == w ? xf[q * WN + w] : v;
+                sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, v, sq[q], 0, 0, 0);
+            }
+        }
+    };
+
+    dma(0, 0);
+    bf16x8 w0[TN], x0[TM], w1[TN], x1[TM];
+    for (int c = 0; c < chunks; c++) {
+        sg_wait_vmcnt<0>();           /* this wave's DMAs of chunk c have landed */
+        __builtin_amdgcn_s_barrier(); /* everyone's have, and everyone is past its reads of chunk c - 1 */
+        __builtin_amdgcn_sched_barrier(0);
+        dma(c + 1, (c + 1) & 1);      /* past the end: the last chunk again, into the idle slot */
+        read(c, 0, w0, x0);
+        settle(w0, x0);
+        read(c, 1, w1, x1);
+        multiply(w0, x0);
+        settle(w1, x1);
+        multiply(w1, x1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    sg_wait_vmcnt<0>();
+
+    float rstd[TM];
+    if constexpr (NORM) {
+        float *ss = reinterpret_cast<float *>(ring);
+        __syncthreads(); /* every wave is past its last read of the ring */
+#pragma unroll
+        for (int q = 0; q < TSQ; q++)
+            if (j == (n >> 2)) ss[16 * (wm * TM + q * WN + wn) + n] = sq[q][n & 3];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TM; u++)
+            rstd[u] = 1.0f / sqrtf(ss[16 * (wm * TM + u) + n] / (float)a.k + 1.1920928955078125e-07f);
+    } else {
+#pragma unroll
+        for (int u = 0; u < TM; u++) rstd[u] = 1.f;
+    }
+
+    const int N = a.n;
+#pragma unroll
+    for (int u = 0; u < TM; u++) {
+        const int b = m0 + 16 * (wm * TM + u) + n;
+        const float r = rstd[u];
+        if (b >= a.m) continue;
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            const int col = row0 + 16 * (wn * TN + t) + 4 * j;
+            if (col >= N) continue;
+            const f32x4 s = acc[t][u];
+            const size_t at = (size_t)b * N + col;
+            if constexpr (EPI == SG_NORM_F32) {
+                *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + at) = s * r;
+            } else {
+                float v[4];
+                if constexpr (EPI == SG_RESID) {
+                    const u32x2 rr = *reinterpret_cast<const u32x2 *>(a.res + at);
+                    v[0] = s[0] + bf16_to_f32(rr[0] & 0xffffu);
+                    v[1] = s[1] + bf16_to_f32(rr[0] >> 16);
+                    v[2] = s[2] + bf16_to_f32(rr[1] & 0xffffu);
+                    v[3] = s[3] + bf16_to_f32(rr[1] >> 16);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float p = s[i] * r;
+                        v[i] = EPI == SG_RELU2_NORM ? fmaxf(p, 0.f) * p : p;
+                    }
+                }
+                const u32x2 o = {f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
+                                 f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
+                *reinterpret_cast<u32x2 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------------------------------ host side */
 
 typedef void (*SgKernel)(SlotGemmArgs);
@@ -344,6 +558,28 @@ extern "C" int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int
     NC_REQUIRE(epi != SG_RESID || res, "nc_slot_gemm_bf16: RESID needs res");
     NC_REQUIRE(((uintptr_t)w | (uintptr_t)x | (uintptr_t)out | (uintptr_t)res) % 16 == 0,
                "nc_slot_gemm_bf16: 16-byte alignment");
+    if (nt == 0 && mt == 0 && m >= RG_MIN_M) { /* many rows: the MFMA-bound tile (the same results) */
+        RowsGemmArgs r;
+        r.w = (const bf16_t *)w;
+        r.x = (const bf16_t *)x;
+        r.out = out;
+        r.res = (const bf16_t *)res;
+        r.n = n;
+        r.k = k;
+        r.m = m;
+        r.n_tiles = (n + RG_BN - 1) / RG_BN;
+        r.m_tiles = (m + RG_BM - 1) / RG_BM;
+        const long long units = (long long)r.n_tiles * r.m_tiles;
+        r.units_per_xcd = (int)((units + 7) / 8);
+        void (*kern)(RowsGemmArgs) = epi == SG_STORE        ? k_rows_gemm<SG_STORE>
+                                     : epi == SG_NORM_STORE ? k_rows_gemm<SG_NORM_STORE>
+                                     : epi == SG_RESID      ? k_rows_gemm<SG_RESID>
+                                     : epi == SG_RELU2_NORM ? k_rows_gemm<SG_RELU2_NORM>
+                                                            : k_rows_gemm<SG_NORM_F32>;
+        hipLaunchKernelGGL(kern, dim3(8 * r.units_per_xcd), dim3(RG_THREADS), 0, (hipStream_t)stream, r);
+        NC_LAUNCH_CHECK();
+        return 0;
+    }
     if (nt == 0 && mt == 0) sg_auto_tile(n, m, nt, mt);
     const SgKernel kern = sg_pick(nt, mt, epi);
     NC_REQUIRE(kern && n % nt == 0, "nc_slot_gemm_bf16: tile %d x %d is not available for n = %d", nt, mt, n);

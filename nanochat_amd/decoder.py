@@ -10,10 +10,11 @@ prefilled, then every step feeds one token per sequence and appends the chosen o
 
 with x0 = norm(embed(token)), a final norm, the untied lm_head and the token choice (nc_choose_tokens: greedy, the
 largest fp32 logit with the lowest id on ties, unless set_sampling asks for temperature / nucleus sampling). The
-decode step's weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the reference's fused epilogues
+weight GEMMs are this package's slot GEMM (nc_slot_gemm_bf16) with the reference's fused epilogues
 (decode.cu:169-184,848-877): the norms fold into the qkv, up and lm_head GEMMs as a per-row rstd, ReLU^2 into the
-up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows go
-through library GEMMs (hipBLASLt through torch) and the separate norm kernels. The cache append, prefill and decode
+up GEMM, and both residual adds into the o and down GEMMs, in place. Prefill rows use the same calls, which take the
+many-rows tile from 512 rows on: every sum in a fixed order, bit-identical to the decode tiles, so a prompt's cache
+bytes depend neither on the run nor on the other prompts prefilled with it. The cache append, prefill and decode
 attention and the token choice are HIP kernels throughout (a decode step's append and attention are one
 nc_decode_step_fp8 call per layer); the decode step is captured once in a hipGraph and replayed.
 
@@ -263,12 +264,11 @@ class Fp8Decoder:
             self.softcap = float(softcap)
 
     # ---------------------------------------------------------------------------------------------- layers
-    def _qkv_append(self, l: int, x: Tensor, h: Tensor, pos: Tensor, seq: Tensor, tok: Tensor,
-                    q_out: Tensor) -> None:
-        """h = norm(x); the projection (with the value-embedding mix), then QK-norm + RoPE + fp8 append of k, v;
-        q into q_out."""
+    def _qkv_append(self, l: int, x: Tensor, pos: Tensor, seq: Tensor, tok: Tensor, q_out: Tensor) -> None:
+        """The projection of norm(x) (the norm folded into the GEMM, as in the decode step), the value-embedding mix,
+        then QK-norm + RoPE + fp8 append of k, v; q into q_out."""
         lw = self.model.layers[l]
-        qkv = torch.matmul(h, lw["wqkv"].t())
+        qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
         self._value_embed(l, qkv, x, tok)
         self.caches[l].append(qkv, pos, seq, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
                               q_out=q_out)
@@ -289,25 +289,20 @@ class Fp8Decoder:
             return
         value_embed(qkv, x, tok, lw["ve"], lw["ve_gate"], self.cfg.heads, self.cfg.kv_heads)
 
-    def _finish_layer(self, l: int, x: Tensor, o: Tensor, h: Tensor) -> None:
-        """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place; h = norm(x), the next layer's (or
-        the final) normed input."""
+    def _finish_layer(self, l: int, x: Tensor, o: Tensor) -> None:
+        """x += o_proj(o); x += down(relu(up(norm(x)))^2), x updated in place: the decode step's three GEMMs and
+        epilogues (decode.cu:848-877)."""
         lw = self.model.layers[l]
-        m = add_rms_norm(x, torch.matmul(o.reshape(o.shape[0], -1), lw["wo"].t()), x)
-        u = relu2(torch.matmul(m, lw["wup"].t()))
-        add_rms_norm(x, torch.matmul(u, lw["wdown"].t()), x, y=h)
-
-    def _embed(self, tok: Tensor) -> tuple[Tensor, Tensor]:
-        """The residual stream x0 = norm(embed(tok)) and its norm, the first layer's input."""
-        x = embed_norm(self.model.wte, tok)
-        return x, add_rms_norm(x, None)
+        slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
+        u = slot_gemm(x, lw["wup"], RELU2_NORM)
+        slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
 
     # ---------------------------------------------------------------------------------------------- prefill
     @torch.no_grad()
     def prefill(self, prompts: Tensor) -> None:
         """Positions 0..T-2 of every prompt (int32 [batch][T]) into the caches (the last prompt token is the first
         decode step's input, inference/decoder.py:211-222). Per layer every row is appended before any attends
-        (decode.cu:859-863); GEMMs and the MLP run in chunks of row_chunk rows."""
+        (decode.cu:859-863); GEMMs and the MLP run in chunks of row_chunk rows (any chunking gives the same bits)."""
         B, T = prompts.shape
         if B != self.batch or T - 1 + 1 > self.max_len:
             raise ValueError(f"prompts {tuple(prompts.shape)} do not fit batch {self.batch}, max_len {self.max_len}")
@@ -322,7 +317,7 @@ class Fp8Decoder:
         """Rows (token, position, sequence) into the caches, each row attending its sequence's keys up to its
         position; every row of a layer is appended before any attends."""
         n = tok.shape[0]
-        x, h = self._embed(tok)
+        x = embed_norm(self.model.wte, tok)  # the residual stream x0 = norm(embed(tok))
         x0 = x.clone() if self.mixes else None
         q = torch.empty((n, self.cfg.heads, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
         o = torch.empty_like(q)
@@ -331,11 +326,10 @@ class Fp8Decoder:
             for r0, r1 in chunks:
                 if self.mixes:
                     self._mix(l, x[r0:r1], x0[r0:r1])
-                    add_rms_norm(x[r0:r1], None, y=h[r0:r1])
-                self._qkv_append(l, x[r0:r1], h[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1], q[r0:r1])
+                self._qkv_append(l, x[r0:r1], pos[r0:r1], seq[r0:r1], tok[r0:r1], q[r0:r1])
             prefill_attention(q, self.caches[l], pos, seq, window=self.cfg.window(l), out=o)
             for r0, r1 in chunks:
-                self._finish_layer(l, x[r0:r1], o[r0:r1], h[r0:r1])
+                self._finish_layer(l, x[r0:r1], o[r0:r1])
 
     # ---------------------------------------------------------------------------------------------- decode
     def _step(self, tok: Tensor, pos: Tensor, out_tok: Tensor, slots: Tensor | None = None) -> Tensor:

@@ -166,3 +166,28 @@ def test_config5_architecture_matches_cpu_model(gpu):
     torch.set_num_threads(min(16, torch.get_num_threads()))
     check_against_cpu(gpu, RandomModel(CFG5_SHAPE, gpu, seed=5), B=4, T=256, steps=4, atol=CFG5_LOGIT_ATOL,
                       mean_tol=CFG5_LOGIT_MEAN, row_chunk=1024)
+
+
+def test_prefill_is_deterministic_and_batch_independent(gpu):
+    """Every sum of the prefill is in a fixed order: prefilling the same prompts twice gives the same cache bytes,
+    and a prompt prefilled alone gives the bytes it gets among others (the reference's promise that a request's
+    tokens depend on neither the batch nor the store, inference/decoder.py:124-125). 700 rows: the GEMMs take the
+    many-rows tile together and the decode tile alone."""
+    model = RandomModel(ModelConfig(layers=2, d_model=512, heads=4, vocab=1000), gpu, seed=17)
+    prompts = torch.from_numpy(np.random.default_rng(18).integers(0, 1000, (4, 176)).astype(np.int32)).to(gpu)
+    a = Fp8Decoder(model, 4, 200, gpu)
+    b = Fp8Decoder(model, 4, 200, gpu)
+    a.prefill(prompts)
+    b.prefill(prompts)
+    alone = Fp8Decoder(model, 1, 200, gpu)
+    alone.prefill(prompts[2:3])
+    torch.cuda.synchronize()
+    mb = a.caches[0].max_blocks
+    for l in range(2):
+        assert torch.equal(a.caches[l].pages, b.caches[l].pages), l
+        assert torch.equal(a.caches[l].pages[2 * mb:3 * mb], alone.caches[l].pages[:mb]), l
+    # and the generations that follow: the same tokens, run after run (bench.py's config 5 digest, at a small size)
+    for d in (a, b):
+        d.start(prompts[:, -1], 175)
+        d.run(12)
+    assert torch.equal(a.tokens(12), b.tokens(12))

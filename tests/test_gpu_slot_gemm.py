@@ -94,3 +94,33 @@ def test_resid_in_place_and_repeatable(gpu):
     again = slot_gemm(x, w, RESID, res=res)
     torch.cuda.synchronize()
     assert torch.equal(again, h)  # same bits, call after call
+
+
+@pytest.mark.parametrize("m, n, k", [
+    (1000, 1664, 1664),   # o / a prefill chunk of the decoder handle: partial x and W tiles
+    (600, 4992, 1664),    # qkv
+    (2100, 6656, 1664),   # up
+    (513, 1664, 6656),    # down, one row past a tile
+])
+@pytest.mark.parametrize("epi", [STORE, NORM_STORE, RESID, RELU2_NORM, NORM_F32])
+def test_many_rows_equal_the_decode_tiles(gpu, m, n, k, epi):
+    """From 512 rows on the automatic tile is the many-rows kernel (256 x 256 tiles): every output bit equals the
+    decode kernel's (a forced 64 x 128 tile) for the same rows, so a row's result does not depend on how many rows
+    were computed with it; and both are within the epilogue's tolerance of fp32."""
+    x, w, res = data(m, n, k, gpu, seed=m + 3 * n + k + epi)
+    r = res if epi == RESID else None
+    got = slot_gemm(x, w, epi, res=r)
+    want = slot_gemm(x, w, epi, res=r, tile=(64, 128))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got.float() - want.float()).abs().max()
+    check(got, reference(x, w, epi, res), f"many rows m {m} n {n} k {k} epi {epi}")
+
+
+def test_many_rows_in_place_residual(gpu):
+    m, n, k = 777, 1664, 1664
+    x, w, res = data(m, n, k, gpu, seed=21)
+    want = slot_gemm(x, w, RESID, res=res)
+    h = res.clone()
+    slot_gemm(x, w, RESID, res=h, out=h)
+    torch.cuda.synchronize()
+    assert torch.equal(h, want)
