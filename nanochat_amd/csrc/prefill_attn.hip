@@ -30,8 +30,9 @@
  * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
  * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
  * conflict-free ds_read_b128 per fragment). Each of the 8 waves issues 2 of a pair's 10 DMAs (one 1 KiB fragment
- * load, one 32 B part of the scales) from a scalar tile base, PF_RING - 1 pairs ahead. Block ids are staged in
- * LDS per chunk of PF_IDS pages.
+ * load, one 32 B part of the scales) from a scalar tile base; the waves meet at a barrier every PF_BATCH pairs,
+ * where the ring's freed slots are refilled, so between barriers the two waves of a SIMD may drift apart. Block ids
+ * are staged in LDS per chunk of PF_IDS pages.
  *
  * Software pipeline: iteration k issues the score MFMAs of pair k + 1 and, independent of them, the softmax and
  * the value MFMAs of pair k. A wave's VALU work does not issue under its own MFMAs on gfx950 (measured: an MFMA
@@ -50,8 +51,10 @@
 #define PF_BLOCKS 2        /* 16-column MFMA blocks per wave */
 #endif
 #ifndef PF_RING
-#define PF_RING 8          /* page-pair slots: 7 pairs (59 KB) in flight while one is computed */
+#define PF_RING 8          /* page-pair slots (67.6 KB) */
 #endif
+#define PF_BATCH 2         /* pairs between barriers: the ring is refilled PF_BATCH pairs at a time, and the waves of
+                              a SIMD drift up to PF_BATCH pairs apart (3 % faster than a barrier every pair) */
 #define PF_DMA_PER_PAIR 2  /* per wave: one fragment, one scale part */
 #define PF_PAIR_BYTES (2 * NC_TILE_BYTES)
 #define PF_IDS 1024        /* block ids staged per chunk of a segment's pages */
@@ -530,20 +533,25 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 ids[e] = e < cp ? lookup_block(block_table, a.max_blocks, a.num_blocks, s, first + cb + e) : -1;
             __syncthreads();
             const PfDma dp = dma_plan(wv, lane);
-            int pro[PF_RING - 1][2];
+            /* the ring: pair p in slot p % PF_RING; pairs 0..PRO - 1 in flight before step 0, and the batch starting
+             * at step k (k % PF_BATCH == 0) refills the slots of pairs k - PF_BATCH .. k - 1 with pairs
+             * k + PRO .. k + PF_RING - 1 (past the end: the last pair again) */
+            constexpr int PRO = PF_RING - PF_BATCH;
+            static_assert(PF_RING >= 2 * PF_BATCH + 1, "ring depth for the batch");
+            int pro[PRO][2];
 #pragma unroll
-            for (int k = 0; k < PF_RING - 1; k++) {
+            for (int k = 0; k < PRO; k++) {
                 pro[k][0] = __builtin_amdgcn_readfirstlane(ids[2 * min(k, npairs - 1)]);
                 pro[k][1] = __builtin_amdgcn_readfirstlane(ids[2 * min(k, npairs - 1) + 1]);
             }
 #pragma unroll
-            for (int k = 0; k < PF_RING - 1; k++) {
+            for (int k = 0; k < PRO; k++) {
                 __builtin_amdgcn_sched_barrier(0);
                 dma_pair(a, pro[k][0], pro[k][1], h, dp, lane, ring + k * PF_PAIR_BYTES);
             }
             __builtin_amdgcn_sched_barrier(0);
             /* pipeline fill: the scores of pair 0 */
-            pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 2)>(); /* this wave's DMAs of pair 0 have landed */
+            pf_wait_vmcnt<PF_DMA_PER_PAIR * (PRO - 1)>(); /* this wave's DMAs of pair 0 have landed */
             __builtin_amdgcn_s_barrier();                      /* everyone's have */
             __builtin_amdgcn_sched_barrier(0);
             PfKeys kf;
@@ -555,17 +563,26 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             /* iteration k: the scores of pair k + 1 into one buffer while pair k's softmax and values read the other
              * (unrolled twice so the buffers swap without copies) */
             auto step = [&](int k, f32x4 (*s_cur)[2], f32x4 (*s_next)[2]) {
-                pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 3)>(); /* this wave's DMAs of pair k + 1 have landed */
-                __builtin_amdgcn_s_barrier();                      /* everyone's have; slot k - 1 is free */
-                __builtin_amdgcn_sched_barrier(0);
-                const int kr = k + PF_RING - 1;
-                dma_pair(a, __builtin_amdgcn_readfirstlane((int)ids_dma[0]),
-                         __builtin_amdgcn_readfirstlane((int)ids_dma[1]), h, dp, lane,
-                         ring + (kr % PF_RING) * PF_PAIR_BYTES);
+                if (k % PF_BATCH == 0) {
+                    /* this wave's DMAs of pairs <= k + PF_BATCH have landed (later ones may fly) */
+                    pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 1 - 2 * PF_BATCH)>();
+                    __builtin_amdgcn_s_barrier(); /* everyone's have; the slots of pairs < k are free */
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int bb = 0; bb < PF_BATCH; bb++) {
+                        const int kr = k + PRO + bb;
+                        u32x2 id;
+                        asm volatile("ds_read_b64 %0, %1\n s_waitcnt lgkmcnt(0)"
+                                     : "=v"(id) : "v"(lds_addr(ids + 2 * min(kr, npairs - 1))) : "memory");
+                        dma_pair(a, __builtin_amdgcn_readfirstlane((int)id[0]),
+                                 __builtin_amdgcn_readfirstlane((int)id[1]), h, dp, lane,
+                                 ring + (kr % PF_RING) * PF_PAIR_BYTES);
+                    }
+                }
                 PfVals vf;
                 u32x2 ids_next;
                 read_stage(ring + (k % PF_RING) * PF_PAIR_BYTES, ring + ((k + 1) % PF_RING) * PF_PAIR_BYTES, ids,
-                           min(k + 1, npairs - 1), min(kr + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
+                           min(k + 1, npairs - 1), min(k + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
                 __builtin_amdgcn_sched_barrier(0);
                 if (c.active) {
                     pair_scores(kf, q8, s_next); /* pair k + 1 (past the end: the clamped refill, unused) */
