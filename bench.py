@@ -169,15 +169,15 @@ def pmc_summary(dirs: list[str], kernels: list[str], last: int) -> dict:
                         per[(name, r["Counter_Name"])].append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
     out = {}
     for name in list(kernels) + ["copy_probe"]:
-        c = {}
+        c, n = {}, 0
         for (k, counter), v in per.items():
             if k == name:
                 v.sort()
                 vals = [x for _, x in v[-(3 if name == "copy_probe" else last):]]
-                c[counter] = sum(vals) / len(vals)
+                c[counter], n = sum(vals) / len(vals), len(vals)
         if not c:
             continue
-        d = {"dispatches_averaged": 3 if name == "copy_probe" else last, "counters": c}
+        d = {"dispatches_averaged": n, "counters": c}
         g = lambda n: c.get(n + "_sum", c.get(n))
         if all(g(n) is not None for n in ("TCC_EA0_RDREQ_32B", "TCC_EA0_RDREQ_64B", "TCC_EA0_RDREQ_128B")):
             d["read_bytes"] = 32 * g("TCC_EA0_RDREQ_32B") + 64 * g("TCC_EA0_RDREQ_64B") + 128 * g("TCC_EA0_RDREQ_128B")

@@ -29,6 +29,10 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wshad
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form",
          f"-I{PACKAGE.parent / 'include'}"]
 
+# Per-source additions. prefill_attn.hip: no IEEE mode and no NaN semantics, so fmaxf compiles to plain v_max
+# without NaN-quieting canonicalisations (the kernel's inputs are finite; a NaN in q or the cache has no meaning).
+FILE_FLAGS = {"prefill_attn.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"]}
+
 
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
@@ -38,7 +42,7 @@ def digest() -> str:
     """Of the command (with the repository-relative include path, so a copy of the tree elsewhere, e.g. on the GPU
     box, sees the same digest) and of every source and header."""
     flags = [f.replace(str(PACKAGE.parent), ".") for f in FLAGS]
-    h = hashlib.sha256(" ".join([os.path.basename(HIPCC), *flags]).encode())
+    h = hashlib.sha256(" ".join([os.path.basename(HIPCC), *flags, repr(sorted(FILE_FLAGS.items()))]).encode())
     for f in sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(PACKAGE.parent / "include").glob("*.h")]):
         h.update(f.name.encode())
         h.update(f.read_bytes())
@@ -58,7 +62,7 @@ def build(verbose: bool = True) -> Path:
 
         def compile_one(pair):
             src, obj = pair
-            cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+            cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
             r = subprocess.run(cmd, capture_output=True, text=True)
             if r.returncode != 0:
                 raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")

@@ -8,10 +8,13 @@
  * included. Rows may come in any order and from any sequences; the kernel is fastest when a sequence's rows are
  * consecutive.
  *
- * Work: one workgroup of 8 waves (two per SIMD) per (kv head h, tile of 16 R consecutive rows), R = floor(16 / G)
+ * Work: one workgroup of 4 waves (one per SIMD) per (kv head h, tile of 8 R consecutive rows), R = floor(16 / G)
  * rows per 16-column MFMA block, G = Hq / Hkv. A wave holds 2 blocks; column n of a block is (row n / G, query
  * head h G + n % G), so the G heads of a row share every key read. The workgroup walks the pages of the union key
- * range of its rows in pairs; all eight waves consume the same pair from LDS.
+ * range of its rows in pairs; its four waves consume the same pair from LDS. Two workgroups share a CU (256
+ * VGPRs and 72 KB of LDS each), so the two waves of a SIMD belong to different workgroups: no barrier ties their
+ * phases together, and one workgroup's set-up and epilogue overlap the other's page loop (short key ranges:
+ * 1.3x the speed of 8-wave workgroups, one per CU).
  *
  * Per page pair (32 keys) a wave computes, for each of its 2 blocks,
  *   scores  Sᵀ[16 keys][16 columns] per page = K · Qᵀ on fp8 MFMAs: v_mfma_scale_f32_16x16x128_f8f6f4 takes the
@@ -29,33 +32,27 @@
  *
  * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
  * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
- * conflict-free ds_read_b128 per fragment). Each of the 8 waves issues 2 of a pair's 10 DMAs (one 1 KiB fragment
- * load, one 32 B part of the scales) from a scalar tile base; the waves meet at a barrier every PF_BATCH pairs,
- * where the ring's freed slots are refilled, so between barriers the two waves of a SIMD may drift apart. Block ids
- * are staged in LDS per chunk of PF_IDS pages.
+ * conflict-free ds_read_b128 per fragment). Each wave issues 2 of a pair's 8 fragment loads from a scalar tile
+ * base, the last wave also the pair's scales; the waves meet at a barrier every PF_BATCH pairs, where the ring's
+ * freed slots are refilled. Block ids are staged in LDS per chunk of PF_IDS pages.
  *
  * Software pipeline: iteration k issues the score MFMAs of pair k + 1 and, independent of them, the softmax and
  * the value MFMAs of pair k. A wave's VALU work does not issue under its own MFMAs on gfx950 (measured: an MFMA
  * plus 4 independent v_mul cost their sum), but it does under the other wave's on the same SIMD; the pipeline
- * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps, and the MFMA bursts
- * run at raised wave priority (s_setprio 1) so that the other wave's VALU fills them (config 4: 187-190 us against
- * 191-192 us without).
+ * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps, and the value MFMA
+ * bursts run at raised wave priority (s_setprio 1) so that the other wave's VALU fills them.
+ *
+ * Compiled without IEEE mode and NaN semantics (build.py): the maxima of the lazy-max and scale checks need no
+ * NaN-quieting canonicalisations then (2-5 % faster, same bits on finite inputs).
  */
 #include "layout.h"
 
-#ifndef PF_WAVES
-#define PF_WAVES 8         /* per workgroup, two per SIMD */
-#endif
+#define PF_WAVES 4         /* per workgroup, one per SIMD; two workgroups per CU */
 #define PF_THREADS (PF_WAVES * NC_WAVE)
-#ifndef PF_BLOCKS
 #define PF_BLOCKS 2        /* 16-column MFMA blocks per wave */
-#endif
-#ifndef PF_RING
 #define PF_RING 8          /* page-pair slots (67.6 KB) */
-#endif
 #define PF_BATCH 2         /* pairs between barriers: the ring is refilled PF_BATCH pairs at a time, and the waves of
                               a SIMD drift up to PF_BATCH pairs apart (3 % faster than a barrier every pair) */
-#define PF_DMA_PER_PAIR 2  /* per wave: one fragment, one scale part */
 #define PF_PAIR_BYTES (2 * NC_TILE_BYTES)
 #define PF_IDS 1024        /* block ids staged per chunk of a segment's pages */
 #define PF_LAZY 8.0f
@@ -116,33 +113,58 @@ template <int N> __device__ __forceinline__ void pf_wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-/* This wave's share of a pair's DMAs: fragment `part` (K bytes 0-15 / 16-31 of every lane, V bytes 0-15 / 16-31)
- * of page `page` of the pair, and a 32 B part of that page's scales (lanes 0-1). Per-lane byte offsets within a
- * tile are fixed for the whole loop; the tile base is wave-uniform. */
+/* A ring slot holds a page pair as [A: K 2 KiB, V 2 KiB][B: K, V][A: K and V scales 128 B][B: scales]. Its 8
+ * fragments of 1 KiB (K bytes 0-15 / 16-31 of every lane, V bytes 0-15 / 16-31, per page) are spread over the
+ * waves, 2 each; the last wave also loads both pages' scales with one dword DMA of all 64 lanes (lane l: page
+ * l / 32, bytes 4 (l % 32) of its scales). No DMA runs under a partial exec mask: the compiler may merge two
+ * exec-masked DMAs of different LDS destinations into one whose M0 (the destination, which must be wave-uniform)
+ * comes from a divergent value. Per-lane byte offsets within a tile are fixed for the whole loop; the tile base is
+ * wave-uniform. */
+#define PF_FRAGS (8 / PF_WAVES)         /* fragments per wave and pair */
+#define PF_SLOT_SCALES (4 * NC_TILE_V)  /* 8192: both pages' scales */
+#define PF_SCALE_WAVE (PF_WAVES - 1)
 struct PfDma {
-    uint32_t frag, scale;
-    int page, part;
+    uint32_t frag[PF_FRAGS];
+    int page[PF_FRAGS], part[PF_FRAGS];
+    uint32_t scale; /* the scale DMA's lane offset within its page's tile */
+    int scale_page;
 };
 
 __device__ __forceinline__ PfDma dma_plan(int wv, int lane) {
-    static_assert(PF_WAVES == 8, "one fragment and one scale part per wave");
     const int n = lane & 15, j = lane >> 4;
     PfDma d;
-    d.page = wv >> 2;
-    d.part = wv & 3;
-    d.frag = (d.part < 2 ? n * NC_HEAD_DIM + j * 32 : NC_TILE_V + j * 512 + n * 32) + 16 * (d.part & 1);
-    d.scale = NC_TILE_KS + 32 * d.part + 16 * lane;
+#pragma unroll
+    for (int i = 0; i < PF_FRAGS; i++) {
+        const int f = wv * PF_FRAGS + i;
+        d.page[i] = f >> 2;
+        d.part[i] = f & 3;
+        d.frag[i] = (d.part[i] < 2 ? n * NC_HEAD_DIM + j * 32 : NC_TILE_V + j * 512 + n * 32) + 16 * (d.part[i] & 1);
+    }
+    d.scale_page = lane >> 5;
+    d.scale = NC_TILE_KS + 4 * (lane & 31);
     return d;
 }
 
-__device__ __forceinline__ void dma_pair(const PrefillArgs &a, int blk0, int blk1, int h, const PfDma &d, int lane,
+__device__ __forceinline__ void dma_pair(const PrefillArgs &a, int blk0, int blk1, int h, const PfDma &d, int wv,
                                          unsigned char *slot) {
-    int blk = d.page ? blk1 : blk0;
-    blk = blk < 0 ? 0 : blk; /* no block: load block 0, masked later */
-    const uint8_t *tile = a.cache + ((size_t)blk * a.hkv + h) * NC_TILE_BYTES;
-    unsigned char *dst = slot + d.page * NC_TILE_BYTES;
-    __builtin_amdgcn_global_load_lds(tile + d.frag, dst + d.part * 1024, 16, 0, 0);
-    if (lane < 2) __builtin_amdgcn_global_load_lds(tile + d.scale, dst + NC_TILE_KS + 32 * d.part, 16, 0, 0);
+    blk0 = blk0 < 0 ? 0 : blk0; /* no block: load block 0, masked later */
+    blk1 = blk1 < 0 ? 0 : blk1;
+    const uint8_t *t0 = a.cache + ((size_t)blk0 * a.hkv + h) * NC_TILE_BYTES;
+    const uint8_t *t1 = a.cache + ((size_t)blk1 * a.hkv + h) * NC_TILE_BYTES;
+#pragma unroll
+    for (int i = 0; i < PF_FRAGS; i++)
+        __builtin_amdgcn_global_load_lds((d.page[i] ? t1 : t0) + d.frag[i],
+                                         slot + d.page[i] * 2 * NC_TILE_V + d.part[i] * 1024, 16, 0, 0);
+    if (wv == PF_SCALE_WAVE) /* wave-uniform */
+        __builtin_amdgcn_global_load_lds((d.scale_page ? t1 : t0) + d.scale, slot + PF_SLOT_SCALES, 4, 0, 0);
+}
+
+/* Wait until at most this wave's DMAs of its last N pairs are in flight. */
+template <int N> __device__ __forceinline__ void pf_wait_pairs(int wv) {
+    if (wv == PF_SCALE_WAVE)
+        pf_wait_vmcnt<(PF_FRAGS + 1) * N>();
+    else
+        pf_wait_vmcnt<PF_FRAGS * N>();
 }
 
 /* K fragments of a pair for the score MFMAs: dims 32j.. of key n, both pages. */
@@ -169,8 +191,8 @@ __device__ __forceinline__ void read_keys(const unsigned char *slot_k, const int
     asm volatile(
         "ds_read_b128 %0, %6\n"
         "ds_read_b128 %1, %6 offset:1024\n"
-        "ds_read_b128 %2, %6 offset:4224\n"
-        "ds_read_b128 %3, %6 offset:5248\n"
+        "ds_read_b128 %2, %6 offset:4096\n"
+        "ds_read_b128 %3, %6 offset:5120\n"
         "ds_read_b64 %4, %7\n"
         "ds_read_b64 %5, %8\n"
         "s_waitcnt lgkmcnt(0)"
@@ -184,23 +206,23 @@ __device__ __forceinline__ void read_keys(const unsigned char *slot_k, const int
 __device__ __forceinline__ void read_stage(const unsigned char *slot_v, const unsigned char *slot_k, const int *ids,
                                            int pair_k, int pair_dma, int lane, PfVals &v, PfKeys &k, u32x2 &ids_k,
                                            u32x2 &ids_dma) {
-    const uint32_t mv = lds_addr(slot_v) + 16 * lane, sv = lds_addr(slot_v) + NC_TILE_KS + 16 * (lane >> 4);
+    const uint32_t mv = lds_addr(slot_v) + 16 * lane, sv = lds_addr(slot_v) + PF_SLOT_SCALES + 16 * (lane >> 4);
     const uint32_t mk = lds_addr(slot_k) + 16 * lane;
     asm volatile(
         "ds_read_b128 %0, %14\n"
         "ds_read_b128 %1, %14 offset:1024\n"
-        "ds_read_b128 %2, %14 offset:4224\n"
-        "ds_read_b128 %3, %14 offset:5248\n"
+        "ds_read_b128 %2, %14 offset:4096\n"
+        "ds_read_b128 %3, %14 offset:5120\n"
         "ds_read_b64 %12, %15\n"
         "ds_read_b64 %13, %16\n"
         "ds_read_b128 %4, %17 offset:2048\n"
         "ds_read_b128 %5, %17 offset:3072\n"
-        "ds_read_b128 %6, %17 offset:6272\n"
-        "ds_read_b128 %7, %17 offset:7296\n"
+        "ds_read_b128 %6, %17 offset:6144\n"
+        "ds_read_b128 %7, %17 offset:7168\n"
         "ds_read_b128 %8, %18\n"
-        "ds_read_b128 %9, %18 offset:4224\n"
+        "ds_read_b128 %9, %18 offset:128\n"
         "ds_read_b128 %10, %18 offset:64\n"
-        "ds_read_b128 %11, %18 offset:4288\n"
+        "ds_read_b128 %11, %18 offset:192\n"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k.a0), "=&v"(k.a1), "=&v"(k.b0), "=&v"(k.b1), "=&v"(v.a0), "=&v"(v.a1), "=&v"(v.b0), "=&v"(v.b1),
           "=&v"(v.ks_a), "=&v"(v.ks_b), "=&v"(v.vs_a), "=&v"(v.vs_b), "=&v"(ids_k), "=&v"(ids_dma)
@@ -413,7 +435,7 @@ __device__ __forceinline__ int key_lo(const PrefillArgs &a, int p) {
     return (a.window < 0 || p <= a.window) ? 0 : p - a.window;
 }
 
-__global__ void __launch_bounds__(PF_THREADS, 1)
+__global__ void __launch_bounds__(PF_THREADS, 2)
     k_prefill(PrefillArgs a, const int32_t *__restrict__ pos, const int32_t *__restrict__ seq,
               const int32_t *__restrict__ block_table) {
     __shared__ __attribute__((aligned(16))) unsigned char ring[PF_RING * PF_PAIR_BYTES];
@@ -547,11 +569,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
             for (int k = 0; k < PRO; k++) {
                 __builtin_amdgcn_sched_barrier(0);
-                dma_pair(a, pro[k][0], pro[k][1], h, dp, lane, ring + k * PF_PAIR_BYTES);
+                dma_pair(a, pro[k][0], pro[k][1], h, dp, wv, ring + k * PF_PAIR_BYTES);
             }
             __builtin_amdgcn_sched_barrier(0);
             /* pipeline fill: the scores of pair 0 */
-            pf_wait_vmcnt<PF_DMA_PER_PAIR * (PRO - 1)>(); /* this wave's DMAs of pair 0 have landed */
+            pf_wait_pairs<PRO - 1>(wv); /* this wave's DMAs of pair 0 have landed */
             __builtin_amdgcn_s_barrier();                      /* everyone's have */
             __builtin_amdgcn_sched_barrier(0);
             PfKeys kf;
@@ -565,7 +587,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             auto step = [&](int k, f32x4 (*s_cur)[2], f32x4 (*s_next)[2]) {
                 if (k % PF_BATCH == 0) {
                     /* this wave's DMAs of pairs <= k + PF_BATCH have landed (later ones may fly) */
-                    pf_wait_vmcnt<PF_DMA_PER_PAIR * (PF_RING - 1 - 2 * PF_BATCH)>();
+                    pf_wait_pairs<PF_RING - 1 - 2 * PF_BATCH>(wv);
                     __builtin_amdgcn_s_barrier(); /* everyone's have; the slots of pairs < k are free */
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -575,7 +597,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                         asm volatile("ds_read_b64 %0, %1\n s_waitcnt lgkmcnt(0)"
                                      : "=v"(id) : "v"(lds_addr(ids + 2 * min(kr, npairs - 1))) : "memory");
                         dma_pair(a, __builtin_amdgcn_readfirstlane((int)id[0]),
-                                 __builtin_amdgcn_readfirstlane((int)id[1]), h, dp, lane,
+                                 __builtin_amdgcn_readfirstlane((int)id[1]), h, dp, wv,
                                  ring + (kr % PF_RING) * PF_PAIR_BYTES);
                     }
                 }
