@@ -56,6 +56,7 @@
 #define PF_PAIR_BYTES (2 * NC_TILE_BYTES)
 #define PF_IDS 1024        /* block ids staged per chunk of a segment's pages */
 #define PF_LAZY 8.0f
+#define PF_LW_MAX 64 /* the largest power of two folded into p (keeps p w and l finite for zero value scales) */
 #define PF_M_INIT -3.0e38f
 #define PF_NO_KEY 0x40000000
 
@@ -231,12 +232,17 @@ __device__ __forceinline__ void read_stage(const unsigned char *slot_v, const un
 }
 
 /* The online-softmax state of a wave's 4 blocks, lane (j, n): column n's reference max m[bl] and this lane's
- * partial sum l[bl]; Oᵀ in o[bl][bb][i] = dim 8 (4j + i) + bb of column n, in units of 2^(e_ref - 126). */
+ * partial sum l[bl]; Oᵀ in o[bl][bb][i] = dim 8 (4j + i) + bb of column n. Both carry the factor w = 2^lw,
+ * lw = min(126 - e_ref, PF_LW_MAX) with e_ref the largest v_scale exponent so far: p w v_scale < 2^9 stays in
+ * fp16 for the value MFMAs, and w folds into the exponent, p w = exp2(s k_scale score_scale - m + lw). */
 struct PfState {
     f32x4 o[PF_BLOCKS][8];
     float m[PF_BLOCKS], l[PF_BLOCKS];
-    float w, vlim;
+    float vlim;
     int e_ref;
+    float mo[PF_BLOCKS]; /* lw - m: t = s k_scale score_scale + mo = log2(p w) */
+    float lazy;          /* PF_LAZY + lw */
+    int lw;              /* log2 w = min(126 - e_ref, PF_LW_MAX) */
 };
 
 /* A wave's view of the segment being attended: per column the key range [lo, hi] (lo > hi: masked throughout),
@@ -257,8 +263,9 @@ struct PfQ8 {
 
 typedef short pf_i16x2 __attribute__((ext_vector_type(2)));
 
-/* 32 bf16 of q (this lane's dims 32j .. 32j+31 of its column) -> the two e4m3 terms; the column's exponent from
- * its absmax over the four lanes holding it (xor 16, 32). A zero column gives zero terms. */
+/* 32 bf16 of q (this lane's dims 32j .. 32j+31 of its column) -> the two e4m3 terms (exact for a bf16 value whose low
+ * term stays in e4m3's normal range: 4 + 4 significant bits); the column's exponent from its absmax over the four
+ * lanes holding it (xor 16, 32). A zero column gives zero terms. */
 __device__ PfQ8 quantize_q(const u32x4 (&u)[4]) {
 #pragma clang fp contract(off)
     float x[32];
@@ -320,7 +327,7 @@ __device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32
 }
 
 /* Softmax and value MFMAs of a pair whose scores are s (keys of pages page0, page0 + 1 with blocks ida, idb) and
- * whose values and scales are v. t = s * k_scale * score_scale - m, so p = exp2(t). */
+ * whose values and scales are v. t = s k_scale score_scale - m + lw, so exp2(t) = p w. */
 __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const f32x4 (*s)[2], const PfVals &v,
                                                     int ida, int idb, int page0, const PfCols &c, int j, PfState &st) {
     float ksc[8], vs[8];
@@ -335,7 +342,7 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) t[bl][i] = __builtin_fmaf(s[bl][i >> 2][i & 3], ksc[i], -st.m[bl]);
+        for (int i = 0; i < 8; i++) t[bl][i] = __builtin_fmaf(s[bl][i >> 2][i & 3], ksc[i], st.mo[bl]);
     /* masks: wave-uniform test, per-lane keys only on pairs that need it */
     const int key0 = page0 * NC_PAGE + 4 * j;
     const bool fast = ida >= 0 && idb >= 0 && !c.masked_always && page0 * NC_PAGE >= c.max_lo &&
@@ -363,7 +370,7 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const float tm = fmaxf(fmaxf(fmaxf(t[bl][0], t[bl][1]), fmaxf(t[bl][2], t[bl][3])),
                                fmaxf(fmaxf(t[bl][4], t[bl][5]), fmaxf(t[bl][6], t[bl][7])));
-        need |= tm > PF_LAZY;
+        need |= tm > st.lazy;
     }
     if (__any(need)) { /* rare: move every block's reference max to its exact max (from the unshifted scores) */
 #pragma unroll
@@ -382,27 +389,32 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= alpha;
             st.m[bl] = m_new;
+            st.mo[bl] = (float)st.lw - m_new;
 #pragma unroll
-            for (int i = 0; i < 8; i++) t[bl][i] = x[i] - m_new;
+            for (int i = 0; i < 8; i++) t[bl][i] = x[i] + st.mo[bl];
         }
     }
     const float vm = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])), fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
-    if (__any(vm >= st.vlim)) { /* rare: a larger v_scale exponent, rescale the units of o */
+    if (__any(vm >= st.vlim)) { /* rare: a larger v_scale exponent: w = 2^lw drops, o, l and t follow */
         float vx = fmaxf(vm, shfl_xor_f(vm, 16));
         vx = fmaxf(vx, shfl_xor_f(vx, 32));
         const int e_new = max(st.e_ref, (int)(__float_as_uint(vx) >> 23));
-        const float r = pf_exp2i(max(st.e_ref - e_new, -126));
+        const int lw_new = min(126 - e_new, PF_LW_MAX), d = lw_new - st.lw;
+        const float r = pf_exp2i(max(d, -126));
 #pragma unroll
-        for (int bl = 0; bl < PF_BLOCKS; bl++)
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= r;
+            st.l[bl] *= r;
+            st.mo[bl] += (float)d;
+#pragma unroll
+            for (int i = 0; i < 8; i++) t[bl][i] += (float)d;
+        }
+        st.lw = lw_new;
+        st.lazy = PF_LAZY + (float)lw_new;
         st.e_ref = e_new;
-        st.w = pf_exp2i(max(126 - e_new, -126));
         st.vlim = pf_exp2i(min(e_new - 126, 127));
     }
-    float vw[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) vw[i] = vs[i] * st.w;
     f16x8 pp[PF_BLOCKS];
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
@@ -411,7 +423,7 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
         for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(t[bl][i]);
         st.l[bl] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 #pragma unroll
-        for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vw[i]);
+        for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vs[i]);
     }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -476,8 +488,11 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         st.l[bl] = 0.f;
     }
     st.e_ref = 0;
-    st.w = pf_exp2i(126);
     st.vlim = pf_exp2i(-126);
+    st.lw = PF_LW_MAX;
+    st.lazy = PF_LAZY + (float)PF_LW_MAX;
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) st.mo[bl] = (float)PF_LW_MAX - PF_M_INIT;
 
     /* the tile's positions and sequences, read once into LDS ((-1, -1) past the rows) */
     for (int k = tid; k < TR; k += PF_THREADS) {
@@ -623,7 +638,6 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
     }
 
     /* normalise and store; rows with an invalid position or sequence get zeros */
-    const float scale_unit = pf_exp2i(st.e_ref - 126);
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         float l = st.l[bl];
@@ -633,7 +647,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         if (!(n < R * G && r < a.n)) continue;
         const int2 ps = rows_ps[r - row0];
         const bool zero = !(row_valid(a, ps.x, ps.y) && l > 0.f); /* +0, not o * 0 (which keeps signs) */
-        const float inv = zero ? 0.f : scale_unit / l;
+        const float inv = zero ? 0.f : 1.0f / l; /* o and l both carry w */
         bf16_t *dst = a.out + ((size_t)r * a.hq + h * G + n % G) * NC_HEAD_DIM;
 #pragma unroll
         for (int i = 0; i < 4; i++) {

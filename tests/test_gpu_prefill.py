@@ -97,3 +97,26 @@ def test_single_rows_agree_with_decode(gpu):
     torch.cuda.synchronize()
     torch.testing.assert_close(out.float(), dec.float(), atol=4e-3, rtol=2e-2)
     assert_attention_close(out, oracle_rows(case, q, case.pos, case.seq, -1), "as-decode")
+
+
+
+def test_value_scales_below_the_headroom_cap(gpu):
+    """Every value scale below 2^-65, so the kernel's P headroom w = 2^lw sits at its cap (2^64) throughout, and the
+    largest v_scale exponent rises once (the first 8 pages at 2^-67 times the ordinary scales, the rest of the cache
+    and the chunk's values at 2^-66): o and l must keep one unit across the rise. Outputs are ~2^-66, so both sides
+    are compared after a factor 2^66; a wrong rescale of o would shift the first pages' half of every row by 2x."""
+    dev = gpu
+    cfg = PrefillConfig("values-below-cap", 2, 8, 2, cached=(200, 150), chunk=(40, 30), paged=True, seed=81)
+    case = build_prefill_case(cfg, dev)
+    c = case.cache
+    v0 = (cfg.hq + cfg.hkv) * 128
+    case.qkv[:, v0:] = (case.qkv[:, v0:].float() * 2.0 ** -66).to(torch.bfloat16)
+    for s in range(cfg.batch):
+        for p in range(-(-int(case.cached[s]) // 16)):
+            blk = int(c.block_table[s, p]) if c.block_table is not None else s * c.max_blocks + p
+            c.v_scale[blk] *= 2.0 ** (-67 if p < 8 else -66)
+    q, out = prefill_step(case)
+    torch.cuda.synchronize()
+    want = oracle_rows(case, q, case.pos, case.seq, -1)
+    assert np.abs(want).max() < 2.0 ** -60
+    assert_attention_close((out.float() * 2.0 ** 66).to(torch.bfloat16), want * 2.0 ** 66, cfg.name)  # exact scaling
