@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
-    ap.add_argument("--only", choices=["decode2", "prefill4", "e2e5"],
+    ap.add_argument("--only", choices=["decode2", "prefill4", "e2e5", "handle5"],
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
     ap.add_argument("--unfused", action="store_true",
@@ -305,6 +305,62 @@ def extra_e2e_cfg5(dev, steps: int | None = None, cpu_s: float | None = None) ->
     return res
 
 
+def extra_e2e_cfg5_handle(dev, steps: int | None = None) -> dict:
+    """Config 5 through the dec_* handle (csrc/decoder.hip, the reference's NativeDecoder protocol,
+    inference/decoder.py:194-232): the model and prompts of e2e_cfg5; every prompt admitted (dec_set_prompt, greedy),
+    prefilled by dec_prefill in dec_prefill_rows() rows per call, then `steps` steps of dec_launch_body +
+    dec_launch_head + dec_tokens, the host waiting for each step's tokens as the reference's loop does. The tokens
+    hash the same way as e2e_cfg5's."""
+    import hashlib
+
+    import torch
+
+    from nanochat_amd.decoder import CONFIG5, RandomModel
+    from nanochat_amd.native_decoder import NativeDecoder
+    from nanochat_amd.sampling import slot_masks
+    from nanochat_amd.serving import prompt_rows
+
+    cfg = CONFIG5
+    steps = cfg.steps if steps is None else steps
+    B, P = cfg.batch, cfg.prompt
+    model = RandomModel(cfg.model, dev, seed=cfg.seed)
+    g = torch.Generator(device=dev).manual_seed(cfg.seed + 1)
+    prompts = torch.randint(0, cfg.model.vocab, (B, P), generator=g, device=dev, dtype=torch.int64).to(torch.int32)
+    ids = prompts.cpu().numpy()
+    nd = NativeDecoder(model, bos=-1, max_length=P - 1 + steps, batch=B)
+    lib, h = nd.lib, nd.handle
+    for b in range(B):
+        lib.dec_set_prompt(h, b, int(ids[b, -1]), P - 1, 0.0, 1.0, 0)
+    rows = prompt_rows([(b, ids[b].tolist()) for b in range(B)])
+    words = np.ascontiguousarray(slot_masks([True] * B))
+    out = np.empty(2 * B, dtype=np.int32)
+    toks = np.empty((steps, B), dtype=np.int32)
+    nd.stream.synchronize()
+    t0 = time.perf_counter()
+    for lo in range(0, rows.shape[1], nd.rows_per_call):
+        part = np.ascontiguousarray(rows[:, lo:lo + nd.rows_per_call])
+        lib.dec_prefill(h, part.shape[1], part.ctypes.data)
+    nd.stream.synchronize()
+    t1 = time.perf_counter()
+    lib.dec_set_active(h, words.ctypes.data)
+    for i in range(steps):
+        lib.dec_launch_body(h)
+        lib.dec_launch_head(h)
+        lib.dec_tokens(h, out.ctypes.data)
+        toks[i] = out[:B]
+    t2 = time.perf_counter()
+    pre_s, dec_s = t1 - t0, t2 - t1
+    res = {"workload": cfg.name.replace(f"steps{cfg.steps}", f"steps{steps}") + "-dec-handle",
+           "prefill_calls": -(-rows.shape[1] // nd.rows_per_call), "prefill_s": round(pre_s, 4),
+           "decode_s": round(dec_s, 4), "decode_ms_per_step": round(dec_s / steps * 1e3, 4),
+           "decode_tokens_per_s": round(B * steps / dec_s, 1), "e2e_tokens_per_s": round(B * steps / (pre_s + dec_s), 1),
+           "timing": "host wall clock (the handle's calls are host-synchronous per step, as the reference's loop)",
+           "tokens_sha256": hashlib.sha256(np.ascontiguousarray(toks.T).astype("<i4").tobytes()).hexdigest()[:16]}
+    del nd
+    torch.cuda.empty_cache()
+    return res
+
+
 def torch_empty_like(t):
     import torch
 
@@ -469,7 +525,8 @@ def main():
         s = torch.cuda.Stream(dev)
         cpu_s = None if args.no_cpu else args.cpu_seconds
         run = {"decode2": lambda: extra_decode_cfg2(dev, s, cpu_s), "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
-               "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s)}[args.only]
+               "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s),
+               "handle5": lambda: extra_e2e_cfg5_handle(dev, args.e2e_steps)}[args.only]
         print(json.dumps(run()), flush=True)
         return
     cfg = CONFIG3
@@ -594,6 +651,9 @@ def main():
         result["decode_cfg2"] = extra_decode_cfg2(dev, stream, cpu_s)
         result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream, cpu_s)
         result["e2e_cfg5"] = extra_e2e_cfg5(dev, args.e2e_steps, cpu_s)
+        hd = extra_e2e_cfg5_handle(dev, args.e2e_steps)
+        hd["same_tokens_as_e2e_cfg5"] = hd["tokens_sha256"] == result["e2e_cfg5"]["tokens_sha256"]
+        result["e2e_cfg5_handle"] = hd
     if args.copy_probe:
         copy_probe(dev)
     if cpu_s:

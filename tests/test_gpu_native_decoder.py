@@ -7,9 +7,10 @@ import numpy as np
 import pytest
 import torch
 
-from nanochat_amd.decoder import ModelConfig, RandomModel
+from nanochat_amd.decoder import Fp8Decoder, ModelConfig, RandomModel
 from nanochat_amd.native_decoder import NativeDecoder
-from nanochat_amd.serving import Request
+from nanochat_amd.sampling import slot_masks
+from nanochat_amd.serving import Request, prompt_rows
 from test_gpu_decoder import TINY
 from test_gpu_serving import BOS, check_alone
 
@@ -152,3 +153,38 @@ def test_torch_server_store_at_unaligned_positions(gpu):
     again = dict(server.generate(reqs))
     assert server.loads == 3
     assert again == first
+
+
+def test_handle_tokens_equal_the_torch_decoder(gpu):
+    """The handle and the torch-driven decoder (Fp8Decoder) run the same kernels on the same rows in the same order,
+    so their greedy tokens are bit-identical: 64 prompts of 260 tokens (16576 prefill rows: two dec_prefill calls of
+    at most dec_prefill_rows() rows against one attention call per layer in the torch decoder; the split falls on
+    a tile boundary), then 8 steps driven the way the reference's loop drives them."""
+    model = RandomModel(ModelConfig(layers=2, d_model=256, heads=2, vocab=1000), gpu, seed=23)
+    B, T, steps = 64, 260, 8
+    ids = np.random.default_rng(24).integers(0, 1000, (B, T)).astype(np.int32)
+    prompts = torch.from_numpy(ids).to(gpu)
+    ref = Fp8Decoder(model, B, T - 1 + steps, gpu)
+    ref.prefill(prompts)
+    ref.start(prompts[:, -1], T - 1)
+    ref.run(steps)
+    want = ref.tokens(steps).cpu().numpy()
+    nd = NativeDecoder(model, bos=-1, max_length=T - 1 + steps, batch=B)
+    lib, h = nd.lib, nd.handle
+    for b in range(B):
+        lib.dec_set_prompt(h, b, int(ids[b, -1]), T - 1, 0.0, 1.0, 0)
+    rows = prompt_rows([(b, ids[b].tolist()) for b in range(B)])
+    assert rows.shape[1] > nd.rows_per_call
+    for lo in range(0, rows.shape[1], nd.rows_per_call):
+        part = np.ascontiguousarray(rows[:, lo:lo + nd.rows_per_call])
+        lib.dec_prefill(h, part.shape[1], part.ctypes.data)
+    words = np.ascontiguousarray(slot_masks([True] * B))
+    lib.dec_set_active(h, words.ctypes.data)
+    out = np.empty(2 * B, dtype=np.int32)
+    got = np.empty((steps, B), dtype=np.int32)
+    for i in range(steps):
+        lib.dec_launch_body(h)
+        lib.dec_launch_head(h)
+        lib.dec_tokens(h, out.ctypes.data)
+        got[i] = out[:B]
+    np.testing.assert_array_equal(got.T, want)
