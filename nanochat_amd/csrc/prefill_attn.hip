@@ -36,11 +36,12 @@
  * base, the last wave also the pair's scales; the waves meet at a barrier every PF_BATCH pairs, where the ring's
  * freed slots are refilled. Block ids are staged in LDS per chunk of PF_IDS pages.
  *
- * Software pipeline: iteration k issues the score MFMAs of pair k + 1 and, independent of them, the softmax and
- * the value MFMAs of pair k. A wave's VALU work does not issue under its own MFMAs on gfx950 (measured: an MFMA
- * plus 4 independent v_mul cost their sum), but it does under the other wave's on the same SIMD; the pipeline
- * gives each region both kinds of work so the two waves of a SIMD can fill each other's gaps, and the value MFMA
- * bursts run at raised wave priority (s_setprio 1) so that the other wave's VALU fills them.
+ * Software pipeline: iteration k runs the softmax of pair k (VALU), then one burst of 24 MFMAs at raised wave
+ * priority (s_setprio 1): the scores of pair k + 1 and the values of pair k. A wave's VALU work does not issue
+ * under its own MFMAs on gfx950 (measured: an MFMA plus 4 independent v_mul cost their sum), but it does under the
+ * other wave's on the same SIMD: each wave alternates one VALU stretch and one MFMA stretch, and the two waves of a
+ * SIMD fill each other's. (Scores first, then the softmax, made the softmax wait out its own wave's score MFMAs:
+ * config 4 8-12 % slower.)
  *
  * Compiled without IEEE mode and NaN semantics (build.py): the maxima of the lazy-max and scale checks need no
  * NaN-quieting canonicalisations then (2-5 % faster, same bits on finite inputs).
@@ -315,7 +316,6 @@ __device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32
                                                      k.a1[3]});
     const i32x8 kb = __builtin_bit_cast(i32x8, u32x8{k.b0[0], k.b0[1], k.b0[2], k.b0[3], k.b1[0], k.b1[1], k.b1[2],
                                                      k.b1[3]});
-    __builtin_amdgcn_s_setprio(1); /* MFMA bursts issue ahead of the other wave's VALU, which fills their cycles */
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -324,13 +324,14 @@ __device__ __forceinline__ void pair_scores(const PfKeys &k, const PfQ8 *q8, f32
         s[bl][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, q8[bl].lo, sa, 0, 0, 0, 127, 0, q8[bl].scale);
         s[bl][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kb, q8[bl].lo, sb, 0, 0, 0, 127, 0, q8[bl].scale);
     }
-    __builtin_amdgcn_s_setprio(0);
 }
 
-/* Softmax and value MFMAs of a pair whose scores are s (keys of pages page0, page0 + 1 with blocks ida, idb) and
- * whose values and scales are v. t = s k_scale score_scale - m + lw, so exp2(t) = p w. */
-__device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const f32x4 (*s)[2], const PfVals &v,
-                                                    int ida, int idb, int page0, const PfCols &c, int j, PfState &st) {
+/* Softmax of a pair whose scores are s (keys of pages page0, page0 + 1 with blocks ida, idb) and whose scales are
+ * v's: t = s k_scale score_scale - m + lw, so exp2(t) = p w; pp receives Pᵀ = p w v_scale in fp16, the value MFMAs'
+ * B operand. */
+__device__ __forceinline__ void pair_softmax(const PrefillArgs &a, const f32x4 (*s)[2], const PfVals &v, int ida,
+                                             int idb, int page0, const PfCols &c, int j, PfState &st,
+                                             f16x8 (&pp)[PF_BLOCKS]) {
     float ksc[8], vs[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -416,7 +417,6 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
         st.e_ref = e_new;
         st.vlim = pf_exp2i(min(e_new - 126, 127));
     }
-    f16x8 pp[PF_BLOCKS];
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         float p[8];
@@ -426,7 +426,10 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
 #pragma unroll
         for (int i = 0; i < 8; i++) pp[bl][i] = (_Float16)(p[i] * vs[i]);
     }
-    __builtin_amdgcn_s_setprio(1);
+}
+
+/* The value MFMAs of a pair: Oᵀ += Vᵀ Pᵀ, V's fp8 codes converted exactly to fp16. */
+__device__ __forceinline__ void pair_values(const PfVals &v, const f16x8 (&pp)[PF_BLOCKS], PfState &st) {
 #pragma unroll
     for (int bb = 0; bb < 8; bb++) {
         const uint32_t wa = bb < 4 ? v.a0[bb] : v.a1[bb - 4];
@@ -436,7 +439,6 @@ __device__ __forceinline__ void pair_softmax_values(const PrefillArgs &a, const 
         for (int bl = 0; bl < PF_BLOCKS; bl++)
             st.o[bl][bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pp[bl], st.o[bl][bb], 0, 0, 0);
     }
-    __builtin_amdgcn_s_setprio(0);
 }
 
 __device__ __forceinline__ bool row_valid(const PrefillArgs &a, int p, int s) {
@@ -629,9 +631,16 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                            min(k + 1, npairs - 1), min(k + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
                 __builtin_amdgcn_sched_barrier(0);
                 if (c.active) {
-                    pair_scores(kf, q8, s_next); /* pair k + 1 (past the end: the clamped refill, unused) */
-                    pair_softmax_values(a, s_cur, vf, __builtin_amdgcn_readfirstlane((int)ids_cur[0]),
-                                        __builtin_amdgcn_readfirstlane((int)ids_cur[1]), first + cb + 2 * k, c, j, st);
+                    /* the softmax of pair k, then all of the step's MFMAs in one burst at raised priority: the
+                     * scores of pair k + 1 (past the end: the clamped refill, unused) and the values of pair k */
+                    f16x8 pp[PF_BLOCKS];
+                    pair_softmax(a, s_cur, vf, __builtin_amdgcn_readfirstlane((int)ids_cur[0]),
+                                 __builtin_amdgcn_readfirstlane((int)ids_cur[1]), first + cb + 2 * k, c, j, st, pp);
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_setprio(1);
+                    pair_scores(kf, q8, s_next);
+                    pair_values(vf, pp, st);
+                    __builtin_amdgcn_s_setprio(0);
                 }
                 ids_cur = ids_next;
                 __builtin_amdgcn_sched_barrier(0);
