@@ -204,32 +204,40 @@ __device__ __forceinline__ void read_keys(const unsigned char *slot_k, const int
         : "memory");
 }
 
-/* As read_keys, plus the values and both scales of slot_v (the pair whose softmax and value MFMAs run this
- * iteration). */
-__device__ __forceinline__ void read_stage(const unsigned char *slot_v, const unsigned char *slot_k, const int *ids,
-                                           int pair_k, int pair_dma, int lane, PfVals &v, PfKeys &k, u32x2 &ids_k,
-                                           u32x2 &ids_dma) {
-    const uint32_t mv = lds_addr(slot_v) + 16 * lane, sv = lds_addr(slot_v) + PF_SLOT_SCALES + 16 * (lane >> 4);
-    const uint32_t mk = lds_addr(slot_k) + 16 * lane;
+/* The scales of slot_v (the pair whose softmax runs this step) and two pairs' block ids: what the softmax reads. */
+__device__ __forceinline__ void read_scales(const unsigned char *slot_v, const int *ids, int pair_k, int pair_dma,
+                                            int lane, PfVals &v, u32x2 &ids_k, u32x2 &ids_dma) {
+    const uint32_t sv = lds_addr(slot_v) + PF_SLOT_SCALES + 16 * (lane >> 4);
     asm volatile(
-        "ds_read_b128 %0, %14\n"
-        "ds_read_b128 %1, %14 offset:1024\n"
-        "ds_read_b128 %2, %14 offset:4096\n"
-        "ds_read_b128 %3, %14 offset:5120\n"
-        "ds_read_b64 %12, %15\n"
-        "ds_read_b64 %13, %16\n"
-        "ds_read_b128 %4, %17 offset:2048\n"
-        "ds_read_b128 %5, %17 offset:3072\n"
-        "ds_read_b128 %6, %17 offset:6144\n"
-        "ds_read_b128 %7, %17 offset:7168\n"
-        "ds_read_b128 %8, %18\n"
-        "ds_read_b128 %9, %18 offset:128\n"
-        "ds_read_b128 %10, %18 offset:64\n"
-        "ds_read_b128 %11, %18 offset:192\n"
+        "ds_read_b128 %0, %6\n"
+        "ds_read_b128 %1, %6 offset:128\n"
+        "ds_read_b128 %2, %6 offset:64\n"
+        "ds_read_b128 %3, %6 offset:192\n"
+        "ds_read_b64 %4, %7\n"
+        "ds_read_b64 %5, %8\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k.a0), "=&v"(k.a1), "=&v"(k.b0), "=&v"(k.b1), "=&v"(v.a0), "=&v"(v.a1), "=&v"(v.b0), "=&v"(v.b1),
-          "=&v"(v.ks_a), "=&v"(v.ks_b), "=&v"(v.vs_a), "=&v"(v.vs_b), "=&v"(ids_k), "=&v"(ids_dma)
-        : "v"(mk), "v"(lds_addr(ids + 2 * pair_k)), "v"(lds_addr(ids + 2 * pair_dma)), "v"(mv), "v"(sv)
+        : "=&v"(v.ks_a), "=&v"(v.ks_b), "=&v"(v.vs_a), "=&v"(v.vs_b), "=&v"(ids_k), "=&v"(ids_dma)
+        : "v"(sv), "v"(lds_addr(ids + 2 * pair_k)), "v"(lds_addr(ids + 2 * pair_dma))
+        : "memory");
+}
+
+/* The value fragments of slot_v and the key fragments of slot_k: what the step's MFMA burst reads. Read after the
+ * softmax, so the fragments are not live across it. */
+__device__ __forceinline__ void read_frags(const unsigned char *slot_v, const unsigned char *slot_k, int lane,
+                                           PfVals &v, PfKeys &k) {
+    const uint32_t mv = lds_addr(slot_v) + 16 * lane, mk = lds_addr(slot_k) + 16 * lane;
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:4096\n"
+        "ds_read_b128 %3, %8 offset:5120\n"
+        "ds_read_b128 %4, %9 offset:2048\n"
+        "ds_read_b128 %5, %9 offset:3072\n"
+        "ds_read_b128 %6, %9 offset:6144\n"
+        "ds_read_b128 %7, %9 offset:7168\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k.a0), "=&v"(k.a1), "=&v"(k.b0), "=&v"(k.b1), "=&v"(v.a0), "=&v"(v.a1), "=&v"(v.b0), "=&v"(v.b1)
+        : "v"(mk), "v"(mv)
         : "memory");
 }
 
@@ -627,8 +635,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                 }
                 PfVals vf;
                 u32x2 ids_next;
-                read_stage(ring + (k % PF_RING) * PF_PAIR_BYTES, ring + ((k + 1) % PF_RING) * PF_PAIR_BYTES, ids,
-                           min(k + 1, npairs - 1), min(k + 1, npairs - 1), lane, vf, kf, ids_next, ids_dma);
+                read_scales(ring + (k % PF_RING) * PF_PAIR_BYTES, ids, min(k + 1, npairs - 1), min(k + 1, npairs - 1),
+                            lane, vf, ids_next, ids_dma);
                 __builtin_amdgcn_sched_barrier(0);
                 if (c.active) {
                     /* the softmax of pair k, then all of the step's MFMAs in one burst at raised priority: the
@@ -636,6 +644,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                     f16x8 pp[PF_BLOCKS];
                     pair_softmax(a, s_cur, vf, __builtin_amdgcn_readfirstlane((int)ids_cur[0]),
                                  __builtin_amdgcn_readfirstlane((int)ids_cur[1]), first + cb + 2 * k, c, j, st, pp);
+                    __builtin_amdgcn_sched_barrier(0);
+                    read_frags(ring + (k % PF_RING) * PF_PAIR_BYTES, ring + ((k + 1) % PF_RING) * PF_PAIR_BYTES, lane,
+                               vf, kf);
                     __builtin_amdgcn_sched_barrier(0);
                     __builtin_amdgcn_s_setprio(1);
                     pair_scores(kf, q8, s_next);
