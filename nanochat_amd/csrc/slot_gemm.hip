@@ -11,9 +11,12 @@
  *     arrive by global_load_lds_dwordx4 (8 whole rows per instruction), shared evenly by the 4 waves, at a swizzled
  *     position so the fragment reads (ds_read_b128) are bank-conflict free;
  *   - the 4 waves split the tile as WN x 4 / WN over W rows and batch rows and multiply with
- *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles); per chunk a wave waits for its own DMAs,
- *     meets the others at one barrier, refills the slot everyone has finished, reads the next chunk's fragments
- *     while this chunk's MFMAs run, and settles them;
+ *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles); per step a wave waits for its own DMAs,
+ *     meets the others at one barrier, refills the slots everyone has finished, reads the next chunk's fragments
+ *     while this chunk's MFMAs run, and settles them. A step covers two chunks where the ring is 6 or more slots
+ *     deep: the loop is bound by each step's chain of waits (barrier, LDS round trip), not by LDS or L2 bandwidth
+ *     (per-workgroup timestamps: 3 % of the loop in DMA waits; counters: LDS busy under half the time, no bank
+ *     conflicts), and halving the steps makes the decode-step GEMMs 4-16 % faster with the same bits;
  *   - the RMS norm of the input rows is fused: the same x fragments feed one more MFMA per 16 rows, x·xᵀ, whose
  *     diagonal is Σ x² of each row, so r = 1 / sqrt(Σ x² / K + FLT_EPSILON) (model/modeling.py:47-49, decode.cu:448-456)
  *     scales the sums in the epilogue instead of a separate normalised copy of x (the reference's RELU2 epilogue,
@@ -31,6 +34,8 @@
 #define SG_WAVES 4
 #define SG_CHUNK 64                 /* K columns per ring slot: 128 bytes of every row */
 #define SG_LDS_BUDGET (128 * 1024) /* ring bytes per workgroup */
+#define SG_MAX_DEPTH 8             /* ring slots: deeper rings measured no faster */
+#define SG_GROUP 2                 /* chunks per barrier where the ring is deep enough: 2 measured faster than 1 and 4 */
 
 enum { SG_STORE = 0, SG_NORM_STORE = 1, SG_RESID = 2, SG_RELU2_NORM = 3, SG_NORM_F32 = 4 };
 
@@ -59,8 +64,10 @@ __host__ __device__ constexpr int sg_waves_n(int nt, int mt) {
 /* Ring geometry of an NT x MT tile: a slot holds the chunk's NT W rows then MT x rows, 128 bytes each. */
 __host__ __device__ constexpr int sg_slot_bytes(int nt, int mt) { return (nt + mt) * 128; }
 __host__ __device__ constexpr int sg_depth(int nt, int mt) {
-    return SG_LDS_BUDGET / sg_slot_bytes(nt, mt) > 8 ? 8 : SG_LDS_BUDGET / sg_slot_bytes(nt, mt);
+    return SG_LDS_BUDGET / sg_slot_bytes(nt, mt) > SG_MAX_DEPTH ? SG_MAX_DEPTH : SG_LDS_BUDGET / sg_slot_bytes(nt, mt);
 }
+/* Chunks per barrier: G (even, or 1) with D >= 2 G + 2, so the ring keeps at least 2 chunks in flight past a step. */
+__host__ __device__ constexpr int sg_group(int d) { return d >= 2 * SG_GROUP + 2 ? SG_GROUP : (d >= 6 ? 2 : 1); }
 
 template <int N> __device__ __forceinline__ void sg_wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
@@ -96,7 +103,7 @@ __device__ __forceinline__ void sg_dma(const unsigned char *const *src, size_t o
 template <int NT, int MT, int EPI>
 __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
     constexpr int ROWS = NT + MT, DMAS = ROWS / 8, DPW = DMAS / SG_WAVES; /* DMA instructions per chunk, per wave */
-    constexpr int SLOT = sg_slot_bytes(NT, MT), D = sg_depth(NT, MT);
+    constexpr int SLOT = sg_slot_bytes(NT, MT), D = sg_depth(NT, MT), G = sg_group(D);
     constexpr int WN = sg_waves_n(NT, MT), WM = SG_WAVES / WN; /* waves over W rows x batch rows */
     constexpr int TNW = NT / 16 / WN, TMW = MT / 16 / WM;     /* 16x16 tiles per wave */
     constexpr int TSQ = (TMW + WN - 1) / WN; /* batch tiles whose Σ x² this wave computes (shared with its row) */
@@ -213,17 +220,52 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-#pragma unroll
-    for (int c = 0; c < D; c++) dma(c, c); /* chunks 0..D-1 in flight (the slot of chunk D is that of chunk 0) */
-    sg_wait_vmcnt<DPW * (D - 1)>();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
     bf16x8 wa[TNW][2], xa[TMW][2], wb[TNW][2], xb[TMW][2];
-    read(0, wa, xa);
-    settle(wa, xa);
-    for (int c = 0; c < chunks; c += 2) {
-        step(c, wa, xa, wb, xb);
-        if (c + 1 < chunks) step(c + 1, wb, xb, wa, xa);
+    if (G > 1 && chunks % 2 == 0) {
+        /* G chunks per barrier (fewer barriers and waits, the same MFMAs in the same order): step c (a multiple of
+         * G) multiplies chunks c..c+G-1 and reads c+1..c+G, once everyone's DMAs of those have landed and everyone
+         * has settled its reads of chunks c-G+1..c, whose slots then take chunks c-G+1+D..c+D. The slots of chunks
+         * D-G+1..D-1 start empty. The last step may hold fewer than G chunks (pairs past the end are skipped; their
+         * reads and waits stay inside the branch). */
+#pragma unroll
+        for (int c = 0; c <= D - G; c++) dma(c, c);
+        sg_wait_vmcnt<DPW * (D - G)>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        read(0, wa, xa);
+        settle(wa, xa);
+        for (int c = 0; c < chunks; c += G) {
+            sg_wait_vmcnt<DPW * (D - 2 * G)>(); /* this wave's DMAs of chunks c + 1..c + G have landed */
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 1; i <= G; i++) dma(c - G + i + D, (c - G + i + D) % D);
+#pragma unroll
+            for (int i = 0; i < G; i += 2) {
+                if (i == 0 || c + i < chunks) {
+                    read(c + i + 1, wb, xb);
+                    multiply(wa, xa);
+                    settle(wb, xb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    read(min(c + i + 2, chunks - 1), wa, xa);
+                    multiply(wb, xb);
+                    settle(wa, xa);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < D; c++) dma(c, c); /* chunks 0..D-1 in flight (the slot of chunk D is that of chunk 0) */
+        sg_wait_vmcnt<DPW * (D - 1)>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        read(0, wa, xa);
+        settle(wa, xa);
+        for (int c = 0; c < chunks; c += 2) {
+            step(c, wa, xa, wb, xb);
+            if (c + 1 < chunks) step(c + 1, wb, xb, wa, xa);
+        }
     }
     sg_wait_vmcnt<0>(); /* the clamped refills past the last chunk land before the ring is reused or released */
 

@@ -54,6 +54,7 @@ def check(got, want, label):
     (128, 1664, 6656),   # down
     (1, 32, 64),
     (5, 64, 64),
+    (9, 96, 128),        # two chunks: fewer than the ring holds
     (37, 224, 192),
     (200, 96, 320),
 ])
