@@ -53,67 +53,111 @@ struct AppendArgs {
     int fused;                /* 1: norm + rope q and k, write q_out; 0: store rows as given */
 };
 
-/* One 8-lane item per (row, head). Fused: heads [0, hq) are q, [hq, hq + hkv) k, then v. Store: [0, hkv) k,
- * then v. A row whose position, sequence or page is out of range writes no cache byte; its q_out row is NaN. */
+/* The 4 x 4 byte transpose of a quad's V codes: lane r of 4 items (8 lanes apart) holds dword w = bytes of dims
+ * 4c..4c+3 of token r; it returns the dword of dim 4c + r over tokens 0..3 (the quad-transposed layout), in two
+ * exchanges (partner r ^ 2, then r ^ 1). */
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t w, int r) {
+    const uint32_t x = (uint32_t)__shfl_xor((int)w, 16, NC_WAVE);
+    const uint32_t w1 = r < 2 ? (w & 0xffffu) | (x << 16) : (x >> 16) | (w & 0xffff0000u);
+    const uint32_t y = (uint32_t)__shfl_xor((int)w1, 8, NC_WAVE);
+    return (r & 1) ? ((y >> 8) & 0x00ff00ffu) | (w1 & 0xff00ff00u) : (w1 & 0x00ff00ffu) | ((y & 0x00ff00ffu) << 8);
+}
+
+/* Items are (row quad, head, row r within the quad), 8 lanes each (qk_row.h). Fused: heads [0, hq) are q,
+ * [hq, hq + hkv) k, then v. Store: [0, hkv) k, then v. The 4 rows of a quad sit in 4 consecutive items of one wave
+ * (lanes 8 r + lane % 8 of a 32-lane half), so when they are the 4 positions of one quad of one page, in order (a
+ * prefill's rows), their V codes are transposed between the items and written as dwords instead of bytes. A row
+ * whose position, sequence or page is out of range writes no cache byte; its q_out row is NaN. */
 __global__ void __launch_bounds__(APPEND_THREADS) k_append(AppendArgs a) {
     const int heads = a.fused ? a.hq + 2 * a.hkv : 2 * a.hkv;
     const long long item = (long long)blockIdx.x * ITEMS_PER_BLOCK + threadIdx.x / NC_ROW_LANES;
-    if (item >= (long long)a.n * heads) return;  /* whole 8-lane groups leave together */
-    const int g = threadIdx.x % NC_ROW_LANES;
-    const int row = (int)(item / heads), head = (int)(item % heads);
-    const int p = a.pos[row], s = a.seq[row];
-    if (a.ctx_out && head == 0 && g == 0) a.ctx_out[row] = p + 1; /* never aliases pos (host check) */
-    bool ok = p >= 0 && s >= 0 && s < a.num_seqs;
-    if (a.fused) ok = ok && p < a.rope_len;
-    const int blk = ok ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, s, p / NC_PAGE) : -1;
+    if (item >= (((long long)a.n + 3) / 4) * heads * 4) return; /* whole quads of items leave together */
+    const int g = threadIdx.x % NC_ROW_LANES, r = (int)(item & 3);
+    const int head = (int)((item >> 2) % heads), row = (int)((item >> 2) / heads) * 4 + r;
+    const bool live = row < a.n;
+    const int rowc = live ? row : a.n - 1; /* a quad's rows past n load row n - 1 and write nothing */
 
     const bool is_q = a.fused && head < a.hq;
     const int kv = a.fused ? head - a.hq : head; /* [0, hkv) k, [hkv, 2 hkv) v */
     const bool is_v = !is_q && kv >= a.hkv;
     const int h = is_v ? kv - a.hkv : kv;
 
-    if (is_q && !ok) {
-        const u32x4 nan = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
-        bf16_t *y = a.q_out + ((size_t)row * a.hq + head) * NC_HEAD_DIM;
-        *reinterpret_cast<u32x4 *>(y + 8 * g) = nan;
-        *reinterpret_cast<u32x4 *>(y + NC_HALF + 8 * g) = nan;
-        return;
-    }
-    if (!is_q && blk < 0) return;
-
+    /* the row's 256 bytes first: their round trip overlaps the position and page lookups */
     const bf16_t *x;
     if (a.fused)
-        x = a.qkv + (size_t)row * a.row_stride + (size_t)head * NC_HEAD_DIM;
+        x = a.qkv + (size_t)rowc * a.row_stride + (size_t)head * NC_HEAD_DIM;
     else
-        x = (is_v ? a.v_rows : a.k_rows) + (size_t)row * a.row_stride + (size_t)h * NC_HEAD_DIM;
+        x = (is_v ? a.v_rows : a.k_rows) + (size_t)rowc * a.row_stride + (size_t)h * NC_HEAD_DIM;
     float x1[8], x2[8];
     load_bf16x8(x + 8 * g, x1);
     load_bf16x8(x + NC_HALF + 8 * g, x2);
 
-    if (a.fused && !is_v) {
-        const float *gain = is_q ? a.q_gain : a.k_gain;
-        float g1[8], g2[8], c[8], sn[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            g1[e] = gain[8 * g + e];
-            g2[e] = gain[NC_HALF + 8 * g + e];
-            c[e] = a.cos[(size_t)p * NC_HALF + 8 * g + e];
-            sn[e] = a.sin[(size_t)p * NC_HALF + 8 * g + e];
+    const int p = a.pos[rowc], s = a.seq[rowc];
+    if (live && a.ctx_out && head == 0 && g == 0) a.ctx_out[row] = p + 1; /* never aliases pos (host check) */
+    bool ok = live && p >= 0 && s >= 0 && s < a.num_seqs;
+    if (a.fused) ok = ok && p < a.rope_len;
+    const int blk = ok ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, s, p / NC_PAGE) : -1;
+    const int t = p % NC_PAGE;
+
+    if (!is_v) {
+        if (is_q && !live) return;
+        if (is_q && !ok) {
+            const u32x4 nan = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+            bf16_t *y = a.q_out + ((size_t)row * a.hq + head) * NC_HEAD_DIM;
+            *reinterpret_cast<u32x4 *>(y + 8 * g) = nan;
+            *reinterpret_cast<u32x4 *>(y + NC_HALF + 8 * g) = nan;
+            return;
         }
-        row_norm_rope(x1, x2, g1, g2, c, sn);
-    }
-    if (is_q) {
-        bf16_t *y = a.q_out + ((size_t)row * a.hq + head) * NC_HEAD_DIM;
-        store_bf16x8(y + 8 * g, x1);
-        store_bf16x8(y + NC_HALF + 8 * g, x2);
+        if (!is_q && blk < 0) return;
+        if (a.fused) {
+            const float *gain = is_q ? a.q_gain : a.k_gain;
+            float g1[8], g2[8], c[8], sn[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                g1[e] = gain[8 * g + e];
+                g2[e] = gain[NC_HALF + 8 * g + e];
+                c[e] = a.cos[(size_t)p * NC_HALF + 8 * g + e];
+                sn[e] = a.sin[(size_t)p * NC_HALF + 8 * g + e];
+            }
+            row_norm_rope(x1, x2, g1, g2, c, sn);
+        }
+        if (is_q) {
+            bf16_t *y = a.q_out + ((size_t)row * a.hq + head) * NC_HEAD_DIM;
+            store_bf16x8(y + 8 * g, x1);
+            store_bf16x8(y + NC_HALF + 8 * g, x2);
+            return;
+        }
+        uint64_t c1, c2;
+        const float scale = row_quantize(x1, x2, &c1, &c2);
+        uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
+        write_codes(tile, t, g, c1, c2, false);
+        if (g == 0) reinterpret_cast<float *>(tile + NC_TILE_KS)[t] = scale;
         return;
     }
+
+    /* v: every item of the quad is here (one head per quad), so the exchanges below see all four */
     uint64_t c1, c2;
     const float scale = row_quantize(x1, x2, &c1, &c2);
-    const int t = p % NC_PAGE;
+    const int qb = blk >= 0 && (p & 3) == r ? blk : -1, qp = p >> 2; /* the quad is whole: same block and quad */
+    const int lo_b = min(min(qb, __shfl_xor(qb, 8, NC_WAVE)), __shfl_xor(min(qb, __shfl_xor(qb, 8, NC_WAVE)), 16, NC_WAVE));
+    const int hi_b = max(max(qb, __shfl_xor(qb, 8, NC_WAVE)), __shfl_xor(max(qb, __shfl_xor(qb, 8, NC_WAVE)), 16, NC_WAVE));
+    const int lo_p = min(min(qp, __shfl_xor(qp, 8, NC_WAVE)), __shfl_xor(min(qp, __shfl_xor(qp, 8, NC_WAVE)), 16, NC_WAVE));
+    const int hi_p = max(max(qp, __shfl_xor(qp, 8, NC_WAVE)), __shfl_xor(max(qp, __shfl_xor(qp, 8, NC_WAVE)), 16, NC_WAVE));
+    const uint32_t d0 = quad_transpose((uint32_t)c1, r), d1 = quad_transpose((uint32_t)(c1 >> 32), r);
+    const uint32_t d2 = quad_transpose((uint32_t)c2, r), d3 = quad_transpose((uint32_t)(c2 >> 32), r);
+    if (blk < 0) return;
     uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
-    write_codes(tile, t, g, c1, c2, is_v);
-    if (g == 0) reinterpret_cast<float *>(tile + (is_v ? NC_TILE_VS : NC_TILE_KS))[t] = scale;
+    if (lo_b >= 0 && lo_b == hi_b && lo_p == hi_p) {
+        /* dims 8g + r, 8g + 4 + r and their partners 64 apart: one dword of 4 keys each */
+        uint32_t *v = reinterpret_cast<uint32_t *>(tile + NC_TILE_V + (t >> 2) * 512);
+        v[8 * g + r] = d0;
+        v[8 * g + 4 + r] = d1;
+        v[NC_HALF + 8 * g + r] = d2;
+        v[NC_HALF + 8 * g + 4 + r] = d3;
+    } else {
+        write_codes(tile, t, g, c1, c2, true);
+    }
+    if (g == 0) reinterpret_cast<float *>(tile + NC_TILE_VS)[t] = scale;
 }
 
 static int check_cache_args(int n, int hkv, int max_blocks, int num_blocks, int num_seqs, const void *cache,
@@ -131,7 +175,7 @@ static int check_cache_args(int n, int hkv, int max_blocks, int num_blocks, int 
 
 static void launch_append(const AppendArgs &a, hipStream_t stream) {
     const int heads = a.fused ? a.hq + 2 * a.hkv : 2 * a.hkv;
-    const long long items = (long long)a.n * heads;
+    const long long items = (((long long)a.n + 3) / 4) * heads * 4; /* whole quads of rows */
     if (items == 0) return;
     const unsigned blocks = (unsigned)((items + ITEMS_PER_BLOCK - 1) / ITEMS_PER_BLOCK);
     hipLaunchKernelGGL(k_append, dim3(blocks), dim3(APPEND_THREADS), 0, stream, a);

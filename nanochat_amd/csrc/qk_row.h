@@ -52,8 +52,9 @@ __device__ __forceinline__ void row_norm_rope(float *x1, float *x2, const float 
 
 /* Per-(token, kv head) absmax quantisation of this lane's 16 values of the row: returns the row's scale
  * (max|x| / 448, one correctly rounded division) and writes the lane's e4m3fn codes, 8 per 64-bit word:
- * c1 = dims [8g, 8g+8), c2 = dims [64+8g, 64+8g+8), byte e = dim 8g+e. A zero row gives scale 0 and codes 0. */
-__device__ __forceinline__ float row_quantize(const float *x1, const float *x2, uint64_t *c1, uint64_t *c2) {
+ * c1 = dims [8g, 8g+8), c2 = dims [64+8g, 64+8g+8), byte e = dim 8g+e. A zero row gives scale 0 and codes 0.
+ * Each code is the e4m3fn rounding (nearest, ties to even) of the correctly rounded quotient x / scale. */
+__device__ __forceinline__ float row_quantize_exact(const float *x1, const float *x2, uint64_t *c1, uint64_t *c2) {
 #pragma clang fp contract(off)
     float a = 0.0f;
 #pragma unroll
@@ -72,5 +73,46 @@ __device__ __forceinline__ float row_quantize(const float *x1, const float *x2, 
     }
     *c1 = w1;
     *c2 = w2;
+    return scale;
+}
+
+/* x / scale for |x| <= 448 scale, scale a normal number: r = 1 / scale correctly rounded, q0 = x r, and one FMA
+ * correction q0 + (x - q0 scale) r, which is the correctly rounded quotient (Markstein's theorem: r within half an
+ * ulp of 1 / scale, q0 within an ulp of the quotient, the residual exact by FMA); the sign restores -0 / scale. */
+__device__ __forceinline__ float quotient(float x, float scale, float r) {
+#pragma clang fp contract(off)
+    const float q0 = x * r;
+    return __builtin_copysignf(fmaf(fmaf(-q0, scale, x), r, q0), x);
+}
+
+/* Four codes of the hardware e4m3fn conversion, which rounds like f32_to_e4m3 for every non-NaN input. */
+__device__ __forceinline__ uint32_t e4m3x4(float q0, float q1, float q2, float q3) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q2, q3, __builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false), true);
+}
+
+/* row_quantize_exact's results with one division per lane instead of 16 and hardware conversions: for a row of
+ * finite values whose scale is a normal number every quotient is x / scale bit for bit and finite (so the
+ * conversion never sees a NaN); other rows (a NaN or infinity, a subnormal scale) take row_quantize_exact. The
+ * row's max |x| is the integer maximum of the magnitudes' bit patterns, which orders finite floats. */
+__device__ __forceinline__ float row_quantize(const float *x1, const float *x2, uint64_t *c1, uint64_t *c2) {
+#pragma clang fp contract(off)
+    uint32_t m = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        m = max(m, max(__float_as_uint(x1[e]) & 0x7fffffffu, __float_as_uint(x2[e]) & 0x7fffffffu));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 4, NC_WAVE));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 2, NC_WAVE));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 1, NC_WAVE));
+    const float scale = __uint_as_float(m) / NC_FP8_MAX; /* not used when m is not finite */
+    if (m >= 0x7f800000u || scale < 0x1p-126f) return row_quantize_exact(x1, x2, c1, c2);
+    const float r = 1.0f / scale;
+    float q1[8], q2[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        q1[e] = quotient(x1[e], scale, r);
+        q2[e] = quotient(x2[e], scale, r);
+    }
+    *c1 = e4m3x4(q1[0], q1[1], q1[2], q1[3]) | (uint64_t)e4m3x4(q1[4], q1[5], q1[6], q1[7]) << 32;
+    *c2 = e4m3x4(q2[0], q2[1], q2[2], q2[3]) | (uint64_t)e4m3x4(q2[4], q2[5], q2[6], q2[7]) << 32;
     return scale;
 }

@@ -66,6 +66,34 @@ def test_append_bit_exact(gpu, name, B, rows, start, hq, hkv, theta, layout):
     assert_same_cache(cache, ref)
 
 
+def test_append_rows_in_any_order(gpu):
+    """Rows of two sequences in an order that keeps some position quads whole and in order (their V codes are
+    written as dwords) and breaks others (reversed, split, or the partial last quad): the cache bytes are the
+    oracle's either way."""
+    dev = gpu
+    hq, hkv, rows = 4, 2, 42
+    cache = make_cache("paged", 2, 48, hkv, dev, seed=31)
+    random_bytes(cache, 32)
+    ref = oracle_cache(cache)
+    order = np.arange(2 * rows)
+    order[4:8], order[8:12] = np.arange(8, 12), np.arange(4, 8)  # two whole quads swapped
+    order[12:16] = order[12:16][::-1]                             # a quad reversed
+    order[20:30] = order[20:30][np.random.default_rng(3).permutation(10)]
+    pos = torch.from_numpy(np.tile(np.arange(rows), 2)[order].astype(np.int32)).to(dev)
+    seq = torch.from_numpy(np.repeat(np.arange(2), rows)[order].astype(np.int32)).to(dev)
+    qkv = seeded_normal((2 * rows, (hq + 2 * hkv) * 128), 33, dev)
+    g = torch.Generator().manual_seed(34)
+    q_gain, k_gain = (0.5 + torch.rand(128, generator=g)).to(dev), (0.5 + torch.rand(128, generator=g)).to(dev)
+    cos, sin = rotary_tables(48, 1e4, dev)
+    q = cache.append(qkv, pos, seq, q_gain, k_gain, cos, sin, hq)
+    torch.cuda.synchronize()
+    q_ref = G.append(ref, bits(qkv), pos.cpu().numpy(), seq.cpu().numpy(), q_gain.cpu().numpy(),
+                     k_gain.cpu().numpy(), cos.cpu().numpy(), sin.cpu().numpy(), hq, hkv, table(cache),
+                     cache.max_blocks)
+    np.testing.assert_array_equal(bits(q), q_ref)
+    assert_same_cache(cache, ref)
+
+
 def test_append_rows_out_of_range_write_nothing(gpu):
     dev = gpu
     hq, hkv = 4, 2
