@@ -143,6 +143,43 @@ def test_store_bit_exact(gpu, layout):
     assert_same_cache(cache, ref)
 
 
+def test_store_scale_extremes_bit_exact(gpu):
+    """Rows whose absmax puts the scale below the normal range (the per-value division path), just above it and
+    near the top of the fp32 range (the reciprocal path, where every quotient must still be x / scale rounded
+    once), and rows with exact ties of the e4m3 rounding: the codes and scales are the oracle's bit for bit."""
+    dev = gpu
+    hkv, B, L = 2, 2, 48
+    cache = make_cache("paged", B, 48, hkv, dev, seed=41)
+    random_bytes(cache, 42)
+    ref = oracle_cache(cache)
+    n = B * L
+    g = torch.Generator(device=dev).manual_seed(43)
+    base = torch.randn((n, hkv * 128), generator=g, device=dev)
+    mags = torch.tensor([1e-39, 3e-38, 1e-37, 1.5e-36, 1.8e-36, 2.2e-36, 1e-30, 1.0, 3e20, 1e37, 5e37], device=dev)
+    k = (base * mags[torch.arange(n, device=dev) % len(mags)][:, None]).to(torch.bfloat16)
+    v = (base.flip(0) * mags.flip(0)[torch.arange(n, device=dev) % len(mags)][:, None]).to(torch.bfloat16)
+    # ties: absmax 28 makes scale 1/16 exactly, and x / scale = 16 x lands on e4m3 midpoints (17 between 16 and 18,
+    # 34 between 32 and 36, ..., 2^-10 and 3 2^-10 between subnormal steps), each rounded to the even neighbour
+    mids = torch.tensor([28.0 * 16, 17, 19, 21, 23, 8.5, 9.5, 34, 38, 68, 76, 136, 152, 272, 304, 2 ** -10,
+                         3 * 2 ** -10, 5 * 2 ** -10], device=dev) / 16
+    row = mids[torch.arange(128, device=dev) % len(mids)] * (1 - 2 * (torch.arange(128, device=dev) % 2))
+    row[0] = 28.0
+    k[3, :128] = row.to(torch.bfloat16)
+    v[4, 128:] = row.flip(0).to(torch.bfloat16)
+    pos = torch.from_numpy(np.tile(np.arange(L), B).astype(np.int32)).to(dev)
+    seq = torch.from_numpy(np.repeat(np.arange(B), L).astype(np.int32)).to(dev)
+    cache.store(k, v, pos, seq)
+    torch.cuda.synchronize()
+    kc, ks = G.quantize_rows(bits(k).reshape(n, hkv, 128))
+    vc, vs = G.quantize_rows(bits(v).reshape(n, hkv, 128))
+    assert (ks[ks > 0] < 2.0 ** -126).any() and (vs > 1e34).any()  # both paths are exercised
+    blk = G.PagedCache.block_of(seq.cpu().numpy(), pos.cpu().numpy(), table(cache), cache.max_blocks)
+    t = pos.cpu().numpy() % 16
+    for h in range(hkv):
+        ref.write(blk, h, t, kc[:, h], ks[:, h], vc[:, h], vs[:, h])
+    assert_same_cache(cache, ref)
+
+
 def test_qkp_forward_bit_exact(gpu):
     """The training-layout prologue (model/ops/qk_prologue.py:13-21 surface) against the oracle's row math."""
     dev = gpu
