@@ -336,10 +336,12 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
  * row does not depend on M, on the tile, or on which of the two kernels ran.
  *
  * K is walked in 64-column chunks through a 2-slot LDS ring (64 KB a slot: the tile's 256 W rows and 256 x rows of
- * 128 bytes, the swizzled layout and DMA of k_slot_gemm): at the start of chunk c the DMAs of chunk c + 1 are issued
- * into the slot chunk c - 1 used (every wave is past its reads, one barrier), then chunk c's fragments are read in
- * two halves, the second half's reads in flight while the first half's MFMAs run. Two waves per SIMD overlap one's
- * LDS reads with the other's MFMAs. Rows past m or n read the last row (clamped) and are not stored.
+ * 128 bytes, the swizzled layout and DMA of k_slot_gemm), chunk c in slot c & 1. Per chunk a wave reads the second
+ * half's fragments while the first half's MFMAs run, then meets the others at the chunk's one barrier (everyone's
+ * DMAs of chunk c + 1 have landed, everyone is done reading chunk c), reads the next chunk's first half and runs the
+ * second half's MFMAs with the DMAs of chunk c + 2 (into chunk c's slot) issued one between each group of 4: every
+ * LDS read is in flight behind MFMAs, and the DMAs no longer stall the MFMAs behind the memory queue. Rows past m or
+ * n read the last row (clamped) and are not stored. The tile leaves through LDS, half at a time, as whole rows.
  *
  * Tiles are ordered XCD-aware (workgroup b on XCD b % 8 takes a contiguous range) and, within it, in groups of
  * RG_GROUP x-row tiles that sweep the W tiles, so neighbouring workgroups share x and W rows in L2.
@@ -350,6 +352,8 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
 #define RG_BN 256 /* W rows per tile */
 #define RG_GROUP 4
 #define RG_MIN_M 512 /* nc_slot_gemm_bf16 takes this kernel from this many rows on (automatic tile) */
+#define RG_SROW (RG_BN + 4) /* floats per staged output row: 65 x 16 bytes, so 16 lanes' 16-byte writes of 16 rows
+                             * land on 16 different bank groups */
 
 struct RowsGemmArgs {
     const bf16_t *w, *x;
@@ -366,12 +370,15 @@ template <int OFF> __device__ __forceinline__ bf16x8 rg_ds_read(uint32_t addr) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
-/* This wave's DMA instructions of a chunk: instruction wv + RG_WAVES d lands at dst + 1024 (wv + RG_WAVES d). */
-template <int DPW>
-__device__ __forceinline__ void rg_dma(const unsigned char *const *src, size_t off, unsigned char *dst, int wv) {
-#pragma unroll
-    for (int d = 0; d < DPW; d++)
-        __builtin_amdgcn_global_load_lds(src[d] + off, dst + 1024 * (wv + RG_WAVES * d), 16, 0, 0);
+/* One 16-byte-per-lane DMA into LDS (a function, not a builtin call inside the kernel's lambdas: clang has dropped
+ * the host stub of kernel templates whose lambdas call this builtin). */
+__device__ __forceinline__ void rg_dma1(const unsigned char *src, unsigned char *dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+/* One of four fragments by a wave-uniform index, as selects on values (an indexed array here ends up in scratch). */
+__device__ __forceinline__ bf16x8 rg_pick4(int w, bf16x8 f0, bf16x8 f1, bf16x8 f2, bf16x8 f3) {
+    return w == 0 ? f0 : (w == 1 ? f1 : (w == 2 ? f2 : f3));
 }
 
 template <int EPI>
@@ -381,7 +388,9 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
     constexpr int TM = RG_BM / 16 / WM, TN = RG_BN / 16 / WN;     /* 8 x tiles, 4 W tiles per wave */
     constexpr int TSQ = TM / WN;                                   /* x tiles whose Σ x² this wave computes */
     constexpr bool NORM = EPI == SG_NORM_STORE || EPI == SG_RELU2_NORM || EPI == SG_NORM_F32;
-    __shared__ __attribute__((aligned(1024))) unsigned char ring[2 * SLOT];
+    /* the epilogue stages half the tile (128 x rows of fp32, rows RG_SROW floats apart) where the ring was */
+    constexpr int STAGE = RG_BM / 2 * RG_SROW * 4, LDS = STAGE > 2 * SLOT ? STAGE : 2 * SLOT;
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[LDS];
 
     const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
     if (unit >= a.n_tiles * a.m_tiles) return;
@@ -396,17 +405,25 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
     const size_t ld = (size_t)a.k;
 
     /* DMA instruction i = wv + RG_WAVES d of a chunk moves slot rows 8i..8i+7 (W rows first, then x rows) */
-    const unsigned char *src[DPW];
+    /* as 32-bit byte offsets from W or x (each under 2 GiB): instructions d < DPW / 2 move W rows, the rest x rows */
+    static_assert(RG_BN == RG_BM && DPW % 2 == 0, "W rows fill the first half of a chunk's DMA instructions");
+    uint32_t soff[DPW];
 #pragma unroll
     for (int d = 0; d < DPW; d++) {
         const int r = 8 * (wv + RG_WAVES * d) + (lane >> 3);
         const int piece = (lane & 7) ^ (r & 7);
-        const bf16_t *row = r < RG_BN ? a.w + (size_t)min(row0 + r, a.n - 1) * ld
-                                      : a.x + (size_t)min(m0 + r - RG_BN, a.m - 1) * ld;
-        src[d] = reinterpret_cast<const unsigned char *>(row) + 16 * piece;
+        const size_t row = r < RG_BN ? (size_t)min(row0 + r, a.n - 1) : (size_t)min(m0 + r - RG_BN, a.m - 1);
+        soff[d] = (uint32_t)(row * ld * 2 + 16 * piece);
     }
+    const unsigned char *wb = reinterpret_cast<const unsigned char *>(a.w);
+    const unsigned char *xb = reinterpret_cast<const unsigned char *>(a.x);
+    auto dma1 = [&](int c, int slot, int d) { /* DMA instruction d of chunk c (clamped to the last) */
+        const unsigned char *base = (d < DPW / 2 ? wb : xb) + (size_t)min(c, chunks - 1) * (SG_CHUNK * 2);
+        rg_dma1(base + soff[d], ring + slot * SLOT + 1024 * (wv + RG_WAVES * d));
+    };
     auto dma = [&](int c, int slot) {
-        rg_dma<DPW>(src, (size_t)min(c, chunks - 1) * (SG_CHUNK * 2), ring + slot * SLOT, wv);
+#pragma unroll
+        for (int d = 0; d < DPW; d++) dma1(c, slot, d);
     };
 
     /* fragment rows: W tile t row 16 (wn TN + t) + n, x tile u row RG_BN + 16 (wm TM + u) + n; a row's swizzle
@@ -469,20 +486,60 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
         }
     };
 
-    dma(0, 0);
+    /* the MFMAs of one half in 8 groups of 4 (W tile g / 2, x tiles 4 (g % 2) .. + 3), the same order as multiply */
+    auto multiply_group = [&](int g, const bf16x8 (&wf)[TN], const bf16x8 (&xf)[TM]) {
+#pragma unroll
+        for (int uu = 0; uu < 4; uu++)
+            acc[g / 2][4 * (g % 2) + uu] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g / 2], xf[4 * (g % 2) + uu], acc[g / 2][4 * (g % 2) + uu], 0, 0, 0);
+    };
+    auto multiply_norm = [&](const bf16x8 (&xf)[TM]) {
+        if constexpr (NORM) {
+            static_assert(WN == 4, "x tile q WN + wn of 4");
+#pragma unroll
+            for (int q = 0; q < TSQ; q++) {
+                const bf16x8 v = rg_pick4(wn, xf[q * WN], xf[q * WN + 1], xf[q * WN + 2], xf[q * WN + 3]);
+                sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, v, sq[q], 0, 0, 0);
+            }
+        }
+    };
+    static_assert(DPW == 8, "one DMA instruction per group of 4 MFMAs");
+
+    /* Chunk c lives in slot c & 1. Per chunk: the second half's reads go out, the first half's MFMAs run, the reads
+     * settle; then one barrier (everyone's DMAs of chunk c + 1 have landed, everyone is done reading chunk c), the
+     * DMAs of chunk c + 2 go into chunk c's slot, the next chunk's first-half reads go out and the second half's
+     * MFMAs run. Every LDS read is in flight behind MFMAs; the barrier is the only exposed step. */
     bf16x8 w0[TN], x0[TM], w1[TN], x1[TM];
+    dma(0, 0);
+    sg_wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    dma(1, 1);
+    read(0, 0, w0, x0);
+    settle(w0, x0);
     for (int c = 0; c < chunks; c++) {
-        sg_wait_vmcnt<0>();           /* this wave's DMAs of chunk c have landed */
-        __builtin_amdgcn_s_barrier(); /* everyone's have, and everyone is past its reads of chunk c - 1 */
-        __builtin_amdgcn_sched_barrier(0);
-        dma(c + 1, (c + 1) & 1);      /* past the end: the last chunk again, into the idle slot */
-        read(c, 0, w0, x0);
-        settle(w0, x0);
         read(c, 1, w1, x1);
-        multiply(w0, x0);
-        settle(w1, x1);
-        multiply(w1, x1);
         __builtin_amdgcn_sched_barrier(0);
+        multiply(w0, x0);
+        __builtin_amdgcn_sched_barrier(0);
+        settle(w1, x1);
+        sg_wait_vmcnt<0>();           /* this wave's DMAs of chunk c + 1 have landed */
+        __builtin_amdgcn_s_barrier(); /* everyone's have, and everyone is past its reads of chunk c */
+        __builtin_amdgcn_sched_barrier(0);
+        multiply_norm(x1); /* no read is in flight here */
+        read(min(c + 1, chunks - 1), 0, w0, x0);
+        {
+            /* the DMAs of chunk c + 2 (past the end: the last chunk again) into chunk c's slot, one between each
+             * group of 4 MFMAs: issued all at once they hold up the MFMAs behind the memory queue */
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                __builtin_amdgcn_sched_barrier(0);
+                dma1(c + 2, c & 1, g);
+                multiply_group(g, w1, x1);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        settle(w0, x0);
     }
     sg_wait_vmcnt<0>();
 
@@ -502,38 +559,63 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
         for (int u = 0; u < TM; u++) rstd[u] = 1.f;
     }
 
+    /* The tile leaves in two passes of 128 x rows (the waves of one x-row half each): those waves stage their values
+     * before rounding -- s, s r or relu(s r) s r, and for RESID s alone -- in LDS, then all 512 threads write
+     * whole output rows, 16 bytes each, coalesced (RESID adds res there, one rounding as before). */
     const int N = a.n;
+    float *stage = reinterpret_cast<float *>(ring);
 #pragma unroll
-    for (int u = 0; u < TM; u++) {
-        const int b = m0 + 16 * (wm * TM + u) + n;
-        const float r = rstd[u];
-        if (b >= a.m) continue;
+    for (int pass = 0; pass < WM; pass++) {
+        __syncthreads(); /* the ring (or the previous pass's stage) is free */
+        if (wm == pass) {
 #pragma unroll
-        for (int t = 0; t < TN; t++) {
-            const int col = row0 + 16 * (wn * TN + t) + 4 * j;
-            if (col >= N) continue;
-            const f32x4 s = acc[t][u];
-            const size_t at = (size_t)b * N + col;
-            if constexpr (EPI == SG_NORM_F32) {
-                *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + at) = s * r;
-            } else {
-                float v[4];
+            for (int u = 0; u < TM; u++) {
+                const float r = rstd[u];
+#pragma unroll
+                for (int t = 0; t < TN; t++) {
+                    f32x4 v = acc[t][u];
+                    if constexpr (EPI != SG_RESID && EPI != SG_STORE) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float pv = v[i] * r;
+                            v[i] = EPI == SG_RELU2_NORM ? fmaxf(pv, 0.f) * pv : pv;
+                        }
+                    }
+                    *reinterpret_cast<f32x4 *>(stage + (16 * u + n) * RG_SROW + 16 * (wn * TN + t) + 4 * j) = v;
+                }
+            }
+        }
+        __syncthreads();
+        const int b0 = m0 + pass * (RG_BM / WM);
+        if constexpr (EPI == SG_NORM_F32) {
+            /* 4 fp32 per 16 bytes: 64 per row */
+            for (int i = threadIdx.x; i < RG_BM / WM * 64; i += RG_THREADS) {
+                const int rr = i >> 6, c4 = (i & 63) * 4, b = b0 + rr, col = row0 + c4;
+                if (b < a.m && col < N)
+                    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + (size_t)b * N + col) =
+                        *reinterpret_cast<const f32x4 *>(stage + rr * RG_SROW + c4);
+            }
+        } else {
+            /* 8 bf16 per 16 bytes: 32 per row */
+            for (int i = threadIdx.x; i < RG_BM / WM * 32; i += RG_THREADS) {
+                const int rr = i >> 5, c8 = (i & 31) * 8, b = b0 + rr, col = row0 + c8;
+                if (b >= a.m || col >= N) continue;
+                const f32x4 lo = *reinterpret_cast<const f32x4 *>(stage + rr * RG_SROW + c8);
+                const f32x4 hi = *reinterpret_cast<const f32x4 *>(stage + rr * RG_SROW + c8 + 4);
+                float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                const size_t at = (size_t)b * N + col;
                 if constexpr (EPI == SG_RESID) {
-                    const u32x2 rr = *reinterpret_cast<const u32x2 *>(a.res + at);
-                    v[0] = s[0] + bf16_to_f32(rr[0] & 0xffffu);
-                    v[1] = s[1] + bf16_to_f32(rr[0] >> 16);
-                    v[2] = s[2] + bf16_to_f32(rr[1] & 0xffffu);
-                    v[3] = s[3] + bf16_to_f32(rr[1] >> 16);
-                } else {
+                    const u32x4 rr4 = *reinterpret_cast<const u32x4 *>(a.res + at);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float p = s[i] * r;
-                        v[i] = EPI == SG_RELU2_NORM ? fmaxf(p, 0.f) * p : p;
+                    for (int e = 0; e < 4; e++) {
+                        v[2 * e] = v[2 * e] + bf16_to_f32(rr4[e] & 0xffffu);
+                        v[2 * e + 1] = v[2 * e + 1] + bf16_to_f32(rr4[e] >> 16);
                     }
                 }
-                const u32x2 o = {f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
-                                 f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
-                *reinterpret_cast<u32x2 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = f32_to_bf16(v[2 * e]) | (f32_to_bf16(v[2 * e + 1]) << 16);
+                *reinterpret_cast<u32x4 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
             }
         }
     }
