@@ -213,8 +213,8 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
         sg_wait_vmcnt<DPW * (D - 2)>(); /* this wave's DMAs of chunk c + 1 have landed */
         __builtin_amdgcn_s_barrier();   /* everyone's have, and everyone has settled chunk c's reads */
         __builtin_amdgcn_sched_barrier(0);
-        dma(c + D, c % D);
         read(min(c + 1, chunks - 1), wn_, xn_);
+        dma(c + D, c % D);
         multiply(wf, xf);
         settle(wn_, xn_);
         __builtin_amdgcn_sched_barrier(0);
@@ -239,11 +239,13 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 1; i <= G; i++) dma(c - G + i + D, (c - G + i + D) % D);
-#pragma unroll
             for (int i = 0; i < G; i += 2) {
                 if (i == 0 || c + i < chunks) {
                     read(c + i + 1, wb, xb);
+                    if (i == 0) { /* the refills after the first reads: a burst of DMAs holds up what follows it */
+#pragma unroll
+                        for (int k = 1; k <= G; k++) dma(c - G + k + D, (c - G + k + D) % D);
+                    }
                     multiply(wa, xa);
                     settle(wb, xb);
                     __builtin_amdgcn_sched_barrier(0);
