@@ -622,16 +622,6 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                     pf_wait_pairs<PF_RING - 1 - 2 * PF_BATCH>(wv);
                     __builtin_amdgcn_s_barrier(); /* everyone's have; the slots of pairs < k are free */
                     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int bb = 0; bb < PF_BATCH; bb++) {
-                        const int kr = k + PRO + bb;
-                        u32x2 id;
-                        asm volatile("ds_read_b64 %0, %1\n s_waitcnt lgkmcnt(0)"
-                                     : "=v"(id) : "v"(lds_addr(ids + 2 * min(kr, npairs - 1))) : "memory");
-                        dma_pair(a, __builtin_amdgcn_readfirstlane((int)id[0]),
-                                 __builtin_amdgcn_readfirstlane((int)id[1]), h, dp, wv,
-                                 ring + (kr % PF_RING) * PF_PAIR_BYTES);
-                    }
                 }
                 PfVals vf;
                 u32x2 ids_next;
@@ -652,6 +642,24 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                     pair_scores(kf, q8, s_next);
                     pair_values(vf, pp, st);
                     __builtin_amdgcn_s_setprio(0);
+                }
+                if (k % PF_BATCH == 0) {
+                    /* the freed slots take pairs k + PRO.. after the step's work (the ring holds them PRO pairs
+                     * ahead, so they are not late): issued before it, the block-id reads and DMA burst held up the
+                     * step's own LDS reads and softmax */
+                    u32x2 id[PF_BATCH];
+#pragma unroll
+                    for (int bb = 0; bb < PF_BATCH; bb++)
+                        asm volatile("ds_read_b64 %0, %1"
+                                     : "=v"(id[bb]) : "v"(lds_addr(ids + 2 * min(k + PRO + bb, npairs - 1))) : "memory");
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                    for (int bb = 0; bb < PF_BATCH; bb++) {
+                        asm volatile("" : "+v"(id[bb]));
+                        dma_pair(a, __builtin_amdgcn_readfirstlane((int)id[bb][0]),
+                                 __builtin_amdgcn_readfirstlane((int)id[bb][1]), h, dp, wv,
+                                 ring + ((k + PRO + bb) % PF_RING) * PF_PAIR_BYTES);
+                    }
                 }
                 ids_cur = ids_next;
                 __builtin_amdgcn_sched_barrier(0);
