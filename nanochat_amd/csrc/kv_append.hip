@@ -63,6 +63,16 @@ __device__ __forceinline__ uint32_t quad_transpose(uint32_t w, int r) {
     return (r & 1) ? ((y >> 8) & 0x00ff00ffu) | (w1 & 0xff00ff00u) : (w1 & 0x00ff00ffu) | ((y & 0x00ff00ffu) << 8);
 }
 
+/* The least and the largest of v over the 4 items of a quad (lanes 8 and 16 apart). */
+__device__ __forceinline__ int quad_min(int v) {
+    v = min(v, __shfl_xor(v, 8, NC_WAVE));
+    return min(v, __shfl_xor(v, 16, NC_WAVE));
+}
+__device__ __forceinline__ int quad_max(int v) {
+    v = max(v, __shfl_xor(v, 8, NC_WAVE));
+    return max(v, __shfl_xor(v, 16, NC_WAVE));
+}
+
 /* Items are (row quad, head, row r within the quad), 8 lanes each (qk_row.h). Fused: heads [0, hq) are q,
  * [hq, hq + hkv) k, then v. Store: [0, hkv) k, then v. The 4 rows of a quad sit in 4 consecutive items of one wave
  * (lanes 8 r + lane % 8 of a 32-lane half), so when they are the 4 positions of one quad of one page, in order (a
@@ -138,16 +148,14 @@ __global__ void __launch_bounds__(APPEND_THREADS) k_append(AppendArgs a) {
     /* v: every item of the quad is here (one head per quad), so the exchanges below see all four */
     uint64_t c1, c2;
     const float scale = row_quantize(x1, x2, &c1, &c2);
-    const int qb = blk >= 0 && (p & 3) == r ? blk : -1, qp = p >> 2; /* the quad is whole: same block and quad */
-    const int lo_b = min(min(qb, __shfl_xor(qb, 8, NC_WAVE)), __shfl_xor(min(qb, __shfl_xor(qb, 8, NC_WAVE)), 16, NC_WAVE));
-    const int hi_b = max(max(qb, __shfl_xor(qb, 8, NC_WAVE)), __shfl_xor(max(qb, __shfl_xor(qb, 8, NC_WAVE)), 16, NC_WAVE));
-    const int lo_p = min(min(qp, __shfl_xor(qp, 8, NC_WAVE)), __shfl_xor(min(qp, __shfl_xor(qp, 8, NC_WAVE)), 16, NC_WAVE));
-    const int hi_p = max(max(qp, __shfl_xor(qp, 8, NC_WAVE)), __shfl_xor(max(qp, __shfl_xor(qp, 8, NC_WAVE)), 16, NC_WAVE));
+    /* the quad is whole when its 4 rows name the same block and position quad, row r at position 4 q + r */
+    const int qb = blk >= 0 && (p & 3) == r ? blk : -1, qp = p >> 2;
+    const bool whole = quad_min(qb) >= 0 && quad_min(qb) == quad_max(qb) && quad_min(qp) == quad_max(qp);
     const uint32_t d0 = quad_transpose((uint32_t)c1, r), d1 = quad_transpose((uint32_t)(c1 >> 32), r);
     const uint32_t d2 = quad_transpose((uint32_t)c2, r), d3 = quad_transpose((uint32_t)(c2 >> 32), r);
     if (blk < 0) return;
     uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
-    if (lo_b >= 0 && lo_b == hi_b && lo_p == hi_p) {
+    if (whole) {
         /* dims 8g + r, 8g + 4 + r and their partners 64 apart: one dword of 4 keys each */
         uint32_t *v = reinterpret_cast<uint32_t *>(tile + NC_TILE_V + (t >> 2) * 512);
         v[8 * g + r] = d0;

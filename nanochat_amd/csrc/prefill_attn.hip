@@ -649,9 +649,10 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
                      * step's own LDS reads and softmax */
                     u32x2 id[PF_BATCH];
 #pragma unroll
-                    for (int bb = 0; bb < PF_BATCH; bb++)
-                        asm volatile("ds_read_b64 %0, %1"
-                                     : "=v"(id[bb]) : "v"(lds_addr(ids + 2 * min(k + PRO + bb, npairs - 1))) : "memory");
+                    for (int bb = 0; bb < PF_BATCH; bb++) {
+                        const uint32_t at = lds_addr(ids + 2 * min(k + PRO + bb, npairs - 1));
+                        asm volatile("ds_read_b64 %0, %1" : "=v"(id[bb]) : "v"(at) : "memory");
+                    }
                     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
                     for (int bb = 0; bb < PF_BATCH; bb++) {

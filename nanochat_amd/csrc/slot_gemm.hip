@@ -35,7 +35,7 @@
 #define SG_CHUNK 64                 /* K columns per ring slot: 128 bytes of every row */
 #define SG_LDS_BUDGET (128 * 1024) /* ring bytes per workgroup */
 #define SG_MAX_DEPTH 8             /* ring slots: deeper rings measured no faster */
-#define SG_GROUP 2                 /* chunks per barrier where the ring is deep enough: 2 measured faster than 1 and 4 */
+#define SG_GROUP 2                 /* chunks per barrier where the ring is deep enough (2 measured faster than 1, 4) */
 
 enum { SG_STORE = 0, SG_NORM_STORE = 1, SG_RESID = 2, SG_RELU2_NORM = 3, SG_NORM_F32 = 4 };
 
@@ -491,9 +491,10 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
     /* the MFMAs of one half in 8 groups of 4 (W tile g / 2, x tiles 4 (g % 2) .. + 3), the same order as multiply */
     auto multiply_group = [&](int g, const bf16x8 (&wf)[TN], const bf16x8 (&xf)[TM]) {
 #pragma unroll
-        for (int uu = 0; uu < 4; uu++)
-            acc[g / 2][4 * (g % 2) + uu] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g / 2], xf[4 * (g % 2) + uu], acc[g / 2][4 * (g % 2) + uu], 0, 0, 0);
+        for (int uu = 0; uu < 4; uu++) {
+            f32x4 &d = acc[g / 2][4 * (g % 2) + uu];
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g / 2], xf[4 * (g % 2) + uu], d, 0, 0, 0);
+        }
     };
     auto multiply_norm = [&](const bf16x8 (&xf)[TM]) {
         if constexpr (NORM) {
