@@ -102,6 +102,7 @@ def test_resid_in_place_and_repeatable(gpu):
     (600, 4992, 1664),    # qkv
     (2100, 6656, 1664),   # up
     (513, 1664, 6656),    # down, one row past a tile
+    (700, 128, 320),      # 5 K chunks (an odd count) and a single partial W tile
 ])
 @pytest.mark.parametrize("epi", [STORE, NORM_STORE, RESID, RELU2_NORM, NORM_F32])
 def test_many_rows_equal_the_decode_tiles(gpu, m, n, k, epi):
