@@ -14,9 +14,9 @@
  *     v_mfma_f32_16x16x32_bf16 (A = 16 W rows, B = 16 x rows: Yᵀ tiles); per step a wave waits for its own DMAs,
  *     meets the others at one barrier, refills the slots everyone has finished, reads the next chunk's fragments
  *     while this chunk's MFMAs run, and settles them. A step covers two chunks where the ring is 6 or more slots
- *     deep: the loop is bound by each step's chain of waits (barrier, LDS round trip), not by LDS or L2 bandwidth
- *     (per-workgroup timestamps: 3 % of the loop in DMA waits; counters: LDS busy under half the time, no bank
- *     conflicts), and halving the steps makes the decode-step GEMMs 4-16 % faster with the same bits;
+ *     deep (half the barriers and waits; the decode-step GEMMs 4-16 % faster with the same bits). The loop moves
+ *     about 50 GB/s into each CU whatever issues the loads (4 or 8 extra DMA-only waves were no faster, nor W loaded
+ *     straight into registers), so the time is the bytes reaching the busiest CU, (NT + MT) K 2 per tile;
  *   - the RMS norm of the input rows is fused: the same x fragments feed one more MFMA per 16 rows, x·xᵀ, whose
  *     diagonal is Σ x² of each row, so r = 1 / sqrt(Σ x² / K + FLT_EPSILON) (model/modeling.py:47-49, decode.cu:448-456)
  *     scales the sums in the epilogue instead of a separate normalised copy of x (the reference's RELU2 epilogue,
