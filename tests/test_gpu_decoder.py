@@ -170,9 +170,10 @@ def test_config5_architecture_matches_cpu_model(gpu):
 
 def test_prefill_is_deterministic_and_batch_independent(gpu):
     """Every sum of the prefill is in a fixed order: prefilling the same prompts twice gives the same cache bytes,
-    and a prompt prefilled alone gives the bytes it gets among others (the reference's promise that a request's
-    tokens depend on neither the batch nor the store, inference/decoder.py:124-125). 700 rows: the GEMMs take the
-    many-rows tile together and the decode tile alone."""
+    and a prompt prefilled alone gives the bytes it gets among others (the prefill's share of the reference's promise
+    that a request's tokens depend on neither the batch nor the store, inference/decoder.py:124-125; the decode
+    step's attention balances its split over the batch, so only run-to-run repetition is asserted for the tokens).
+    700 rows: the GEMMs take the many-rows tile together and the decode tile alone."""
     model = RandomModel(ModelConfig(layers=2, d_model=512, heads=4, vocab=1000), gpu, seed=17)
     prompts = torch.from_numpy(np.random.default_rng(18).integers(0, 1000, (4, 176)).astype(np.int32)).to(gpu)
     a = Fp8Decoder(model, 4, 200, gpu)
