@@ -1,10 +1,14 @@
-"""Seeded random sweeps of decode attention, the fused decode step and chunked prefill against the oracle, and of
-the slot GEMM against its fp32 torch restatement. The configurations come from a fixed generator: batch, GQA group,
-per-sequence contexts, paging, windows and outliers; for the GEMM, rows, weight rows, K and the epilogue. Each one is
-held to the fixed-shape tests' bars through their own check functions. For the append, q rows and cache
-bytes are bit-exact. The fused step is bit-identical to the append followed by decode attention. Attention is within
-max abs 2e-2 and mean 2e-3 of fp64. The GEMM is within its bf16 rounding bound, and each row's bits are the same when
-the row is computed alone. Sizes keep each oracle call to a few seconds."""
+"""Seeded random sweeps against the same bars as the fixed-shape tests, through their own check functions:
+
+- decode attention, the fused decode step and chunked prefill against the oracle (batch, GQA group, per-sequence
+  contexts, paging, windows, outliers): q rows and cache bytes bit-exact, the fused step bit-identical to the append
+  followed by decode attention, attention within max abs 2e-2 and mean 2e-3 of fp64;
+- the slot GEMM against its fp32 torch restatement (rows, weight rows, K, epilogue): within its bf16 rounding bound,
+  and each row's bits the same when the row is computed alone;
+- the token choice against oracle/sampling.py (slots, vocabulary, padding, logit cap, lazy token): the same tokens,
+  alternatives and positions.
+
+The configurations come from fixed generators; sizes keep each oracle call to a few seconds."""
 
 import numpy as np
 import pytest
@@ -13,6 +17,7 @@ import torch
 import test_gpu_decode as D
 import test_gpu_slot_gemm as GM
 import test_gpu_prefill as P
+import test_gpu_sampling as C
 import test_gpu_step as S
 from nanochat_amd.slot_gemm import NORM_F32, NORM_STORE, RELU2_NORM, RESID, STORE, slot_gemm
 from nanochat_amd.workloads import DecodeConfig, PrefillConfig
@@ -70,10 +75,22 @@ def gemm_cases(n: int, seed: int) -> list[tuple[int, int, int, int]]:
              int(rng.choice(epis))) for _ in range(n)]
 
 
+def choose_cases(n: int, seed: int) -> list[tuple[int, int, int, int, float, int]]:
+    """(slots, vocabulary, case seed, padded columns, logit cap, lazy token or -1)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        V = int(rng.integers(2, 70000))
+        cases.append((int(rng.integers(1, 300)), V, seed * 100 + i, int(rng.choice((0, 0, 7, 32))),
+                      float(rng.choice((0.0, 15.0, 30.0))), int(rng.integers(0, V)) if rng.random() < 0.5 else -1))
+    return cases
+
+
 DECODE = decode_cases(24, 2024)
 STEP = decode_cases(16, 2025)
 PREFILL = prefill_cases(16, 2026)
 GEMM = gemm_cases(24, 2027)
+CHOOSE = choose_cases(12, 2028)
 
 
 @pytest.mark.parametrize("cfg", DECODE, ids=[c.name for c in DECODE])
@@ -102,3 +119,16 @@ def test_slot_gemm_sweep(gpu, m, n, k, epi):
     alone = slot_gemm(x[:rows].contiguous(), w, epi, res=res[:rows].contiguous() if epi == RESID else None)
     torch.cuda.synchronize()
     assert torch.equal(alone, got[:rows]), "a row's result depends on the rows computed with it"
+
+
+@pytest.mark.parametrize("B, V, seed, pad, softcap, lazy", CHOOSE,
+                         ids=[f"b{b}-v{v}-pad{p}-cap{c:g}-lazy{z}" for b, v, _, p, c, z in CHOOSE])
+def test_choose_sweep(gpu, B, V, seed, pad, softcap, lazy):
+    print(f"choose B {B} V {V} seed {seed} pad {pad} softcap {softcap} lazy {lazy}", flush=True)
+    c = C.make_case(B, V, seed, pad)
+    (tok, alt, pos), (wt, wa, wp) = C.run_both(c, gpu, softcap=softcap, lazy=lazy)
+    act = c["active"]
+    np.testing.assert_array_equal(tok[act], wt[act])
+    np.testing.assert_array_equal(alt[act], wa[act])
+    np.testing.assert_array_equal(pos, wp)
+    assert (tok[~act] == -2).all() and (alt[~act] == -2).all()
