@@ -248,11 +248,13 @@ __device__ __forceinline__ void read_frags(const unsigned char *slot_v, const un
 struct PfState {
     f32x4 o[PF_BLOCKS][8];
     float m[PF_BLOCKS], l[PF_BLOCKS];
-    float vlim;
-    int e_ref;
-    float mo[PF_BLOCKS]; /* lw - m: t = s k_scale score_scale + mo = log2(p w) */
-    float lazy;          /* PF_LAZY + lw */
-    int lw;              /* log2 w = min(126 - e_ref, PF_LW_MAX) */
+    float mo[PF_BLOCKS];   /* lw - m: t = s k_scale score_scale + mo = log2(p w) */
+    /* per column, like m: a column's state follows its own keys only, so its result does not depend on the rows
+     * that share its wave */
+    float vlim[PF_BLOCKS]; /* 2^(e_ref - 126): a v_scale at or above it raises e_ref */
+    int e_ref[PF_BLOCKS];  /* the largest v_scale exponent (biased) among the column's keys so far */
+    float lazy[PF_BLOCKS]; /* PF_LAZY + lw */
+    int lw[PF_BLOCKS];     /* log2 w = min(126 - e_ref, PF_LW_MAX) */
 };
 
 /* A wave's view of the segment being attended: per column the key range [lo, hi] (lo > hi: masked throughout),
@@ -358,9 +360,19 @@ __device__ __forceinline__ void pair_softmax(const PrefillArgs &a, const f32x4 (
     const bool fast = ida >= 0 && idb >= 0 && !c.masked_always && page0 * NC_PAGE >= c.max_lo &&
                       page0 * NC_PAGE + 2 * NC_PAGE - 1 <= c.min_hi;
     unsigned ok[PF_BLOCKS];
+    float vm[PF_BLOCKS]; /* the largest v_scale among the keys each column keeps (this lane's 8) */
+    {
+        const float v = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])),
+                              fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
 #pragma unroll
-    for (int bl = 0; bl < PF_BLOCKS; bl++) ok[bl] = 0xffu;
+        for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            ok[bl] = 0xffu;
+            vm[bl] = v; /* a pair on the fast path: every column keeps every key */
+        }
+    }
     if (!fast) {
+#pragma unroll
+        for (int bl = 0; bl < PF_BLOCKS; bl++) vm[bl] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int key = key0 + (i < 4 ? i : NC_PAGE + i - 4);
@@ -372,58 +384,74 @@ __device__ __forceinline__ void pair_softmax(const PrefillArgs &a, const f32x4 (
                 const bool keep = in_seg && key >= c.lo[bl] && key <= c.hi[bl];
                 ok[bl] &= ~((keep ? 0u : 1u) << i);
                 t[bl][i] = keep ? t[bl][i] : -INFINITY;
+                vm[bl] = fmaxf(vm[bl], keep ? vs[i] : 0.f);
             }
         }
     }
-    bool need = false;
+    bool need[PF_BLOCKS], any_need = false;
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const float tm = fmaxf(fmaxf(fmaxf(t[bl][0], t[bl][1]), fmaxf(t[bl][2], t[bl][3])),
                                fmaxf(fmaxf(t[bl][4], t[bl][5]), fmaxf(t[bl][6], t[bl][7])));
-        need |= tm > st.lazy;
+        need[bl] = tm > st.lazy[bl];
+        any_need |= need[bl];
     }
-    if (__any(need)) { /* rare: move every block's reference max to its exact max (from the unshifted scores) */
+    if (__any(any_need)) {
+        /* rare: a column whose score passed its lazy bound moves its reference max to its exact max over its keys
+         * so far; the others keep m, mo, o, l and t bit for bit */
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
-            float x[8], xm = -INFINITY;
+            int cn = need[bl] ? 1 : 0; /* the column's decision: any of its 4 lanes */
+            cn |= __shfl_xor(cn, 16, 64);
+            cn |= __shfl_xor(cn, 32, 64);
+            float xm = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                x[i] = (ok[bl] >> i) & 1 ? s[bl][i >> 2][i & 3] * ksc[i] : -INFINITY;
-                xm = fmaxf(xm, x[i]);
-            }
+            for (int i = 0; i < 8; i++)
+                xm = fmaxf(xm, (ok[bl] >> i) & 1 ? s[bl][i >> 2][i & 3] * ksc[i] : -INFINITY);
             xm = fmaxf(xm, shfl_xor_f(xm, 16));
             xm = fmaxf(xm, shfl_xor_f(xm, 32));
             const float m_new = fmaxf(st.m[bl], xm);
-            const float alpha = __builtin_amdgcn_exp2f(st.m[bl] - m_new);
+            const float alpha = cn ? __builtin_amdgcn_exp2f(st.m[bl] - m_new) : 1.f; /* x 1: exact */
             st.l[bl] *= alpha;
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= alpha;
-            st.m[bl] = m_new;
-            st.mo[bl] = (float)st.lw - m_new;
+            st.m[bl] = cn ? m_new : st.m[bl];
+            st.mo[bl] = cn ? (float)st.lw[bl] - m_new : st.mo[bl];
+            /* every column's t again, by the fast path's FMA (the same bits where mo did not move); mo through an
+             * empty asm, so the compiler does not keep the unmasked FMA results alive across the masked path to
+             * reuse them here */
+            float mo_b = st.mo[bl];
+            asm volatile("" : "+v"(mo_b));
 #pragma unroll
-            for (int i = 0; i < 8; i++) t[bl][i] = x[i] + st.mo[bl];
+            for (int i = 0; i < 8; i++)
+                t[bl][i] = (ok[bl] >> i) & 1 ? __builtin_fmaf(s[bl][i >> 2][i & 3], ksc[i], mo_b) : -INFINITY;
         }
     }
-    const float vm = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])), fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
-    if (__any(vm >= st.vlim)) { /* rare: a larger v_scale exponent: w = 2^lw drops, o, l and t follow */
-        float vx = fmaxf(vm, shfl_xor_f(vm, 16));
-        vx = fmaxf(vx, shfl_xor_f(vx, 32));
-        const int e_new = max(st.e_ref, (int)(__float_as_uint(vx) >> 23));
-        const int lw_new = min(126 - e_new, PF_LW_MAX), d = lw_new - st.lw;
-        const float r = pf_exp2i(max(d, -126));
+    bool vneed = false;
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) vneed |= vm[bl] >= st.vlim[bl];
+    if (__any(vneed)) {
+        /* rare: a column met a larger v_scale exponent: its w = 2^lw drops, and its o, l and t follow. The others
+         * have d = 0: x 1 and + 0 keep their bits (mo and t are never -0: round-to-nearest differences and FMAs of
+         * a nonzero mo give +0) */
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
+            float vx = fmaxf(vm[bl], shfl_xor_f(vm[bl], 16));
+            vx = fmaxf(vx, shfl_xor_f(vx, 32));
+            const int e_new = max(st.e_ref[bl], (int)(__float_as_uint(vx) >> 23));
+            const int lw_new = min(126 - e_new, PF_LW_MAX), d = lw_new - st.lw[bl];
+            const float r = pf_exp2i(max(d, -126));
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) st.o[bl][bb] *= r;
             st.l[bl] *= r;
             st.mo[bl] += (float)d;
 #pragma unroll
             for (int i = 0; i < 8; i++) t[bl][i] += (float)d;
+            st.lw[bl] = lw_new;
+            st.lazy[bl] = PF_LAZY + (float)lw_new;
+            st.e_ref[bl] = e_new;
+            st.vlim[bl] = pf_exp2i(min(e_new - 126, 127));
         }
-        st.lw = lw_new;
-        st.lazy = PF_LAZY + (float)lw_new;
-        st.e_ref = e_new;
-        st.vlim = pf_exp2i(min(e_new - 126, 127));
     }
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
@@ -504,10 +532,13 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         st.m[bl] = PF_M_INIT;
         st.l[bl] = 0.f;
     }
-    st.e_ref = 0;
-    st.vlim = pf_exp2i(-126);
-    st.lw = PF_LW_MAX;
-    st.lazy = PF_LAZY + (float)PF_LW_MAX;
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        st.e_ref[bl] = 0;
+        st.vlim[bl] = pf_exp2i(-126);
+        st.lw[bl] = PF_LW_MAX;
+        st.lazy[bl] = PF_LAZY + (float)PF_LW_MAX;
+    }
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) st.mo[bl] = (float)PF_LW_MAX - PF_M_INIT;
 
@@ -579,7 +610,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         c.seg_lo = lo;
         c.seg_hi = hi;
 
-        const int first = lo / NC_PAGE, npages = hi / NC_PAGE - first + 1;
+        /* pairs start at even pages whatever the segment's first key: a column meets its keys in the same pairs,
+         * slots and sum trees whichever rows share its workgroup (pages before lo are masked) */
+        const int first = (lo / NC_PAGE) & ~1, npages = hi / NC_PAGE - first + 1;
         for (int cb = 0; cb < npages; cb += PF_IDS) {
             const int cp = min(PF_IDS, npages - cb), npairs = (cp + 1) / 2;
             __syncthreads(); /* the previous chunk's ring and ids are no longer read */

@@ -57,6 +57,35 @@ def test_prefill_edge_shapes(gpu, cfg):
     run_and_check(cfg, gpu)
 
 
+@pytest.mark.parametrize("cfg", [
+    CONFIG4,
+    PrefillConfig("causal-g1", 4, 16, 16, cached=(0,), chunk=(700,), seed=9),
+    PrefillConfig("g4-outliers", 4, 16, 4, cached=(300,), chunk=(500,), outliers=0.01, seed=10),
+    PrefillConfig("g8-window-paged", 3, 16, 2, cached=(900, 50, 400), chunk=(200, 300, 90), window=250, paged=True,
+                  seed=11),
+])
+def test_a_row_does_not_depend_on_its_neighbours(gpu, cfg):
+    """Each column keeps its own softmax state (lazy max, value-scale exponent) and meets its keys in page pairs that
+    start at even pages, so a row's output bits do not depend on the rows computed with it: every subset, order and
+    alignment gives the bits of the full call (the reference's k_attn attends each row alone)."""
+    print(f"prefill grouping case {cfg.name}", flush=True)
+    case = build_prefill_case(cfg, gpu)
+    q = case.cache.append(case.qkv, case.pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    full = prefill_attention(q, case.cache, case.pos, case.seq, window=cfg.window)
+    n = q.shape[0]
+    perm = torch.from_numpy(np.random.default_rng(cfg.seed).permutation(n)).to(gpu)
+    subsets = {"odd rows": torch.arange(1, n, 2, device=gpu), "shifted by 5": torch.arange(5, n, device=gpu),
+               "reversed": torch.arange(n - 1, -1, -1, device=gpu), "permuted": perm,
+               "a few alone": perm[:7]}
+    for name, idx in subsets.items():
+        rows = [idx[i:i + 1] for i in range(idx.numel())] if name == "a few alone" else [idx]
+        for r in rows:
+            sub = prefill_attention(q[r].contiguous(), case.cache, case.pos[r].contiguous(),
+                                    case.seq[r].contiguous(), window=cfg.window)
+            torch.cuda.synchronize()
+            assert torch.equal(sub.view(torch.int16), full[r].view(torch.int16)), f"{cfg.name}: {name}"
+
+
 def test_rows_in_any_order_and_invalid_rows(gpu):
     """Shuffled rows (so tiles mix sequences and positions) give the oracle's per-row result; rows with pos < 0 or
     a sequence out of range are zero and disturb no other row."""
