@@ -168,6 +168,27 @@ def test_config5_architecture_matches_cpu_model(gpu):
                       mean_tol=CFG5_LOGIT_MEAN, row_chunk=1024)
 
 
+def test_prefill_in_chunks_leaves_the_same_bytes(gpu):
+    """A prompt prefilled in two calls (positions 0..99, then 100..174) leaves the bytes of one call in every layer:
+    each row attends its own key range with its own arithmetic (whatever rows share its workgroup), and a GEMM row's
+    bits do not depend on the rows computed with it. GQA (4 query heads per kv head), a window and a value-embedding
+    layer, so every prefill path takes part."""
+    cfg = ModelConfig(layers=3, d_model=512, heads=8, vocab=1000, n_kv_heads=2, windows=(64, -1, -1), ve_layers=(1,))
+    model = RandomModel(cfg, gpu, seed=19)
+    prompts = torch.from_numpy(np.random.default_rng(20).integers(0, 1000, (3, 176)).astype(np.int32)).to(gpu)
+    whole = Fp8Decoder(model, 3, 200, gpu)
+    whole.prefill(prompts)
+    parts = Fp8Decoder(model, 3, 200, gpu)
+    for lo, hi in ((0, 100), (100, 175)):
+        tok = prompts[:, lo:hi].reshape(-1).contiguous()
+        pos = torch.arange(lo, hi, dtype=torch.int32, device=gpu).repeat(3)
+        seq = torch.arange(3, dtype=torch.int32, device=gpu).repeat_interleave(hi - lo)
+        parts._prefill_rows(tok, pos, seq)
+    torch.cuda.synchronize()
+    for l in range(cfg.layers):
+        assert torch.equal(whole.caches[l].pages, parts.caches[l].pages), f"layer {l}"
+
+
 def test_prefill_is_deterministic_and_batch_independent(gpu):
     """Every sum of the prefill is in a fixed order: prefilling the same prompts twice gives the same cache bytes,
     and a prompt prefilled alone gives the bytes it gets among others (the prefill's share of the reference's promise
