@@ -28,7 +28,7 @@
  * carry position -1: the decode step does no work for them and the choice leaves them untouched.
  *
  * Small host-to-device updates (a slot's prompt state, the slot words, dec_take_alt) are kernels whose values travel
- * in the kernel arguments, so no host buffer is read after the call returns. dec_prefill's rows (up to 12 KB) go
+ * in the kernel arguments, so no host buffer is read after the call returns. dec_prefill's rows (up to 192 KB) go
  * through the ring of pinned buffers, each guarded by an event recorded after its copy.
  *
  * Errors follow the reference's handle (decode.cu:47-53,927-931): an argument out of range or a failed HIP call
@@ -279,9 +279,9 @@ static int create(Decoder *d, const int *cfg, int ncfg, const uint64_t *ptrs, co
     d->Hkv = ncfg > 7 && cfg[7] > 0 ? cfg[7] : d->H;
     const int batch = ncfg > 8 ? cfg[8] : 0;
     d->wte_fp32 = ncfg > 9 ? cfg[9] == 0 : 1; /* field 9: 1 for a bf16 embedding table; the reference's is fp32 */
-    NC_REQUIRE(d->L > 0 && d->C > 0 && d->C % NC_HEAD_DIM == 0 && d->C % 64 == 0 && d->C <= 8192,
+    NC_REQUIRE(d->L > 0 && d->C > 0 && d->C % NC_HEAD_DIM == 0 && d->C <= 8192,
                "dec_create: L %d, C %d (a multiple of 128, at most 8192)", d->L, d->C);
-    NC_REQUIRE(d->F > 0 && d->F % 64 == 0 && d->F % 32 == 0, "dec_create: F %d must be a multiple of 64", d->F);
+    NC_REQUIRE(d->F > 0 && d->F % 64 == 0, "dec_create: F %d must be a multiple of 64", d->F);
     NC_REQUIRE(d->vocab > 0 && d->vocab <= 131072, "dec_create: vocab %d outside [1, 131072]", d->vocab);
     NC_REQUIRE(d->max_len > 0, "dec_create: max_len %d", d->max_len);
     NC_REQUIRE(d->Hkv > 0 && d->H % d->Hkv == 0 && d->H / d->Hkv <= 16, "dec_create: %d heads over %d kv heads", d->H,
@@ -434,8 +434,9 @@ extern "C" void dec_prefill(void *handle, int n, const int32_t *rows) {
     NC_HIP_CHECK(hipEventSynchronize(d->staged[k]));
     int32_t *host = d->host_rows + (size_t)k * 3 * DEC_ROWS;
     for (int c = 0; c < 3; c++) memcpy(host + c * DEC_ROWS, rows + (size_t)c * n, n * sizeof(int32_t));
-    NC_HIP_CHECK(hipMemcpyAsync(d->r.tok, host, 3 * (size_t)DEC_ROWS * sizeof(int32_t), hipMemcpyHostToDevice,
-                                d->stream));
+    const size_t pitch = (size_t)DEC_ROWS * sizeof(int32_t); /* the n rows of each of the 3 fields */
+    NC_HIP_CHECK(hipMemcpy2DAsync(d->r.tok, pitch, host, pitch, n * sizeof(int32_t), 3, hipMemcpyHostToDevice,
+                                  d->stream));
     NC_HIP_CHECK(hipEventRecord(d->staged[k], d->stream));
     if (enqueue_prefill(d, n) < 0) {
         fprintf(stderr, "dec_prefill: %s\n", nc_last_error());
