@@ -157,11 +157,11 @@ __global__ void __launch_bounds__(APPEND_THREADS) k_append(AppendArgs a) {
     uint8_t *tile = a.cache + tile_offset(blk, h, a.hkv);
     if (whole) {
         /* dims 8g + r, 8g + 4 + r and their partners 64 apart: one dword of 4 keys each */
-        uint32_t *v = reinterpret_cast<uint32_t *>(tile + NC_TILE_V + (t >> 2) * 512);
-        v[8 * g + r] = d0;
-        v[8 * g + 4 + r] = d1;
-        v[NC_HALF + 8 * g + r] = d2;
-        v[NC_HALF + 8 * g + 4 + r] = d3;
+        const int t0 = t & ~3;
+        *reinterpret_cast<uint32_t *>(tile + v_byte(t0, 8 * g + r)) = d0;
+        *reinterpret_cast<uint32_t *>(tile + v_byte(t0, 8 * g + 4 + r)) = d1;
+        *reinterpret_cast<uint32_t *>(tile + v_byte(t0, NC_HALF + 8 * g + r)) = d2;
+        *reinterpret_cast<uint32_t *>(tile + v_byte(t0, NC_HALF + 8 * g + 4 + r)) = d3;
     } else {
         write_codes(tile, t, g, c1, c2, true);
     }
@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(256) k_gather(const uint8_t *cache, const int3
     float ks = 0.0f, vs = 0.0f;
     if (blk >= 0) {
         const uint8_t *tile = cache + tile_offset(blk, h, hkv);
-        kw = *reinterpret_cast<const uint64_t *>(tile + t * NC_HEAD_DIM + 8 * c);
+        kw = *reinterpret_cast<const uint64_t *>(tile + k_byte(t, 8 * c));
 #pragma unroll
         for (int e = 0; e < 8; e++) vw |= (uint64_t)tile[v_byte(t, 8 * c + e)] << (8 * e);
         ks = reinterpret_cast<const float *>(tile + NC_TILE_KS)[t];

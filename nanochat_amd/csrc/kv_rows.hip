@@ -51,7 +51,7 @@ __global__ void __launch_bounds__(ROWS_PER_BLOCK * NC_WAVE) k_rows_export(RowArg
     uint32_t word = 0;
     if (tile) {
         if (lane < 32) {
-            word = *reinterpret_cast<const uint32_t *>(tile + t * NC_HEAD_DIM + 4 * lane);
+            word = *reinterpret_cast<const uint32_t *>(tile + k_byte(t, 4 * lane));
         } else {
             const int d = 4 * (lane - 32);
 #pragma unroll
@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(ROWS_PER_BLOCK * NC_WAVE) k_rows_import(RowArg
     const uint8_t *src = a.flat + r * ROW_BYTES;
     const uint32_t word = reinterpret_cast<const uint32_t *>(src)[lane];
     if (lane < 32) {
-        *reinterpret_cast<uint32_t *>(tile + t * NC_HEAD_DIM + 4 * lane) = word;
+        *reinterpret_cast<uint32_t *>(tile + k_byte(t, 4 * lane)) = word;
     } else {
         const int d = 4 * (lane - 32);
 #pragma unroll

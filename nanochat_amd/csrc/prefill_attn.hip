@@ -31,7 +31,7 @@
  * Roofline: MFMA (the dense bf16/fp16 peak; the fp8 score MFMAs run at twice that rate over twice the work).
  *
  * K/V staging: a ring of PF_RING page-pair slots in LDS, filled by global_load_lds_dwordx4 (lane i of a DMA lands
- * at slot + 16 i, so the global side gathers each lane's MFMA fragment and the read back is a contiguous,
+ * at slot + 16 i: the tile's fragment-major parts arrive as they lie, and the read back is a contiguous,
  * conflict-free ds_read_b128 per fragment). Each wave issues 2 of a pair's 8 fragment loads from a scalar tile
  * base, the last wave also the pair's scales; the waves meet at a barrier every PF_BATCH pairs, where the ring's
  * freed slots are refilled. Block ids are staged in LDS per chunk of PF_IDS pages.
@@ -117,11 +117,11 @@ template <int N> __device__ __forceinline__ void pf_wait_vmcnt() {
 }
 
 /* A ring slot holds a page pair as [A: K 2 KiB, V 2 KiB][B: K, V][A: K and V scales 128 B][B: scales]. Its 8
- * fragments of 1 KiB (K bytes 0-15 / 16-31 of every lane, V bytes 0-15 / 16-31, per page) are spread over the
- * waves, 2 each; the last wave also loads both pages' scales with one dword DMA of all 64 lanes (lane l: page
- * l / 32, bytes 4 (l % 32) of its scales). No DMA runs under a partial exec mask: the compiler may merge two
- * exec-masked DMAs of different LDS destinations into one whose M0 (the destination, which must be wave-uniform)
- * comes from a divergent value. Per-lane byte offsets within a tile are fixed for the whole loop; the tile base is
+ * fragments of 1 KiB (per page the tile's four contiguous parts: K bytes 0-15 / 16-31 of every lane, V bytes
+ * 0-15 / 16-31) are spread over the waves, 2 each; the last wave also loads both pages' scales with one dword DMA
+ * of all 64 lanes (lane l: page l / 32, bytes 4 (l % 32) of its scales). No DMA runs under a partial exec mask:
+ * the compiler may merge two exec-masked DMAs of different LDS destinations into one whose M0 (the destination,
+ * which must be wave-uniform) comes from a divergent value. Per-lane byte offsets within a tile are fixed for the whole loop; the tile base is
  * wave-uniform. */
 #define PF_FRAGS (8 / PF_WAVES)         /* fragments per wave and pair */
 #define PF_SLOT_SCALES (4 * NC_TILE_V)  /* 8192: both pages' scales */
@@ -141,7 +141,7 @@ __device__ __forceinline__ PfDma dma_plan(int wv, int lane) {
         const int f = wv * PF_FRAGS + i;
         d.page[i] = f >> 2;
         d.part[i] = f & 3;
-        d.frag[i] = (d.part[i] < 2 ? n * NC_HEAD_DIM + j * 32 : NC_TILE_V + j * 512 + n * 32) + 16 * (d.part[i] & 1);
+        d.frag[i] = d.part[i] * NC_TILE_PART + 16 * (n + 16 * j);
     }
     d.scale_page = lane >> 5;
     d.scale = NC_TILE_KS + 4 * (lane & 31);

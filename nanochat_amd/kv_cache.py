@@ -6,12 +6,13 @@ The reference caches K and V in bf16, contiguous per slot ([slot][layer][max_len
 contiguous cache is the special case where sequence s owns blocks [s * max_blocks, (s + 1) * max_blocks).
 
 Device layout (also nanochat_amd/csrc/layout.h): one pool `pages`, uint8 [num_blocks][Hkv][4224], and per
-(block, kv head) tile the views
-  k        [16][128]      bytes [0, 2048)      key t of a page at row t
-  v        [4][128][4]    bytes [2048, 4096)   key t, dim d at [t // 4][d][t % 4] (quad-transposed)
-  k_scale  fp32 [16]      bytes [4096, 4160)
-  v_scale  fp32 [16]      bytes [4160, 4224)
-so that one page of one kv head is a single contiguous 4224-byte read.
+(block, kv head) tile
+  K codes  bytes [0, 2048)      key t, dim d at K_BYTES[t][d]
+  V codes  bytes [2048, 4096)   key t, dim d at V_BYTES[t][d] (quad-transposed: the 4 keys of a quad in one dword)
+  k_scale  fp32 [16]            bytes [4096, 4160)
+  v_scale  fp32 [16]            bytes [4160, 4224)
+so that one page of one kv head is a single contiguous 4224-byte read. The codes lie in four 1 KiB parts of 64
+16-byte fragments, lane f's MFMA fragment at part * 1024 + 16 f, so each load of a wave reads 1 KiB contiguous.
 """
 
 from __future__ import annotations
@@ -25,6 +26,16 @@ PAGE = 16
 HEAD_DIM = 128
 TILE_BYTES = 4224
 ROW_BYTES = 264  # one position of one kv head as a row: K codes, V codes, K scale, V scale
+
+
+def _code_bytes() -> tuple[Tensor, Tensor]:
+    t, d = torch.arange(PAGE)[:, None], torch.arange(HEAD_DIM)[None, :]
+    k = (d // 16 % 2) * 1024 + (t + 16 * (d // 32)) * 16 + d % 16
+    v = 2048 + (d // 4 % 2) * 1024 + (d // 8 + 16 * (t // 4)) * 16 + d % 4 * 4 + t % 4
+    return k, v
+
+
+K_BYTES, V_BYTES = _code_bytes()  # byte of key t, dim d within a tile, int64 [16][128] (CPU)
 
 
 def _require(t: Tensor, name: str, dtype: torch.dtype, dim: int | None = None) -> None:
@@ -50,16 +61,6 @@ class Fp8KVCache:
         self.num_blocks, self.hkv, self.max_blocks, self.num_seqs = num_blocks, hkv, max_blocks, num_seqs
         self.block_table = block_table
         self.pages = torch.zeros((num_blocks, hkv, TILE_BYTES), dtype=torch.uint8, device=device)
-
-    @property
-    def k(self) -> Tensor:
-        """K codes, a view [num_blocks][hkv][16][128]."""
-        return self.pages[..., :2048].unflatten(-1, (PAGE, HEAD_DIM))
-
-    @property
-    def v(self) -> Tensor:
-        """V codes, a view [num_blocks][hkv][4][128][4] (quad-transposed)."""
-        return self.pages[..., 2048:4096].unflatten(-1, (PAGE // 4, HEAD_DIM, 4))
 
     @property
     def k_scale(self) -> Tensor:
@@ -140,7 +141,7 @@ class Fp8KVCache:
         B = ctx_len.shape[0]
         if B > self.num_seqs:
             raise ValueError(f"{B} sequences, the cache holds {self.num_seqs}")
-        dev = self.k.device
+        dev = self.pages.device
         k = torch.empty((B, self.hkv, max_ctx, HEAD_DIM), dtype=torch.uint8, device=dev)
         v = torch.empty_like(k)
         ks = torch.empty((B, self.hkv, max_ctx), dtype=torch.float32, device=dev)

@@ -5,9 +5,9 @@ Every function states the rule it fixes and the reference file:line it follows. 
 benchmark configuration, not by the reference, and is restated here as the build's spec.
 
 Layout spec shared with the HIP kernels (nanochat_amd/csrc/layout.h): one byte pool [num_blocks][Hkv][4224]; the
-(block, kv head) tile holds
-  [0, 2048)     K codes, row-major: key t of a page at t*128
-  [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + (t/4)*512 + d*4 + t%4
+(block, kv head) tile holds, in four 1 KiB parts of 64 16-byte fragments (fragment f at part*1024 + 16 f),
+  [0, 2048)     K codes: key t, dim d at ((d/16)%2)*1024 + (t + 16 (d/32))*16 + d%16
+  [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + ((d/4)%2)*1024 + (d/8 + 16 (t/4))*16 + (d%4)*4 + t%4
   [4096, 4160)  K scales fp32 [16], one per (token, kv head)
   [4160, 4224)  V scales fp32 [16]
   block table int32 [B][max_blocks]; None means contiguous: sequence b's page i is block b*max_blocks + i.
@@ -140,19 +140,31 @@ def dequantize(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
 TILE_BYTES = 4224
 
 
+def k_byte(t, d):
+    """Byte of key t, dim d in a tile (module docstring)."""
+    return ((d // 16) % 2) * 1024 + (t + 16 * (d // 32)) * 16 + d % 16
+
+
+def v_byte(t, d):
+    """Byte of key t, dim d in a tile (module docstring)."""
+    return 2048 + ((d // 4) % 2) * 1024 + (d // 8 + 16 * (t // 4)) * 16 + (d % 4) * 4 + t % 4
+
+
+_T, _D = np.meshgrid(np.arange(PAGE), np.arange(HEAD_DIM), indexing="ij")
+K_BYTES = k_byte(_T, _D)  # [16][128]
+V_BYTES = v_byte(_T, _D)
+
+
 class PagedCache:
-    """The HIP kernels' cache layout (module docstring): the byte pool `pages` and named views of its regions
-    (k [nb][Hkv][16][128], v [nb][Hkv][4][128][4], k_scale / v_scale fp32 [nb][Hkv][16]); writes through a view
-    land in the pool."""
+    """The HIP kernels' cache layout (module docstring): the byte pool `pages`, its codes at K_BYTES / V_BYTES
+    [t][d] of a tile, and views of the scales (k_scale / v_scale fp32 [nb][Hkv][16]); writes land in the pool."""
 
     def __init__(self, num_blocks: int, hkv: int):
         self.num_blocks, self.hkv = num_blocks, hkv
         self.pages = np.zeros((num_blocks, hkv, TILE_BYTES), np.uint8)
-        self.k = self.pages[..., :2048].reshape(num_blocks, hkv, PAGE, HEAD_DIM)
-        self.v = self.pages[..., 2048:4096].reshape(num_blocks, hkv, PAGE // 4, HEAD_DIM, 4)
         self.k_scale = self.pages[..., 4096:4160].view(np.float32)
         self.v_scale = self.pages[..., 4160:4224].view(np.float32)
-        assert all(np.shares_memory(x, self.pages) for x in (self.k, self.v, self.k_scale, self.v_scale))
+        assert all(np.shares_memory(x, self.pages) for x in (self.k_scale, self.v_scale))
 
     @staticmethod
     def block_of(seq: np.ndarray, pos: np.ndarray, block_table: np.ndarray | None, max_blocks: int) -> np.ndarray:
@@ -162,15 +174,18 @@ class PagedCache:
         return np.asarray(block_table, np.int64)[seq, pos // PAGE]
 
     def write(self, blk, head, t, k_codes, k_scale, v_codes, v_scale) -> None:
-        """Rows for (block, kv head, token-in-page) triples: K row-major, V at (t/4, d, t%4)."""
-        self.k[blk, head, t] = k_codes
-        self.v[blk, head, t // 4, :, t % 4] = v_codes
+        """Rows (codes [..][128] in dim order) for (block, kv head, token-in-page) index arrays (broadcast)."""
+        blk, head, t = np.broadcast_arrays(np.asarray(blk), np.asarray(head), np.asarray(t))
+        self.pages[blk[..., None], head[..., None], K_BYTES[t]] = k_codes
+        self.pages[blk[..., None], head[..., None], V_BYTES[t]] = v_codes
         self.k_scale[blk, head, t] = k_scale
         self.v_scale[blk, head, t] = v_scale
 
     def read(self, blk, head, t) -> tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
-        """(K codes, V codes row-major, K scale, V scale) at index arrays blk, head, t (broadcast)."""
-        return (self.k[blk, head, t], self.v[blk, head, t // 4, :, t % 4], self.k_scale[blk, head, t],
+        """(K codes, V codes in dim order, K scale, V scale) at index arrays blk, head, t (broadcast)."""
+        blk, head, t = np.broadcast_arrays(np.asarray(blk), np.asarray(head), np.asarray(t))
+        return (self.pages[blk[..., None], head[..., None], K_BYTES[t]],
+                self.pages[blk[..., None], head[..., None], V_BYTES[t]], self.k_scale[blk, head, t],
                 self.v_scale[blk, head, t])
 
 

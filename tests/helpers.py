@@ -28,10 +28,10 @@ def table(cache):
 def assert_same_cache(gpu_cache, ref: G.PagedCache) -> None:
     """Every byte of the pool: codes and the scales' fp32 bit patterns."""
     got = gpu_cache.pages.cpu().numpy()
-    for name in ("k", "v", "k_scale", "v_scale"):  # name the region that differs first
-        g = G.PagedCache(gpu_cache.num_blocks, gpu_cache.hkv)
-        g.pages[...] = got
-        np.testing.assert_array_equal(getattr(g, name).view(np.uint8), getattr(ref, name).view(np.uint8), name)
+    regions = {"k codes [block][head][key][dim]": G.K_BYTES, "v codes [block][head][key][dim]": G.V_BYTES,
+               "k scales": np.arange(4096, 4160), "v scales": np.arange(4160, 4224)}
+    for name, at in regions.items():  # name the region that differs first
+        np.testing.assert_array_equal(got[..., at], ref.pages[..., at], name)
     np.testing.assert_array_equal(got, ref.pages)
 
 

@@ -9,7 +9,7 @@ import torch
 
 from helpers import assert_attention_close, assert_same_cache, bits, oracle_cache, table
 from nanochat_amd.attention import decode_attention, decode_workspace
-from nanochat_amd.kv_cache import Fp8KVCache
+from nanochat_amd.kv_cache import K_BYTES, V_BYTES, Fp8KVCache
 from nanochat_amd.workloads import CONFIG1, CONFIG2, CONFIG3, DecodeConfig, build_decode_case, decode_step
 from oracle import golden as G
 
@@ -70,11 +70,11 @@ def test_single_key_returns_the_value_exactly(gpu):
     cache = Fp8KVCache.contiguous(1, 16, hkv, dev)
     codes = torch.tensor([c for c in range(256) if c & 0x7F != 0x7F] + [0, 0], dtype=torch.uint8)
     v_rows = codes.view(hkv, 128)
-    cache.v[0, :, 0, :, 0] = v_rows.to(dev)  # key 0 of the page: quad 0, byte 0 of every dim's dword
-    cache.k[0, :, 0] = torch.randint(0, 0x7E, (hkv, 128), dtype=torch.uint8).to(dev)
+    cache.pages[0, :, V_BYTES[0].to(dev)] = v_rows.to(dev)  # key 0 of the page: byte 0 of every dim's dword
+    cache.pages[0, :, K_BYTES[0].to(dev)] = torch.randint(0, 0x7E, (hkv, 128), dtype=torch.uint8).to(dev)
     cache.k_scale[0, :, 0] = 0.01
     cache.v_scale[0, :, 0] = 0.25
-    assert cache.pages[0, 1, 4160:4164].view(torch.float32).item() == 0.25  # the views write the pool
+    assert cache.pages[0, 1, 4160:4164].view(torch.float32).item() == 0.25  # the scale views write the pool
     q = torch.randn((1, hq, 128), device=dev).to(torch.bfloat16)
     out = decode_attention(q, cache, torch.tensor([1], dtype=torch.int32, device=dev), max_ctx=16)
     want = G.E4M3_TABLE[v_rows.numpy()] * np.float32(0.25)

@@ -199,21 +199,54 @@ def test_quantize_rows_absmax_maps_to_448_and_error_bound():
 # ----------------------------------------------------------------------------------------------- cache layout
 
 def test_cache_layout_byte_offsets():
-    """Tile (block, head) at byte (block * Hkv + head) * 4224 of the pool: K key t at t*128, V key t dim d at
-    2048 + (t/4)*512 + d*4 + t%4, K scale t at 4096 + 4t, V scale t at 4160 + 4t."""
+    """Tile (block, head) at byte (block * Hkv + head) * 4224 of the pool; K key 13, V key 13 at hand-computed bytes
+    (K dims 0 / 20 / 77 / 127 at 208 / 1236 / 733 / 2015, V dims 0 / 5 / 77 / 127 at 2049 + 16 * 48 = 2817,
+    3073 + 16 * 48 + 4, 3073 + 16 * 57 + 4, 3073 + 16 * 63 + 12), K scale t at 4096 + 4t, V scale t at
+    4160 + 4t."""
     c = G.PagedCache(3, 2)
     kc = np.arange(128, dtype=np.uint8)
     vc = (np.arange(128) + 100).astype(np.uint8)
     c.write(np.array([2]), 1, np.array([13]), kc[None], np.float32(0.5), vc[None], np.float32(0.25))
     flat = c.pages.reshape(-1)
     tile = (2 * 2 + 1) * 4224
-    np.testing.assert_array_equal(flat[tile + 13 * 128: tile + 14 * 128], kc)
-    for d in (0, 1, 77, 127):
-        assert flat[tile + 2048 + (13 // 4) * 512 + d * 4 + 13 % 4] == vc[d]
+    for d, at in ((0, 208), (20, 1024 + 13 * 16 + 4), (77, (13 + 32) * 16 + 13), (127, 1024 + (13 + 48) * 16 + 15)):
+        assert flat[tile + at] == kc[d], d
+    for d, at in ((0, 2048 + 48 * 16 + 1), (5, 3072 + 48 * 16 + 4 + 1), (77, 3072 + (9 + 48) * 16 + 4 + 1),
+                  (127, 3072 + (15 + 48) * 16 + 12 + 1)):
+        assert flat[tile + at] == vc[d], d
     assert flat[tile + 4096 + 4 * 13: tile + 4096 + 4 * 14].view(np.float32)[0] == 0.5
     assert flat[tile + 4160 + 4 * 13: tile + 4160 + 4 * 14].view(np.float32)[0] == 0.25
     # 127 nonzero K codes, 128 V codes, and the scales' nonzero bytes: 0.5 = 0x3f000000 (1), 0.25 = 0x3e800000 (2)
     assert np.count_nonzero(flat) == 127 + 128 + 1 + 2
+
+
+def test_cache_parts_are_the_lanes_mfma_fragments():
+    """Each 1 KiB part of a tile, read as [64 lanes][16 B], is what lane f = n + 16 j holds for the MFMAs: K part P,
+    key n, dims 32 j + 16 P .. + 15 (16x16x32 A operand: row n, k slots of group j); V part 2 + P, dims
+    8 n + 4 P .. 8 n + 4 P + 3 of keys 4 j .. 4 j + 3, one dword per dim with key 4 j + i in byte i."""
+    c = G.PagedCache(1, 1)
+    t = np.arange(16)
+    dims = np.broadcast_to(np.arange(128, dtype=np.uint8), (16, 128))
+    keys = np.broadcast_to((np.arange(16, dtype=np.uint8) + 128)[:, None], (16, 128))
+    c.write(np.zeros(16, np.int64), 0, t, dims, np.float32(1), keys, np.float32(1))  # K code = dim, V code = key
+    tile = c.pages[0, 0]
+    for f in range(64):
+        n, j = f % 16, f // 16
+        for P in range(2):
+            frag = tile[P * 1024 + 16 * f: P * 1024 + 16 * f + 16]
+            np.testing.assert_array_equal(frag, 32 * j + 16 * P + np.arange(16))  # key n's dims: K codes are dims
+            vfrag = tile[2048 + P * 1024 + 16 * f: 2048 + P * 1024 + 16 * f + 16].reshape(4, 4)  # [dim][key]
+            np.testing.assert_array_equal(vfrag, np.broadcast_to(128 + 4 * j + np.arange(4), (4, 4)))
+    # V dims: plant one code per (key, dim) and read the dword layout back
+    rng = np.random.default_rng(3)
+    vcodes = rng.integers(0, 256, (16, 128), dtype=np.uint8)
+    c.write(np.zeros(16, np.int64), 0, t, dims, np.float32(1), vcodes, np.float32(1))
+    tile = c.pages[0, 0]
+    for f in (0, 5, 17, 40, 63):
+        n, j = f % 16, f // 16
+        for P in range(2):
+            vfrag = tile[2048 + P * 1024 + 16 * f: 2048 + P * 1024 + 16 * f + 16].reshape(4, 4)
+            np.testing.assert_array_equal(vfrag, vcodes[4 * j: 4 * j + 4, 8 * n + 4 * P: 8 * n + 4 * P + 4].T)
 
 
 def test_append_then_gather_paged_equals_contiguous():
@@ -264,8 +297,10 @@ def test_export_rows_reads_the_tile_bytes_and_matches_gather():
     tile = (11 * hkv + h) * 4224
     rows = G.export_rows(c, table, max_blocks, 0, 30, 20)  # positions 30..49, unaligned both ends
     row = rows[pos - 30, h]
-    np.testing.assert_array_equal(row[:128], flat[tile + 5 * 128: tile + 6 * 128])
-    np.testing.assert_array_equal(row[128:256], [flat[tile + 2048 + (5 // 4) * 512 + d * 4 + 5 % 4] for d in range(128)])
+    kd = [(d // 16 % 2) * 1024 + (5 + 16 * (d // 32)) * 16 + d % 16 for d in range(128)]  # key 5 of the tile
+    vd = [2048 + (d // 4 % 2) * 1024 + (d // 8 + 16 * (5 // 4)) * 16 + d % 4 * 4 + 5 % 4 for d in range(128)]
+    np.testing.assert_array_equal(row[:128], flat[tile + np.array(kd)])
+    np.testing.assert_array_equal(row[128:256], flat[tile + np.array(vd)])
     np.testing.assert_array_equal(row[256:260], flat[tile + 4096 + 20: tile + 4096 + 24])
     np.testing.assert_array_equal(row[260:264], flat[tile + 4160 + 20: tile + 4160 + 24])
     k, v, ks, vs = G.gather(c, table, max_blocks, np.array([64, 64]), 64)
@@ -387,7 +422,7 @@ def test_prefill_attention_reduces_to_decode_and_is_causal():
                                    scale)
             np.testing.assert_allclose(out[r0 + i], d[0], rtol=1e-12)
     # causality: changing keys after a row's position leaves that row unchanged
-    c.k[bt[0, 2], 0, 15] ^= 0x11  # position 47 of sequence 0
+    c.pages[bt[0, 2], 0, G.K_BYTES[15]] ^= 0x11  # position 47 of sequence 0
     out2 = G.prefill_attention(q, cu, start, c, bt, mb, -1, hq, hkv, scale)
     np.testing.assert_array_equal(out2[:15], out[:15])
     assert not np.array_equal(out2[15], out[15])
