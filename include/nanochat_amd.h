@@ -11,9 +11,11 @@
  * out of bounds.
  *
  * Cache layout (per layer), PAGE = 16 positions per block, D = 128: one pool, uint8 [num_blocks][Hkv][4224]; the
- * (block, kv head) tile is
- *   [0, 2048)     K codes [16][128], row-major
- *   [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + (t/4)*512 + d*4 + t%4
+ * (block, kv head) tile is four 1 KiB parts of 64 16-byte fragments (a wave's MFMA operands in lane order), then
+ * the scales:
+ *   [0, 2048)     K codes: key t, dim d at ((d/16)%2)*1024 + (t + 16*(d/32))*16 + d%16
+ *   [2048, 4096)  V codes, quad-transposed: key t, dim d at 2048 + ((d/4)%2)*1024 + (d/8 + 16*(t/4))*16 + (d%4)*4
+ *                 + t%4
  *   [4096, 4160)  K scales fp32 [16], one absmax/448 scale per (token, kv head)
  *   [4160, 4224)  V scales fp32 [16]
  *   block_table int32 [num_seqs][max_blocks], or NULL: contiguous, sequence s's page i is block s*max_blocks + i
