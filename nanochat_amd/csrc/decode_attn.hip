@@ -11,7 +11,7 @@
  *
  * Per page (16 keys) a wave computes
  *   scores  Sᵀ[16 keys][16 heads] = K[16][128] · Qᵀ, 4 v_mfma_f32_16x16x32_bf16. A is the K tile as loaded (lane:
- *           key lane%16, 32 contiguous bytes at dims 32 (lane/16)), fp8 -> bf16 exact by
+ *           key lane%16, dims 32 (lane/16) .. + 31, its fragments of the tile's parts 0 and 1), fp8 -> bf16 exact by
  *           v_cvt_scalef32_pk_bf16_fp8; B is q (bf16), head = lane%16 (zero past G). Lane (j = lane/16,
  *           n = lane%16) receives keys 4j..4j+3 for head n.
  *   softmax fp32, base 2 (scores times k_scale · sm_scale · log2 e). The reference max m of a head moves only
@@ -21,10 +21,12 @@
  *           4 probabilities times v_scale times 2^(126 - e_ref), e_ref the largest v_scale exponent seen (so the
  *           factor is <= 256 and fits fp16 with 11-bit precision; bf16 probabilities measurably miss the
  *           benchmark's max-error bound on outlier data). Vᵀ comes straight from the quad-transposed V tile:
- *           lane (j, n) loads the 32 bytes of dims 8n..8n+7 for keys 4j..4j+3; dword bb is one MFMA's A operand.
+ *           lane (j, n) holds the 32 bytes of dims 8n..8n+7 for keys 4j..4j+3 (its fragments of parts 2 and 3);
+ *           dword bb is one MFMA's A operand.
  *           The accumulator lane holds head n, so rescales are lane-local.
  * DEC_DEPTH page buffers rotate in registers (DEC_DEPTH - 1 pages in flight while one is computed), one wave per
- * SIMD: with two, the older wave wins issue arbitration and the younger finishes its equal share ~1.6x later.
+ * SIMD: with two, the older wave wins issue arbitration and the younger finishes its equal share ~1.6x later. A
+ * page is six nontemporal loads per lane; each code load of the wave reads one contiguous 1 KiB part of the tile.
  *
  * A piece covering its whole segment writes the normalised bf16 output. Otherwise it writes (Σ p v, max, sum)
  * to a workspace slot, and k_merge, launched next, combines a segment's slots with weights exp2(m_s - max m)
