@@ -5,8 +5,9 @@ Workload (config 3): batch 64, 16 query / 4 kv heads, head dim 128, prior contex
 (seeded), fp8 e4m3 K/V in 16-token pages under a random block permutation, values N(0,1) with 1 % outliers at
 8σ. A step appends one token to every sequence (QK-norm + RoPE + quantise) and runs decode attention over the fp8
 cache, new keys included: one nc_decode_step_fp8 call (the append fused into the attention kernel; --unfused: an
-nc_kv_append_fp8 call, then nc_decode_attn_fp8). Each step also writes the next positions, pos + 1; two steps
-(positions ping-ponging between two tensors) are captured in a HIP graph and replayed.
+nc_kv_append_fp8 call, then nc_decode_attn_fp8). Each step also writes the next positions, pos + 1; ten steps
+(positions ping-ponging between two tensors) are captured in a HIP graph and replayed, as a decoder captures a
+whole multi-layer step.
 
 Output: one JSON line. value = algorithmic attention bytes per step / measured step time (GB/s, inputs resident in
 HBM); roofline = the step's attention call (k_decode, then k_merge): the timed steps themselves (one
@@ -38,6 +39,7 @@ METRIC = "decode-attn HBM GB/s (% of peak) + decode tokens/sec, bs64 ctx8K"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFS = 2500.0  # dense bf16 / fp16 MFMA, MI355X
 ATTN_REPS = 10  # decode-attention calls per timed graph replay: the replay-to-replay gap is not kernel time
+STEP_GROUP = 10  # fused decode steps per timed graph replay (even: the positions ping-pong between two tensors)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_attn_traffic.json")
 
 
@@ -554,12 +556,19 @@ def main():
     step = unfused if args.unfused else fused
 
     stream = torch.cuda.Stream(dev)
-    graph_ab, graph_a, attn_graph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    # STEP_GROUP steps per graph, as a decoder captures a whole multi-layer step (the gap between two graph
+    # replays is host launch latency, not kernel time); graph_ab and graph_a take the remainder
+    graph_n, graph_ab, graph_a = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    attn_graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         # eager warm-up of every launch path before capture: two steps, positions back in p0
         step(p0, p1)
         step(p1, p0)
         stream.synchronize()
+        with torch.cuda.graph(graph_n, stream=stream):
+            for _ in range(STEP_GROUP // 2):
+                step(p0, p1)
+                step(p1, p0)
         with torch.cuda.graph(graph_ab, stream=stream):
             step(p0, p1)
             step(p1, p0)
@@ -575,7 +584,9 @@ def main():
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
-        for _ in range(steps // 2):
+        for _ in range(steps // STEP_GROUP):
+            graph_n.replay()
+        for _ in range(steps % STEP_GROUP // 2):
             graph_ab.replay()
         if steps % 2:
             graph_a.replay()
@@ -631,7 +642,7 @@ def main():
                    "step": ("nc_kv_append_fp8 + nc_decode_attn_fp8" if args.unfused else
                             "nc_decode_step_fp8 (append fused into the attention kernel)") +
                            ": append 1 token/seq (qk-norm+rope+fp8 quantise, emitting the next positions) + split-K "
-                           "decode attention, one attention layer, graph replays of two steps"},
+                           f"decode attention, one attention layer, graph replays of {STEP_GROUP} steps"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_one_layer": round(B / (step_ms * 1e-3), 1),
         "attention_only": {"kernel": attn_kernel, "call_us": round(attn_ms * 1e3, 3),
