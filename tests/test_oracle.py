@@ -220,6 +220,16 @@ def test_cache_layout_byte_offsets():
     assert np.count_nonzero(flat) == 127 + 128 + 1 + 2
 
 
+def test_host_byte_tables_match_the_layout():
+    """nanochat_amd.kv_cache's K_BYTES / V_BYTES (what host code indexes the device pool with) are the oracle's, and
+    the two tables cover a tile's 4096 code bytes once each."""
+    from nanochat_amd.kv_cache import K_BYTES, V_BYTES
+    np.testing.assert_array_equal(K_BYTES.numpy(), G.K_BYTES)
+    np.testing.assert_array_equal(V_BYTES.numpy(), G.V_BYTES)
+    both = np.concatenate([G.K_BYTES.ravel(), G.V_BYTES.ravel()])
+    np.testing.assert_array_equal(np.sort(both), np.arange(4096))
+
+
 def test_cache_parts_are_the_lanes_mfma_fragments():
     """Each 1 KiB part of a tile, read as [64 lanes][16 B], is what lane f = n + 16 j holds for the MFMAs: K part P,
     key n, dims 32 j + 16 P .. + 15 (16x16x32 A operand: row n, k slots of group j); V part 2 + P, dims
