@@ -1,0 +1,275 @@
+"""Pins of oracle/model.py's CpuModel (the config-5 and end-to-end checker) on the CPU, against references that share
+none of its code:
+
+* an independent dense forward written from inference/modeling_nanochat.py:120-175's order (embed, norm, per-layer
+  residual / x0 mix, attention with QK-norm + RoPE and the value-embedding gate, MLP with its own norm, final norm,
+  untied head), over whole sequences at once with explicit causal / sliding-window masks, GQA by repeating kv heads,
+  and unquantised bf16 K/V; the CpuModel (fp8 cache, fp64 attention) must agree within the fp8 quantisation's
+  effect on the logits, and every planted structural slip (on the CPU, in a subclass of the oracle) must not;
+* a known answer: with every projection weight zero, attention and MLP add nothing, so the logits are
+  norm(h_L) · lm_headᵀ, h_L the residual / x0 mix chain applied to x0 = norm(embed(token)); with the identity mix
+  that is norm(x0) · lm_headᵀ.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nanochat_amd.decoder import ModelConfig, RandomModel
+from oracle.model import CpuModel
+
+EPS = float(torch.finfo(torch.float32).eps)
+D = 128
+
+# GQA (4 query heads on 2 kv heads), a sliding-window layer, a value-embedding layer, a non-identity mix
+CFG = ModelConfig(layers=3, d_model=256, heads=4, vocab=512, theta=1e4, windows=(5, -1, 3), ve_layers=(1,),
+                  n_kv_heads=2)
+
+
+def model(cfg=CFG, seed=21, std=0.06):
+    """Weights large enough (std ~ 1/sqrt(d)) that every sublayer moves the residual stream visibly."""
+    m = RandomModel(cfg, "cpu", seed=seed, std=std)
+    g = torch.Generator().manual_seed(seed + 1)
+    m.resid_lambdas = 0.7 + 0.6 * torch.rand(cfg.layers, generator=g)
+    m.x0_lambdas = 0.3 + 0.3 * torch.rand(cfg.layers, generator=g)
+    for lw in m.layers:
+        lw["q_gain"] = 0.5 + torch.rand(D, generator=g)
+        lw["k_gain"] = 0.5 + torch.rand(D, generator=g)
+        if "ve_gate" in lw:
+            lw["ve_gate"] = torch.randn(lw["ve_gate"].shape, generator=g) * 0.2
+            lw["ve"] = (torch.randn(lw["ve"].shape, generator=g) * 0.8).to(torch.bfloat16)
+    return m
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 and back to fp32 (a bf16 tensor of the reference's forward)."""
+    return x.to(torch.bfloat16).float()
+
+
+def rms(x: torch.Tensor) -> torch.Tensor:
+    return x * torch.rsqrt(x.square().mean(-1, keepdim=True) + EPS)
+
+
+def fp8_rows(x: torch.Tensor) -> torch.Tensor:
+    """Per-row absmax fp8 e4m3 round trip (BASELINE.json's cache scheme) with torch's own cast: scale = absmax / 448,
+    x -> e4m3(x / scale) * scale; a zero row stays zero."""
+    scale = x.abs().amax(-1, keepdim=True) / 448
+    q = torch.where(scale > 0, x / torch.where(scale > 0, scale, 1), 0)
+    return q.to(torch.float8_e4m3fn).float() * scale
+
+
+def dense_logits(m, ids: np.ndarray, fp8_kv: bool = False) -> torch.Tensor:
+    """The reference model's forward over whole sequences ids [B][T]: fp32 logits [B][T][vocab]. Activations are
+    rounded to bf16 where the reference's bf16 tensors hold them; attention scores and softmax in fp32 over bf16
+    q, k, v; K/V unquantised, or with fp8_kv each (token, kv head) row of K and V through fp8_rows."""
+    cfg = m.cfg
+    B, T = ids.shape
+    H, Hk, C = cfg.heads, cfg.kv_heads, cfg.heads * D
+    ids_t = torch.from_numpy(ids.astype(np.int64))
+    pos = torch.arange(T, dtype=torch.float64)
+    freqs = pos[:, None] * cfg.theta ** -(torch.arange(0, D, 2, dtype=torch.float64) / D)
+    cos, sin = freqs.cos().float(), freqs.sin().float()  # [T][64]
+
+    def qk(x, gain):  # x [B][T][h][D] bf16 values
+        y = rms(x) * gain
+        y1, y2 = y[..., :D // 2], y[..., D // 2:]
+        c, s = cos[None, :, None, :], sin[None, :, None, :]
+        return bf(torch.cat([y1 * c + y2 * s, y2 * c - y1 * s], -1))
+
+    def lin(x, w):
+        return bf(x @ w.float().t())
+
+    x0 = bf(rms(m.wte.float()[ids_t]))
+    h = x0
+    qi, ki = torch.arange(T)[:, None], torch.arange(T)[None, :]
+    for i, lw in enumerate(m.layers):
+        h = bf(m.resid_lambdas[i] * h + m.x0_lambdas[i] * x0)
+        n = bf(rms(h))
+        qkv = lin(n, lw["wqkv"])
+        q = qkv[..., :C].reshape(B, T, H, D)
+        k = qkv[..., C:C + Hk * D].reshape(B, T, Hk, D)
+        v = qkv[..., C + Hk * D:].reshape(B, T, Hk, D)
+        if "ve" in lw:
+            gate = 2 * torch.sigmoid(n @ lw["ve_gate"].float().t())  # [B][T][Hk]
+            v = bf(v + gate[..., None] * lw["ve"].float()[ids_t].reshape(B, T, Hk, D))
+        q, k = qk(q, lw["q_gain"]), qk(k, lw["k_gain"])
+        if fp8_kv:
+            k, v = fp8_rows(k), fp8_rows(v)
+        rep = H // Hk
+        k, v = k.repeat_interleave(rep, dim=2), v.repeat_interleave(rep, dim=2)  # head j reads kv head j // rep
+        s = torch.einsum("bqhd,bkhd->bhqk", q, k) * D ** -0.5
+        w = cfg.window(i)
+        allowed = (ki <= qi) & ((qi - ki <= w) if w >= 0 else True)
+        p = s.masked_fill(~allowed, float("-inf")).softmax(-1)
+        o = bf(torch.einsum("bhqk,bkhd->bqhd", p, v)).reshape(B, T, C)
+        h = bf(h + lin(o, lw["wo"]))
+        u = lin(bf(rms(h)), lw["wup"])
+        h = bf(h + lin(bf(F.relu(u).square()), lw["wdown"]))
+    return bf(rms(h)) @ m.lm_head.float().t()
+
+
+def cpu_logits(cpu: CpuModel, ids: np.ndarray, T: int, extra: int) -> list[np.ndarray]:
+    """The CpuModel's logits at positions T-1 .. T-1+extra of ids [B][T + extra]: prefill of positions 0..T-2, then
+    one step per position, each fed the sequence's own next token."""
+    cpu.prefill(ids[:, :T])
+    return [cpu.step(ids[:, T - 1 + s].copy(), T - 1 + s) for s in range(extra + 1)]
+
+
+T_PROMPT, EXTRA = 10, 3
+
+
+def compare(cpu_cls, m=None, fp8_kv: bool = True) -> tuple[float, float]:
+    """Max and mean |CpuModel − dense| over the compared positions, relative to the logits' spread."""
+    m = model() if m is None else m
+    ids = np.random.default_rng(5).integers(0, m.cfg.vocab, (2, T_PROMPT + EXTRA)).astype(np.int64)
+    want = dense_logits(m, ids, fp8_kv).numpy()
+    got = cpu_logits(cpu_cls(m, 2, T_PROMPT + EXTRA + 1), ids, T_PROMPT, EXTRA)
+    err = np.stack([np.abs(g - want[:, T_PROMPT - 1 + s]) for s, g in enumerate(got)])
+    scale = want[:, T_PROMPT - 1:].std()
+    return float(err.max() / scale), float(err.mean() / scale)
+
+
+# Measured at this size: the CpuModel against the dense forward with the same fp8 round trip of K and V: max 0.036,
+# mean 0.0036 of the logits' spread (fp64 against fp32 attention, the QK-norm's rounding rule, bf16 summation
+# orders); against unquantised bf16 K/V: max 0.108, mean 0.018 (the fp8 cache's own effect). The smallest planted
+# slip (the value-embedding gate's factor 2) moves them by max 0.31, mean 0.070.
+MAX_REL, MEAN_REL = 0.08, 0.01
+FP8_MAX_REL, FP8_MEAN_REL = 0.2, 0.04
+
+
+def test_cpu_model_matches_dense_reference():
+    mx, mean = compare(CpuModel)
+    print(f"CpuModel vs dense (fp8 K/V): max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+def test_cpu_model_within_the_fp8_cache_effect_of_bf16_kv():
+    mx, mean = compare(CpuModel, fp8_kv=False)
+    print(f"CpuModel vs dense (bf16 K/V): max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx <= FP8_MAX_REL and mean <= FP8_MEAN_REL, (mx, mean)
+
+
+def _mlp_norm_of_input_layer(self, l, x, pos, seq, tok, attend):
+    import oracle.golden as G
+    from oracle.model import bits, cpu_norm
+
+    lw, cfg = self.w[l], self.cfg
+    n = cpu_norm(x)
+    qkv = n @ lw["wqkv"].t()
+    if "ve" in lw:
+        H = cfg.kv_heads
+        gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))
+        v = qkv[:, (cfg.heads + H) * 128:].reshape(-1, H, 128)
+        ve = lw["ve"][torch.from_numpy(np.asarray(tok, np.int64))].reshape(-1, H, 128)
+        qkv[:, (cfg.heads + H) * 128:] = (v.float() + gate[..., None] * ve.float()).to(torch.bfloat16).flatten(1)
+    q = G.append(self.caches[l], bits(qkv), pos, seq, lw["q_gain"].numpy(), lw["k_gain"].numpy(), self.cos,
+                 self.sin, cfg.heads, cfg.kv_heads, None, self.max_blocks)
+    o = torch.from_numpy(attend(q, self.caches[l]).astype(np.float32)).to(torch.bfloat16)
+    h = x + o.reshape(o.shape[0], -1) @ lw["wo"].t()
+    u = (n @ lw["wup"].t()).float().relu().square().to(torch.bfloat16)  # the slip: n, not norm(h)
+    return h + u @ lw["wdown"].t()
+
+
+class MlpNormOfLayerInput(CpuModel):
+    """Slip: the MLP's norm taken of the layer's input instead of the stream after the attention's residual."""
+
+    _layer = _mlp_norm_of_input_layer
+
+
+class SwappedMix(CpuModel):
+    """Slip: the mix's two weights exchanged."""
+
+    def _mix(self, l, x, x0):
+        return (self.l0[l] * x.float() + self.lr[l] * x0.float()).to(torch.bfloat16)
+
+
+class MixIgnoresX0(CpuModel):
+    """Slip: the x0 term of the mix dropped."""
+
+    def _mix(self, l, x, x0):
+        return (self.lr[l] * x.float()).to(torch.bfloat16)
+
+
+class NoFinalNorm(CpuModel):
+    """Slip: the head reads the stream without the final norm."""
+
+    def step(self, tok, position):
+        return self._step_no_final(tok, position)
+
+    def _step_no_final(self, tok, position):
+        import oracle.golden as G
+        from oracle.model import cpu_norm
+
+        B = self.batch
+        pos, seq = np.broadcast_to(np.asarray(position), (B,)).copy(), np.arange(B)
+        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
+        for l in range(self.cfg.layers):
+            w = self.cfg.window(l)
+            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.decode_attention(
+                q, c, None, self.max_blocks, pos + 1, w, self.cfg.heads, self.cfg.kv_heads, 128 ** -0.5))
+        return (x.float() @ self.lm_head.float().t()).numpy()
+
+
+class VeGateWithoutFactor2(CpuModel):
+    """Slip: the value-embedding gate σ(W n) instead of 2 σ(W n)."""
+
+    def _layer(self, l, x, pos, seq, tok, attend):
+        if "ve_gate" in self.w[l]:
+            saved = self.w[l]["ve"]
+            self.w[l]["ve"] = (saved.float() / 2).to(torch.bfloat16)
+            try:
+                return super()._layer(l, x, pos, seq, tok, attend)
+            finally:
+                self.w[l]["ve"] = saved
+        return super()._layer(l, x, pos, seq, tok, attend)
+
+
+class WindowOffByOne(CpuModel):
+    """Slip: a window of w keys before the query read as w - 1."""
+
+    def __init__(self, model, batch, max_len):
+        super().__init__(model, batch, max_len)
+        from dataclasses import replace
+
+        self.cfg = replace(self.cfg, windows=tuple(w - 1 if w > 0 else w for w in self.cfg.windows))
+
+
+@pytest.mark.parametrize("slip", [MlpNormOfLayerInput, SwappedMix, MixIgnoresX0, NoFinalNorm, VeGateWithoutFactor2,
+                                  WindowOffByOne], ids=lambda c: c.__name__)
+def test_dense_reference_catches_structural_slips(slip):
+    """Each slip fails the bar test_cpu_model_matches_dense_reference holds the CpuModel to."""
+    mx, mean = compare(slip)
+    print(f"{slip.__name__}: max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx > MAX_REL or mean > MEAN_REL, f"{slip.__name__} passed the comparison: the test does not pin it"
+
+
+def zero_projection_model(identity_mix: bool):
+    m = model(seed=31)
+    for lw in m.layers:
+        for k in ("wqkv", "wo", "wup", "wdown"):
+            lw[k] = torch.zeros_like(lw[k])
+    if identity_mix:
+        m.resid_lambdas = torch.ones(m.cfg.layers)
+        m.x0_lambdas = torch.zeros(m.cfg.layers)
+    return m
+
+
+@pytest.mark.parametrize("identity_mix", [True, False])
+def test_zero_projections_known_answer(identity_mix):
+    """Every projection zero: q = k = v = 0 (the value embedding's term reaches v but o W_o = 0), so each layer only
+    mixes; logits = norm(h_L) · lm_headᵀ with h_0 = x0 = norm(embed(tok)) and h_(l+1) = bf16(λr_l h_l + λ0_l x0).
+    With the identity mix the logits are norm(x0) · lm_headᵀ."""
+    m = zero_projection_model(identity_mix)
+    tok = np.array([3, 77, 500], dtype=np.int64)
+    cpu = CpuModel(m, 3, 8)
+    got = cpu.step(tok, 0)
+    x0 = bf(F.rms_norm(m.wte.float()[torch.from_numpy(tok)], (m.cfg.d_model,), eps=EPS))
+    h = x0
+    for i in range(m.cfg.layers):
+        h = bf(m.resid_lambdas[i] * h + m.x0_lambdas[i] * x0)
+    want = (bf(F.rms_norm(h, (m.cfg.d_model,), eps=EPS)) @ m.lm_head.float().t()).numpy()
+    if identity_mix:
+        np.testing.assert_array_equal(bf(h).numpy(), x0.numpy())
+    # the head's fp32 GEMM is the only inexact step: summation order
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
