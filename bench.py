@@ -39,7 +39,8 @@ METRIC = "decode-attn HBM GB/s (% of peak) + decode tokens/sec, bs64 ctx8K"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFS = 2500.0  # dense bf16 / fp16 MFMA, MI355X
 ATTN_REPS = 10  # decode-attention calls per timed graph replay: the replay-to-replay gap is not kernel time
-STEP_GROUP = 10  # fused decode steps per timed graph replay (even: the positions ping-pong between two tensors)
+POOLS = 2  # distinct cache pools (layers) the timed steps alternate between, so each step reads its pool cold
+STEP_GROUP = 12  # decode steps per timed graph replay: whole cycles of the pools' position ping-pong (2 x POOLS)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_attn_traffic.json")
 
 
@@ -52,7 +53,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
-    ap.add_argument("--only", choices=["decode2", "prefill4", "e2e5", "handle5"],
+    ap.add_argument("--only", choices=["decode1", "decode2", "prefill4", "e2e5", "handle5"],
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
     ap.add_argument("--unfused", action="store_true",
@@ -224,26 +225,79 @@ def time_calls(fn, calls: int, replays: int, stream) -> float:
 
 
 def extra_decode_cfg2(dev, stream, cpu_s: float | None = None) -> dict:
-    """Config 2 (B 32, 10/10 heads, ctx 4096 contiguous): one decode-attention call after the step's append; with
-    cpu_s, the oracle's CPU leg on a bounded sample of the same sequences."""
+    """Config 2 (B 32, 10/10 heads, ctx 4096 contiguous): the decode-attention call after the step's append, over
+    POOLS pools in turn (each read cold, as in a model); with cpu_s, the oracle's CPU leg on a bounded sample of the
+    same sequences."""
     from nanochat_amd.attention import decode_attention, decode_workspace
     from nanochat_amd.workloads import CONFIG2, build_decode_case, decode_bytes
 
     cfg = CONFIG2
-    case = build_decode_case(cfg, dev, steps=1)
+    cases = [build_decode_case(cfg, dev, steps=1) for _ in range(POOLS)]
+    case = cases[0]
     pos = case.positions(0)
-    q = case.cache.append(case.qkv[0], pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    qs = [c.cache.append(c.qkv[0], pos, c.seq, c.q_gain, c.k_gain, c.cos, c.sin, cfg.hq) for c in cases]
     ctx = pos + 1
     ws = decode_workspace(cfg.batch, cfg.hq, cfg.hkv, case.cache.capacity, dev)
-    out = torch_empty_like(q)
-    ms = time_calls(lambda: decode_attention(q, case.cache, ctx, max_ctx=case.cache.capacity, out=out, workspace=ws),
-                    ATTN_REPS, 20, stream)
+    out = torch_empty_like(qs[0])
+    turn = [0]
+
+    def call():
+        k = turn[0] % POOLS
+        turn[0] += 1
+        decode_attention(qs[k], cases[k].cache, ctx, max_ctx=case.cache.capacity, out=out, workspace=ws)
+
+    ms = time_calls(call, ATTN_REPS, 20, stream)
     nbytes = decode_bytes(case.ctx + 1, cfg.hkv, cfg.window)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    res = {"workload": cfg.name, "attn_us": round(ms * 1e3, 3), "bytes": int(nbytes), "GB_s": round(gbs, 2),
-           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    res = {"workload": cfg.name, "pools": POOLS, "attn_us": round(ms * 1e3, 3), "bytes": int(nbytes),
+           "GB_s": round(gbs, 2), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if cpu_s:
-        res["cpu_baseline"] = cpu_decode(case, case.ctx + 1, q, cpu_s, gbs)
+        res["cpu_baseline"] = cpu_decode(case, case.ctx + 1, qs[0], cpu_s, gbs)
+    return res
+
+
+def extra_decode_cfg1(dev, stream, cpu_s: float | None = None) -> dict:
+    """Config 1 (CPU plumbing: B 1, 6/6 heads, 1024 cached tokens + 1 appended, θ 1e6): the fused step on the GPU (a
+    launch-bound figure, reported for completeness) and, with cpu_s, the oracle's append + decode attention on the
+    host (1 warm-up, median of the timed calls)."""
+    import math
+
+    from nanochat_amd.attention import decode_step, decode_workspace
+    from nanochat_amd.workloads import CONFIG1, build_decode_case, decode_bytes
+    from oracle import golden as G
+
+    cfg = CONFIG1
+    case = build_decode_case(cfg, dev, steps=1)
+    host, _ = _host_cache(case.cache)
+    pos = case.positions(0)
+    max_ctx = int(case.ctx.max()) + 1
+    ws = decode_workspace(cfg.batch, cfg.hq, cfg.hkv, max_ctx, dev)
+    out = torch_empty_like(case.qkv[0][:, :cfg.hq * 128].reshape(cfg.batch, cfg.hq, 128))
+    ms = time_calls(lambda: decode_step(case.qkv[0], case.cache, pos, case.q_gain, case.k_gain, case.cos, case.sin,
+                                        cfg.hq, max_ctx=max_ctx, out=out, workspace=ws), ATTN_REPS, 20, stream)
+    nbytes = decode_bytes(case.ctx + 1, cfg.hkv, cfg.window)
+    res = {"workload": cfg.name, "step_us": round(ms * 1e3, 3), "bytes": int(nbytes),
+           "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 2), "note": "1.6 MB per step: launch-bound, not a bandwidth figure"}
+    if cpu_s:
+        qkv = _q_bits(case.qkv[0])
+        p = pos.cpu().numpy()
+        args = (case.q_gain.cpu().numpy(), case.k_gain.cpu().numpy(), case.cos.cpu().numpy(), case.sin.cpu().numpy())
+
+        def call():
+            c = G.PagedCache(host.pages.shape[0], cfg.hkv)
+            c.pages[...] = host.pages
+            qr = G.append(c, qkv, p, np.arange(cfg.batch), *args, cfg.hq, cfg.hkv, None, case.cache.max_blocks)
+            G.decode_attention(qr, c, None, case.cache.max_blocks, p + 1, cfg.window, cfg.hq, cfg.hkv,
+                               1 / math.sqrt(128))
+
+        from threadpoolctl import threadpool_limits
+
+        with threadpool_limits(limits=1):
+            med, times = cpu_timed(call, cpu_s)
+        res["cpu_baseline"] = {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                               "sample": f"the whole config: oracle append (numpy) + decode attention (fp64), 1 "
+                                         f"warm-up call, median of {len(times)} timed calls ({med * 1e3:.1f} ms)",
+                               "call_ms": round(med * 1e3, 2), "host": host_info()}
     return res
 
 
@@ -401,9 +455,29 @@ def _host_cache(cache):
     return host, table
 
 
+CPU_CALLS = 5  # timed calls of every CPU leg after one warm-up call; the median is reported
+
+
+def cpu_timed(call, budget_s: float) -> tuple[float, list[float]]:
+    """One warm-up call, then CPU_CALLS timed calls (more while the budget lasts, up to 9); (median s, times)."""
+    call()
+    times, t_all = [], time.perf_counter()
+    while len(times) < CPU_CALLS or (len(times) < 9 and time.perf_counter() - t_all < budget_s / 2):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times
+
+
+def cpu_sample(one_cost: float, n: int, budget_s: float) -> int:
+    """How many of n equal units (one measured at one_cost s) fit a call of budget_s / (CPU_CALLS + 1)."""
+    return int(max(1, min(n, (budget_s / (CPU_CALLS + 1)) // max(one_cost, 1e-9))))
+
+
 def cpu_decode(case, final_ctx: np.ndarray, q, budget_s: float, gpu_gbs: float) -> dict:
-    """The oracle's decode attention (numpy, fp64 over the dequantised cache) on whole sequences of the same cache,
-    in order, until budget_s of work; GB/s over the same algorithmic bytes as the GPU figure."""
+    """The oracle's decode attention (numpy, fp64 over the dequantised cache) on the first sequences of the same
+    cache (as many as let 1 warm-up + CPU_CALLS timed calls fit budget_s); the median call, in GB/s over the same
+    algorithmic bytes as the GPU figure."""
     import math
 
     from threadpoolctl import threadpool_limits
@@ -416,27 +490,33 @@ def cpu_decode(case, final_ctx: np.ndarray, q, budget_s: float, gpu_gbs: float) 
     host, table = _host_cache(cache)
     qb = _q_bits(q)
     cfg = case.cfg
-    done, t_total = 0, 0.0
+
+    def call(n):
+        G.decode_attention(qb[:n], host, table[:n] if table is not None else None, cache.max_blocks,
+                           final_ctx[:n], cfg.window, cfg.hq, cfg.hkv, 1 / math.sqrt(128))
+
     with threadpool_limits(limits=cores):
-        while done < cfg.batch and t_total < budget_s:
-            b = done
-            t0 = time.perf_counter()
-            G.decode_attention(qb[b:b + 1], host, table[b:b + 1] if table is not None else None, cache.max_blocks,
-                               final_ctx[b:b + 1], cfg.window, cfg.hq, cfg.hkv, 1 / math.sqrt(128))
-            t_total += time.perf_counter() - t0
-            done += 1
-    nbytes = decode_bytes(final_ctx[:done], cfg.hkv, cfg.window)
-    value = nbytes / t_total / 1e9
+        t0 = time.perf_counter()
+        call(1)
+        per_key = (time.perf_counter() - t0) / final_ctx[0]
+        n, acc = 0, 0.0  # sequences whose keys fit one call's share of the budget
+        while n < cfg.batch and (acc + final_ctx[n] * per_key <= budget_s / (CPU_CALLS + 1) or n == 0):
+            acc += final_ctx[n] * per_key
+            n += 1
+        med, times = cpu_timed(lambda: call(n), budget_s)
+    nbytes = decode_bytes(final_ctx[:n], cfg.hkv, cfg.window)
+    value = nbytes / med / 1e9
     return {"value": round(value, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"oracle decode attention (numpy fp64 over dequantised fp8) of the first {done} of "
-                      f"{cfg.batch} sequences ({int(final_ctx[:done].sum())} keys x {cfg.hkv} kv heads), "
-                      f"{t_total:.1f} s",
+            "sample": f"oracle decode attention (numpy fp64 over dequantised fp8) of the first {n} of {cfg.batch} "
+                      f"sequences ({int(final_ctx[:n].sum())} keys x {cfg.hkv} kv heads) per call; 1 warm-up call, "
+                      f"median of {len(times)} timed calls ({med:.2f} s, range {min(times):.2f}-{max(times):.2f} s)",
             "speedup_gpu_over_cpu": round(gpu_gbs / value, 1), "host": host_info()}
 
 
 def cpu_prefill(case, q, budget_s: float, gpu_tfs: float) -> dict:
-    """The oracle's prefill attention (numpy fp64 over the dequantised cache) on the rows of whole sequences of the
-    same chunk, in order, until budget_s of work; TFLOP/s over the same algorithmic flops as the GPU figure."""
+    """The oracle's prefill attention (numpy fp64 over the dequantised cache) on the chunk rows of the first
+    sequences (as many as let 1 warm-up + CPU_CALLS timed calls fit budget_s); the median call, in TFLOP/s over the
+    same algorithmic flops as the GPU figure."""
     import math
 
     from threadpoolctl import threadpool_limits
@@ -449,20 +529,25 @@ def cpu_prefill(case, q, budget_s: float, gpu_tfs: float) -> dict:
     host, table = _host_cache(case.cache)
     qb = _q_bits(q)
     pos, seq = case.pos.cpu().numpy(), case.seq.cpu().numpy()
-    done, t_total, flops = 0, 0.0, 0
+
+    def call(n):
+        rows = np.nonzero(seq < n)[0]
+        G.rows_attention(qb[rows], pos[rows], seq[rows], host, table, case.cache.max_blocks, cfg.batch,
+                         cfg.window, cfg.hq, cfg.hkv, 1 / math.sqrt(128))
+        return rows
+
     with threadpool_limits(limits=cores):
-        while done < cfg.batch and t_total < budget_s:
-            rows = np.nonzero(seq == done)[0]
-            t0 = time.perf_counter()
-            G.rows_attention(qb[rows], pos[rows], seq[rows], host, table, case.cache.max_blocks, cfg.batch,
-                             cfg.window, cfg.hq, cfg.hkv, 1 / math.sqrt(128))
-            t_total += time.perf_counter() - t0
-            flops += prefill_flops(pos[rows], cfg.hq, cfg.window)
-            done += 1
-    value = flops / t_total / 1e12
+        t0 = time.perf_counter()
+        call(1)
+        n = cpu_sample(time.perf_counter() - t0, cfg.batch, budget_s)
+        med, times = cpu_timed(lambda: call(n), budget_s)
+    rows = np.nonzero(seq < n)[0]
+    flops = prefill_flops(pos[rows], cfg.hq, cfg.window)
+    value = flops / med / 1e12
     return {"value": round(value, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"oracle prefill attention (numpy fp64 over dequantised fp8) of the chunk rows of the first "
-                      f"{done} of {cfg.batch} sequences ({flops:.3e} flop), {t_total:.1f} s",
+            "sample": f"oracle prefill attention (numpy fp64 over dequantised fp8) of the chunk rows of the first {n} "
+                      f"of {cfg.batch} sequences ({flops:.3e} flop) per call; 1 warm-up call, median of {len(times)} "
+                      f"timed calls ({med:.2f} s, range {min(times):.2f}-{max(times):.2f} s)",
             "speedup_gpu_over_cpu": round(gpu_tfs / value, 1), "host": host_info()}
 
 
@@ -478,7 +563,7 @@ def cpu_e2e(model, prompts, cfg, budget_s: float, gpu: dict) -> dict:
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     n_prompt, steps = cfg.prompt - 1, 8
-    cpu = CpuModel(model, 1, cfg.prompt + steps)
+    cpu = CpuModel(model, 1, cfg.prompt + steps + 1)
     ids = prompts[0].cpu().numpy().astype(np.int64)
     done, t0 = 0, time.perf_counter()
     while done < n_prompt and time.perf_counter() - t0 < budget_s * 2 / 3:
@@ -487,16 +572,20 @@ def cpu_e2e(model, prompts, cfg, budget_s: float, gpu: dict) -> dict:
         done += n
     prefill_s = time.perf_counter() - t0
     tok = ids[n_prompt:n_prompt + 1] if done == n_prompt else ids[done:done + 1]
-    t1 = time.perf_counter()
-    for i in range(steps):
+    times = []
+    for i in range(steps + 1):  # step 0 is the warm-up
+        t1 = time.perf_counter()
         tok = cpu.step(tok, done + i).argmax(1)
-    step_s = (time.perf_counter() - t1) / steps
+        if i:
+            times.append(time.perf_counter() - t1)
+    step_s = float(np.median(times))
     per_seq = prefill_s * n_prompt / done + cfg.steps * step_s
     total_s = cfg.batch * per_seq
     value = cfg.batch * cfg.steps / total_s
     return {"value": round(value, 3), "unit": "tokens/s", "cores": cores, "kind": "port", "extrapolated": True,
             "sample": f"oracle CPU model, sequence 0 only: {done} of its {n_prompt} prompt positions prefilled in "
-                      f"{prefill_s:.1f} s, then {steps} greedy steps at batch 1 ({step_s:.2f} s each); the full run "
+                      f"{prefill_s:.1f} s (one pass), then 1 warm-up and {steps} timed greedy steps at batch 1 (median "
+                      f"{step_s:.2f} s, range {min(times):.2f}-{max(times):.2f} s); the full run "
                       f"extrapolated as {cfg.batch} sequences one after another, prefill scaled to {n_prompt} rows "
                       f"and {cfg.steps} steps each: {total_s:.0f} s",
             "decode_tokens_per_s_batch1": round(1 / step_s, 3),
@@ -526,102 +615,137 @@ def main():
     if args.only:
         s = torch.cuda.Stream(dev)
         cpu_s = None if args.no_cpu else args.cpu_seconds
-        run = {"decode2": lambda: extra_decode_cfg2(dev, s, cpu_s), "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
+        run = {"decode1": lambda: extra_decode_cfg1(dev, s, cpu_s), "decode2": lambda: extra_decode_cfg2(dev, s, cpu_s),
+               "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
                "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s),
                "handle5": lambda: extra_e2e_cfg5_handle(dev, args.e2e_steps)}[args.only]
         print(json.dumps(run()), flush=True)
         return
     cfg = CONFIG3
     steps, warmup = args.steps, args.warmup
-    case = build_decode_case(cfg, dev, steps=steps + warmup + 2)
     B = cfg.batch
+    # POOLS layer pools at different addresses (the same seeded contents), stepped in turn: as in a model, where a
+    # layer's cache is read again only after the other layers' caches, no step finds its pages in the 256 MB
+    # memory-side cache (one pool is ~330 MB; two alternate with a whole pool read between two reads of each)
+    per_pool = (steps + warmup + 3 * STEP_GROUP) // POOLS + 4
+    cases = [build_decode_case(cfg, dev, steps=per_pool) for _ in range(POOLS)]
+    case = cases[0]
     max_ctx = case.cache.capacity
-    # positions ping-pong between two tensors: a step appends at pos and writes pos + 1 into the other tensor, the
-    # next step's positions (no position-advance kernel)
-    p0 = case.positions(0).contiguous()
-    p1 = torch.empty_like(p0)
+    # each pool's positions ping-pong between two tensors: a step appends at pos and writes pos + 1 into the other
+    # tensor, the pool's next positions (no position-advance kernel)
+    pos = [[c.positions(0).contiguous(), torch.empty_like(c.positions(0))] for c in cases]
     qkv = case.qkv[0].contiguous()
     ws = decode_workspace(B, cfg.hq, cfg.hkv, max_ctx, dev)
     out = torch.empty((B, cfg.hq, 128), dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
 
-    def fused(pos, nxt):
-        decode_step(qkv, case.cache, pos, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq, max_ctx=max_ctx,
-                    window=cfg.window, out=out, workspace=ws, pos_out=nxt)
+    def fused(c, p_in, p_out):
+        decode_step(qkv, c.cache, p_in, c.q_gain, c.k_gain, c.cos, c.sin, cfg.hq, max_ctx=max_ctx,
+                    window=cfg.window, out=out, workspace=ws, pos_out=p_out)
 
-    def unfused(pos, ctx):
-        q = case.cache.append(qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq, ctx_out=ctx)
-        decode_attention(q, case.cache, ctx, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+    def unfused(c, p_in, p_out):
+        q = c.cache.append(qkv, p_in, c.seq, c.q_gain, c.k_gain, c.cos, c.sin, cfg.hq, ctx_out=p_out)
+        decode_attention(q, c.cache, p_out, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
 
     step = unfused if args.unfused else fused
 
+    def phase_step(i: int) -> None:
+        """Step i of the cycle of 2 POOLS: pool i % POOLS, its positions forward (0 -> 1) or back (1 -> 0)."""
+        k, d = i % POOLS, (i // POOLS) % 2
+        step(cases[k], pos[k][d], pos[k][1 - d])
+
+    cycle = 2 * POOLS  # steps after which every pool's positions are back in their first tensor
     stream = torch.cuda.Stream(dev)
     # STEP_GROUP steps per graph, as a decoder captures a whole multi-layer step (the gap between two graph
-    # replays is host launch latency, not kernel time); graph_ab and graph_a take the remainder
-    graph_n, graph_ab, graph_a = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    # replays is host launch latency, not kernel time); graph_c (one cycle) and the single steps take the rest
+    graph_n, graph_c = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    singles = [torch.cuda.CUDAGraph() for _ in range(cycle)]
     attn_graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        # eager warm-up of every launch path before capture: two steps, positions back in p0
-        step(p0, p1)
-        step(p1, p0)
+        # eager warm-up of every launch path before capture: one cycle, positions back in their first tensors
+        for i in range(cycle):
+            phase_step(i)
         stream.synchronize()
         with torch.cuda.graph(graph_n, stream=stream):
-            for _ in range(STEP_GROUP // 2):
-                step(p0, p1)
-                step(p1, p0)
-        with torch.cuda.graph(graph_ab, stream=stream):
-            step(p0, p1)
-            step(p1, p0)
-        with torch.cuda.graph(graph_a, stream=stream):
-            step(p0, p1)
-    done = 2
-    for _ in range(warmup // 2):
-        graph_ab.replay()
-        done += 2
+            for i in range(STEP_GROUP):
+                phase_step(i)
+        with torch.cuda.graph(graph_c, stream=stream):
+            for i in range(cycle):
+                phase_step(i)
+        for i in range(cycle):
+            with torch.cuda.graph(singles[i], stream=stream):
+                phase_step(i)
+    done = cycle
+
+    def replay(n: int, at: int) -> int:
+        """n steps from cycle phase `at` (graph_n whenever the phase is 0); returns the phase after them."""
+        while n > 0:
+            if at == 0 and n >= STEP_GROUP:
+                graph_n.replay()
+                n -= STEP_GROUP
+            elif at == 0 and n >= cycle:
+                graph_c.replay()
+                n -= cycle
+            else:
+                singles[at].replay()
+                at, n = (at + 1) % cycle, n - 1
+        return at
+
+    with torch.cuda.stream(stream):
+        # warm-up: graph_n once (its first replay is not timed), then `warmup` steps, ending at phase 0
+        graph_n.replay()
+        w = warmup + (-warmup) % cycle
+        replay(w, 0)
+        done += STEP_GROUP + w
     stream.synchronize()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
-        for _ in range(steps // STEP_GROUP):
-            graph_n.replay()
-        for _ in range(steps % STEP_GROUP // 2):
-            graph_ab.replay()
-        if steps % 2:
-            graph_a.replay()
+        replay(steps, 0)
         e1.record(stream)
     e1.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
     wall = time.perf_counter() - t0
     torch.cuda.synchronize()
-    base = case.ctx + done  # keys before the timed steps (prior context + the appended tokens)
-    final_ctx = base + steps  # the keys of the last step
-    ctx_len = p1 if steps % 2 else p0  # the last step's context lengths: its positions + 1
-    with torch.cuda.stream(stream):
-        # the last step's queries (cpu_baseline); appending its tokens again rewrites the same cache bytes
-        q = case.cache.append(qkv, ctx_len - 1, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
-    step_bytes = np.mean([decode_bytes(base + i + 1, cfg.hkv, cfg.window) for i in range(steps)])
+    # keys before the timed steps per pool (prior context + the tokens each pool appended); timed step i is step
+    # i // POOLS of pool i % POOLS
+    base = case.ctx + done // POOLS
+    step_bytes = np.mean([decode_bytes(base + i // POOLS + 1, cfg.hkv, cfg.window) for i in range(steps)])
     value = step_bytes / (step_ms * 1e-3) / 1e9
-    # the attention call alone (the metric's decode kernel + split-K merge, without the append): ATTN_REPS calls at
-    # the last step's context in one graph
+    pool_steps = [(done + steps - k + POOLS - 1) // POOLS for k in range(POOLS)]  # steps each pool has taken
+    ctx_len = [pos[k][pool_steps[k] % 2] for k in range(POOLS)]  # each pool's last context lengths: positions + 1
+    final_ctx = [case.ctx + n for n in pool_steps]
     with torch.cuda.stream(stream):
-        decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+        # each pool's last queries (attention alone, cpu_baseline); appending them again rewrites the same bytes
+        qs = [c.cache.append(qkv, cl - 1, c.seq, c.q_gain, c.k_gain, c.cos, c.sin, cfg.hq)
+              for c, cl in zip(cases, ctx_len)]
+    q = qs[0]
+    # the attention call alone (the metric's decode kernel + split-K merge, without the append): ATTN_REPS calls
+    # in one graph, the pools in turn at their last contexts
+    with torch.cuda.stream(stream):
+        for k in range(POOLS):
+            decode_attention(qs[k], cases[k].cache, ctx_len[k], max_ctx=max_ctx, window=cfg.window, out=out,
+                             workspace=ws)
         stream.synchronize()
         with torch.cuda.graph(attn_graph, stream=stream):
-            for _ in range(ATTN_REPS):
-                decode_attention(q, case.cache, ctx_len, max_ctx=max_ctx, window=cfg.window, out=out, workspace=ws)
+            for r in range(ATTN_REPS):
+                k = r % POOLS
+                decode_attention(qs[k], cases[k].cache, ctx_len[k], max_ctx=max_ctx, window=cfg.window, out=out,
+                                 workspace=ws)
+        attn_graph.replay()
     attn_ms = replay_ms(attn_graph, max(steps // ATTN_REPS, 2), stream) / ATTN_REPS
-    attn_bytes = decode_bytes(final_ctx, cfg.hkv, cfg.window)
-    attn_kernel = (f"nc_decode_attn_fp8 = k_decode<false> + k_merge, a graph of {ATTN_REPS} calls at the last "
-                   "step's context, HIP events on their stream")
+    attn_bytes = np.mean([decode_bytes(final_ctx[r % POOLS], cfg.hkv, cfg.window) for r in range(ATTN_REPS)])
+    attn_kernel = (f"nc_decode_attn_fp8 = k_decode<false> + k_merge, a graph of {ATTN_REPS} calls over {POOLS} "
+                   "pools in turn at their last contexts, HIP events on their stream")
     if args.unfused:
         call_ms, call_bytes, call_kernel = attn_ms, attn_bytes, attn_kernel
     else:
         # the step is one nc_decode_step_fp8 call: the timed region is the roofline measurement itself
         call_ms, call_bytes = step_ms, step_bytes
         call_kernel = ("nc_decode_step_fp8 = k_decode<true> + k_merge, one call per timed step, HIP events on their "
-                       "stream")
+                       f"stream, {POOLS} pools in turn")
     achieved = call_bytes / (call_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC,
@@ -638,11 +762,12 @@ def main():
         "data": "synthetic",
         "config": {"workload": cfg.name, "batch": B, "hq": cfg.hq, "hkv": cfg.hkv, "head_dim": 128,
                    "ctx_prior": "U[512,8192] seed 3", "page": 16, "outliers": "1% at 8 sigma",
-                   "mean_keys_per_seq": round(float(np.mean(base + steps / 2 + 1)), 1),
+                   "pools": POOLS, "mean_keys_per_seq": round(float(np.mean(base + steps / (2 * POOLS) + 1)), 1),
                    "step": ("nc_kv_append_fp8 + nc_decode_attn_fp8" if args.unfused else
                             "nc_decode_step_fp8 (append fused into the attention kernel)") +
                            ": append 1 token/seq (qk-norm+rope+fp8 quantise, emitting the next positions) + split-K "
-                           f"decode attention, one attention layer, graph replays of {STEP_GROUP} steps"},
+                           f"decode attention, one attention layer per step, {POOLS} layer pools stepped in turn "
+                           f"(cold), graph replays of {STEP_GROUP} steps"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_one_layer": round(B / (step_ms * 1e-3), 1),
         "attention_only": {"kernel": attn_kernel, "call_us": round(attn_ms * 1e3, 3),
@@ -659,6 +784,7 @@ def main():
     }
     cpu_s = None if args.no_cpu else args.cpu_seconds
     if not args.no_extra:
+        result["decode_cfg1"] = extra_decode_cfg1(dev, stream, cpu_s)
         result["decode_cfg2"] = extra_decode_cfg2(dev, stream, cpu_s)
         result["prefill_cfg4"] = extra_prefill_cfg4(dev, stream, cpu_s)
         result["e2e_cfg5"] = extra_e2e_cfg5(dev, args.e2e_steps, cpu_s)
@@ -668,7 +794,7 @@ def main():
     if args.copy_probe:
         copy_probe(dev)
     if cpu_s:
-        result["cpu_baseline"] = cpu_decode(case, final_ctx, q, cpu_s, value)
+        result["cpu_baseline"] = cpu_decode(case, final_ctx[0], q, cpu_s, value)
     print(json.dumps(result), flush=True)
 
 

@@ -28,18 +28,21 @@
  * SIMD: with two, the older wave wins issue arbitration and the younger finishes its equal share ~1.6x later. A
  * page is six nontemporal loads per lane; each code load of the wave reads one contiguous 1 KiB part of the tile.
  *
- * A piece covering its whole segment writes the normalised bf16 output. Otherwise it writes (Σ p v, max, sum)
- * to a workspace slot, and k_merge, launched next, combines a segment's slots with weights exp2(m_s - max m)
+ * A piece covering its whole segment writes the normalised bf16 output. Otherwise it writes (Σ p v, max, sum) to a
+ * workspace slot, and k_merge, launched next, combines a segment's slots with weights exp2(m_s - max m)
  * (decode.cu:547-548's rescale). The merge is a second kernel on purpose: the eight XCDs' L2 caches are not
- * coherent with each other, so an in-kernel "last wave merges" handshake needs agent-scope fences, which on
- * gfx950 write back and invalidate the whole L2 (buffer_wbl2 / buffer_inv) and cost more than a launch.
+ * coherent with each other, so a piece's partials reach a merging wave on another XCD only through device-scope
+ * (write-through) stores, whose acknowledgements the in-order memory counter puts ahead of the next pages' loads.
+ * An in-kernel merge built that way (the last piece to arrive at a per-segment counter merges) was measured: about
+ * 3 µs slower per config-3 call with the partials written as they finish, 1 µs slower with them held in registers
+ * until the end of the wave, than this launch.
  *
  * The fused step (nc_decode_step_fp8) is the append and the attention of a decode step in these two launches
  * instead of three (reference: k_prologue's append, decode.cu:550-565, then k_attn). Every piece builds its q
- * rows from the projection (QK-norm, gain, RoPE, the row math of k_append, so bit-identical), and the piece that
- * ends a segment also quantises the new key and value, patches them into its registers for the last page and
- * stores them in the cache after its pages: that page is read by no other wave, so the new key needs no ordering
- * between waves.
+ * rows from the projection (QK-norm, gain, RoPE, the row math of k_append, so bit-identical) while its first pages
+ * load, and the piece that ends a segment also quantises the new key and value (after its first page, off the
+ * critical path), patches them into its registers for the last page and stores them in the cache after its pages:
+ * that page is read by no other wave, so the new key needs no ordering between waves.
  *
  * Roofline: HBM. Per (token, kv head) the kernel reads 128 B of K, 128 B of V and two fp32 scales: 264 B.
  */
@@ -317,45 +320,62 @@ __device__ __forceinline__ void attend_page(const DecodeArgs &a, Page pg, int pa
 
 /* ------------------------------------------------------------------------------------------ fused step rows */
 
-#define DEC_ROW_PASSES ((DEC_MAX_G + 2 + 7) / 8) /* 8-lane rows per wave pass: G q heads, the k and v heads */
+#define DEC_Q_PASSES ((DEC_MAX_G + 7) / 8) /* 8-lane rows per wave pass: the G q heads */
 
-/* A piece's projection rows in the 8-lane row layout of qk_row.h (lane g = lane % 8 holds dims [8g, 8g + 8) and
- * [64 + 8g, 64 + 8g + 8)): row ri = 8 pass + lane / 8 is q head h G + ri for ri < G, then the k head and the v
- * head of kv head h when the piece appends. Loaded before the first pages, used once they are in flight. */
-struct Rows {
-    u32x4 lo[DEC_ROW_PASSES], hi[DEC_ROW_PASSES];
-    f32x4 qg[4], kg[4], cs[2], sn[2];
-    int blk; /* the new key's block (table entry, unchecked) */
+/* A piece's q rows in the 8-lane row layout of qk_row.h (lane g = lane % 8 holds dims [8g, 8g + 8) and
+ * [64 + 8g, 64 + 8g + 8)): row ri = 8 pass + lane / 8 is q head h G + ri for ri < G; with the q gains and the
+ * position's rotation table entries. Loaded after the block ids, so the page loads wait for the ids alone. */
+struct QRows {
+    u32x4 lo[DEC_Q_PASSES], hi[DEC_Q_PASSES];
+    f32x4 qg[4], cs[2], sn[2];
 };
 
-__device__ __forceinline__ void load_rows(const DecodeArgs &a, int b, int h, int p, bool app, int lane, Rows &rw) {
-    const int g = lane & 7, G = a.group, rows = G + (app ? 2 : 0);
+/* The appending piece's new key and value rows (lanes 0-7: the k head, lanes 8-15: the v head; the other lanes
+ * repeat the k head), the k gains and the new key's block (table entry, unchecked). */
+struct KvRows {
+    u32x4 lo, hi;
+    f32x4 kg[4];
+    int blk;
+};
+
+__device__ __forceinline__ void load_qrows(const DecodeArgs &a, int b, int h, int p, int lane, QRows &qr) {
+    const int g = lane & 7, G = a.group;
     const bf16_t *row = a.qkv + (size_t)b * a.row_stride;
 #pragma unroll
-    for (int ps = 0; ps < DEC_ROW_PASSES; ps++) {
-        const int ri = 8 * ps + (lane >> 3);
-        int head = ri < G ? h * G + ri : (ri == G ? a.hq + h : a.hq + a.hkv + h);
-        if (ri >= rows) head = h * G; /* unused rows read a valid one */
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(row + (size_t)head * NC_HEAD_DIM);
-        rw.lo[ps] = src[g];
-        rw.hi[ps] = src[8 + g];
+    for (int ps = 0; ps < DEC_Q_PASSES; ps++) {
+        const int ri = min(8 * ps + (lane >> 3), G - 1); /* unused rows read a valid one */
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(row + (size_t)(h * G + ri) * NC_HEAD_DIM);
+        qr.lo[ps] = src[g];
+        qr.hi[ps] = src[8 + g];
     }
-    const f32x4 *qg = reinterpret_cast<const f32x4 *>(a.q_gain), *kg = reinterpret_cast<const f32x4 *>(a.k_gain);
+    const f32x4 *qg = reinterpret_cast<const f32x4 *>(a.q_gain);
     const f32x4 *cp = reinterpret_cast<const f32x4 *>(a.cos + (size_t)p * NC_HALF);
     const f32x4 *sp = reinterpret_cast<const f32x4 *>(a.sin + (size_t)p * NC_HALF);
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        rw.qg[i] = qg[2 * g + i];
-        rw.qg[2 + i] = qg[16 + 2 * g + i];
-        rw.kg[i] = kg[2 * g + i];
-        rw.kg[2 + i] = kg[16 + 2 * g + i];
-        rw.cs[i] = cp[2 * g + i];
-        rw.sn[i] = sp[2 * g + i];
+        qr.qg[i] = qg[2 * g + i];
+        qr.qg[2 + i] = qg[16 + 2 * g + i];
+        qr.cs[i] = cp[2 * g + i];
+        qr.sn[i] = sp[2 * g + i];
     }
-    /* the new key's block: the table entry is loaded without a branch (from ctx_len when there is no table) so
-     * that its wait lands in build_rows, after the first pages' loads; p < max_ctx keeps the page in the table */
-    const size_t at = (size_t)b * a.max_blocks + p / NC_PAGE;
-    rw.blk = *(a.block_table ? a.block_table + at : a.ctx_len); /* no table: replaced by `at` in build_rows */
+}
+
+template <bool TABLE>
+__device__ __forceinline__ void load_kvrows(const DecodeArgs &a, int b, int h, int p, int lane, KvRows &kr) {
+    const int g = lane & 7;
+    const int head = (lane >> 3) == 1 ? a.hq + a.hkv + h : a.hq + h;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.qkv + (size_t)b * a.row_stride + (size_t)head * NC_HEAD_DIM);
+    kr.lo = src[g];
+    kr.hi = src[8 + g];
+    const f32x4 *kg = reinterpret_cast<const f32x4 *>(a.k_gain);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        kr.kg[i] = kg[2 * g + i];
+        kr.kg[2 + i] = kg[16 + 2 * g + i];
+    }
+    /* the new key's page: p < max_ctx keeps it in the table (contiguous: computed in build_kv) */
+    if constexpr (TABLE) kr.blk = a.block_table[(size_t)b * a.max_blocks + p / NC_PAGE];
+    else kr.blk = 0;
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const u32x4 u, float *v) {
@@ -366,55 +386,37 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 u, float *v) {
     }
 }
 
-/* Norm, gain and rotate the piece's q rows (k_append's row math, so bit-identical to its q_out) into this lane's
- * MFMA operand (head n, dims 32 j..) through LDS. A piece that appends also quantises the new key and value
- * into LDS, for its last page and for store_new_kv. */
-__device__ __forceinline__ void build_rows(const DecodeArgs &a, int b, int h, int p, bool app, const Rows &rw, int lane,
-                                           bf16x8 *qop, StepLds &sm) {
-    const int g = lane & 7, G = a.group, rows = G + (app ? 2 : 0);
-    float c[8], s[8], qg1[8], qg2[8], kg1[8], kg2[8];
+__device__ __forceinline__ void rope_entries(const QRows &qr, float *c, float *s) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        c[e] = rw.cs[e / 4][e % 4];
-        s[e] = rw.sn[e / 4][e % 4];
-        qg1[e] = rw.qg[e / 4][e % 4];
-        qg2[e] = rw.qg[2 + e / 4][e % 4];
-        kg1[e] = rw.kg[e / 4][e % 4];
-        kg2[e] = rw.kg[2 + e / 4][e % 4];
+        c[e] = qr.cs[e / 4][e % 4];
+        s[e] = qr.sn[e / 4][e % 4];
     }
-    __syncthreads(); /* the previous piece's reads of sm are done */
+}
+
+/* Norm, gain and rotate the piece's q rows (k_append's row math, so bit-identical to its q_out) into this lane's
+ * MFMA operand (head n, dims 32 j..) through LDS. */
+__device__ __forceinline__ void build_q(const DecodeArgs &a, const QRows &qr, int lane, bf16x8 *qop, StepLds &sm) {
+    const int g = lane & 7, G = a.group;
+    float c[8], s[8], g1[8], g2[8];
+    rope_entries(qr, c, s);
 #pragma unroll
-    for (int ps = 0; ps < DEC_ROW_PASSES; ps++) {
-        if (8 * ps >= rows) break;
+    for (int e = 0; e < 8; e++) {
+        g1[e] = qr.qg[e / 4][e % 4];
+        g2[e] = qr.qg[2 + e / 4][e % 4];
+    }
+    __syncthreads(); /* the previous piece's reads of sm.q are done */
+#pragma unroll
+    for (int ps = 0; ps < DEC_Q_PASSES; ps++) {
+        if (8 * ps >= G) break;
         const int ri = 8 * ps + (lane >> 3);
-        if (ri >= rows) continue; /* whole 8-lane rows: the row reductions stay inside active lanes */
+        if (ri >= G) continue; /* whole 8-lane rows: the row reductions stay inside active lanes */
         float x1[8], x2[8];
-        unpack_bf16x8(rw.lo[ps], x1);
-        unpack_bf16x8(rw.hi[ps], x2);
-        if (ri <= G) {
-            float g1[8], g2[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                g1[e] = ri < G ? qg1[e] : kg1[e];
-                g2[e] = ri < G ? qg2[e] : kg2[e];
-            }
-            row_norm_rope(x1, x2, g1, g2, c, s);
-        }
-        if (ri < G) {
-            store_bf16x8(&sm.q[ri][8 * g], x1);
-            store_bf16x8(&sm.q[ri][NC_HALF + 8 * g], x2);
-            continue;
-        }
-        const int is_v = ri > G;
-        uint64_t c1, c2;
-        const float scale = row_quantize(x1, x2, &c1, &c2);
-        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][8 * g]) = c1;
-        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][NC_HALF + 8 * g]) = c2;
-        if (g == 0) sm.scale[is_v] = scale;
-        if (g == 0 && !is_v) {
-            const int blk = a.block_table ? rw.blk : b * a.max_blocks + p / NC_PAGE;
-            sm.blk = (blk >= 0 && blk < a.num_blocks) ? blk : -1;
-        }
+        unpack_bf16x8(qr.lo[ps], x1);
+        unpack_bf16x8(qr.hi[ps], x2);
+        row_norm_rope(x1, x2, g1, g2, c, s);
+        store_bf16x8(&sm.q[ri][8 * g], x1);
+        store_bf16x8(&sm.q[ri][NC_HALF + 8 * g], x2);
     }
     __syncthreads();
     const int n = lane & 15, j = lane >> 4;
@@ -422,6 +424,38 @@ __device__ __forceinline__ void build_rows(const DecodeArgs &a, int b, int h, in
     for (int cc = 0; cc < 4; cc++)
         qop[cc] = n < G ? *reinterpret_cast<const bf16x8 *>(&sm.q[n][32 * j + 8 * cc])
                         : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+}
+
+/* The appending piece's new key (norm, gain, rotation) and value, quantised into LDS (codes, scales, block) for
+ * the last page's patch and for store_new_kv. Lanes 0-15 work, two 8-lane rows. */
+__device__ __forceinline__ void build_kv(const DecodeArgs &a, int b, int p, const QRows &qr, const KvRows &kr,
+                                         int lane, StepLds &sm) {
+    const int g = lane & 7, is_v = lane >> 3;
+    if (lane < 16) {
+        float x1[8], x2[8];
+        unpack_bf16x8(kr.lo, x1);
+        unpack_bf16x8(kr.hi, x2);
+        if (!is_v) {
+            float c[8], s[8], g1[8], g2[8];
+            rope_entries(qr, c, s);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                g1[e] = kr.kg[e / 4][e % 4];
+                g2[e] = kr.kg[2 + e / 4][e % 4];
+            }
+            row_norm_rope(x1, x2, g1, g2, c, s);
+        }
+        uint64_t c1, c2;
+        const float scale = row_quantize(x1, x2, &c1, &c2);
+        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][8 * g]) = c1;
+        *reinterpret_cast<uint64_t *>(&sm.codes[is_v][NC_HALF + 8 * g]) = c2;
+        if (g == 0) sm.scale[is_v] = scale;
+        if (lane == 0) {
+            const int blk = a.block_table ? kr.blk : b * a.max_blocks + p / NC_PAGE;
+            sm.blk = (blk >= 0 && blk < a.num_blocks) ? blk : -1;
+        }
+    }
+    __syncthreads(); /* the codes are in LDS before the last page's patch reads them */
 }
 
 /* The fused step's cache write of the new key and value (codes and scales from LDS, the bytes k_append writes),
@@ -439,63 +473,99 @@ __device__ __forceinline__ void store_new_kv(const DecodeArgs &a, int h, int p, 
     if (lane < 2) reinterpret_cast<float *>(tile + (lane ? NC_TILE_VS : NC_TILE_KS))[t] = sm.scale[lane];
 }
 
-/* The pages [pg_lo, pg_lo + npg) of segment (b, h), DEC_DEPTH buffers in rotation: DEC_DEPTH - 1 pages are in
- * flight while one is computed. The fused step builds q (and the append) while the first pages are in flight. */
-template <bool FUSED>
-__device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
-                                           bool app, bf16x8 *qop, int lane, StepLds &sm, State &st) {
+/* The table entry of page `page` of sequence b (TABLE: loaded from an index clamped into the table, always in
+ * bounds; contiguous: computed), and its check: the block, or -1 when the page or the block is out of range. Split
+ * so that a wave can issue the entry's load, then other loads, and wait for the entry alone. */
+template <bool TABLE>
+__device__ __forceinline__ int block_entry(const DecodeArgs &a, int b, int page) {
+    const int pc = min(max(page, 0), a.max_blocks - 1);
+    if constexpr (TABLE) return a.block_table[(size_t)b * a.max_blocks + pc];
+    return b * a.max_blocks + pc;
+}
+
+__device__ __forceinline__ int block_checked(const DecodeArgs &a, int entry, int page) {
+    return (page >= 0 && page < a.max_blocks && entry >= 0 && entry < a.num_blocks) ? entry : -1;
+}
+
+/* One window of at most 64 pages [base, base + nw) of segment (b, h): lane i's entry is page base + i's. The first
+ * window of a fused piece also builds q once its pages are in flight, and the appending piece's key and value after
+ * its first page (before the last). */
+template <bool FUSED, bool FIRST>
+__device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h, int base, int nw, int entry,
+                                              const SeqRange &sr, bool app, const QRows &qr, const KvRows &kr,
+                                              bf16x8 *qop, int lane, StepLds &sm, State &st) {
     const int n = lane & 15, j = lane >> 4;
     const int patch_t = FUSED && app ? sr.p % NC_PAGE : -1;
-    for (int win = 0; win < npg; win += 64) {
-        const int nw = min(64, npg - win);
-        const int base = pg_lo + win;
-        /* the fused step's rows first: they arrive with the block ids, and are used while the first pages load */
-        Rows rw;
-        if (FUSED && win == 0) {
-            load_rows(a, b, h, sr.p, app, lane, rw);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        /* lane i holds the block of page base + i */
-        const int ids = lane < nw ? lookup_block(a.block_table, a.max_blocks, a.num_blocks, b, base + lane) : -1;
-        const int last = __builtin_amdgcn_readfirstlane(nw - 1);
-        Page r[DEC_DEPTH];
+    const int ids = lane < nw ? block_checked(a, entry, base + lane) : -1;
+    const int last = __builtin_amdgcn_readfirstlane(nw - 1);
+    Page r[DEC_DEPTH];
 #pragma unroll
-        for (int i = 0; i < DEC_DEPTH - 1; i++) {
-            __builtin_amdgcn_sched_barrier(0);
-            load_page(a, __builtin_amdgcn_readlane(ids, min(i, last)), h, n, j, r[i]);
-        }
+    for (int i = 0; i < DEC_DEPTH - 1; i++) {
         __builtin_amdgcn_sched_barrier(0);
-        if (FUSED && win == 0) {
-            build_rows(a, b, h, sr.p, app, rw, lane, qop, sm);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        /* sched_barrier keeps each reload after the math that frees its buffer: with the live ranges apart the
-         * buffers keep their registers across iterations (no copies of in-flight loads, no vmcnt(0)). Loads are
-         * unconditional (clamped to the last page) so the counted waits stay exact. */
-        for (int k = 0; k < nw; k += DEC_DEPTH) {
+        load_page(a, __builtin_amdgcn_readlane(ids, min(i, last)), h, n, j, r[i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FUSED && FIRST) {
+        build_q(a, qr, lane, qop, sm);
+        if (app && nw == 1 && sr.p / NC_PAGE == base) build_kv(a, b, sr.p, qr, kr, lane, sm); /* the only page */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    /* sched_barrier keeps each reload after the math that frees its buffer: with the live ranges apart the buffers
+     * keep their registers across iterations (no copies of in-flight loads, no vmcnt(0)). Loads are unconditional
+     * (clamped to the last page) so the counted waits stay exact. */
+    for (int k = 0; k < nw; k += DEC_DEPTH) {
 #pragma unroll
-            for (int u = 0; u < DEC_DEPTH; u++) {
-                load_page(a, __builtin_amdgcn_readlane(ids, min(k + u + DEC_DEPTH - 1, last)), h, n, j,
-                          r[(u + DEC_DEPTH - 1) % DEC_DEPTH]);
-                __builtin_amdgcn_sched_barrier(0);
-                if (u == 0 || k + u < nw) attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < DEC_DEPTH; u++) {
+            load_page(a, __builtin_amdgcn_readlane(ids, min(k + u + DEC_DEPTH - 1, last)), h, n, j,
+                      r[(u + DEC_DEPTH - 1) % DEC_DEPTH]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u == 0 || k + u < nw) attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (FUSED && FIRST) {
+                if (app && k == 0 && u == 0 && !(nw == 1 && sr.p / NC_PAGE == base)) {
+                    build_kv(a, b, sr.p, qr, kr, lane, sm); /* after the first page, before the last */
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     }
 }
 
+/* The pages [pg_lo, pg_lo + npg) of segment (b, h), DEC_DEPTH buffers in rotation: DEC_DEPTH - 1 pages are in
+ * flight while one is computed. The first window's block ids load first, the fused step's rows behind them (every
+ * piece loads both row sets: unconditional loads keep every wait a counted one), so its page loads wait for the
+ * ids alone. */
+template <bool FUSED, bool TABLE>
+__device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
+                                           bool app, bf16x8 *qop, int lane, StepLds &sm, State &st) {
+    QRows qr;
+    KvRows kr;
+    const int entry = block_entry<TABLE>(a, b, pg_lo + lane);
+    if constexpr (FUSED) {
+        load_qrows(a, b, h, sr.p, lane, qr);
+        load_kvrows<TABLE>(a, b, h, sr.p, lane, kr);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    stream_window<FUSED, true>(a, b, h, pg_lo, min(64, npg), entry, sr, app, qr, kr, qop, lane, sm, st);
+    for (int win = 64; win < npg; win += 64) {
+        const int e = block_entry<TABLE>(a, b, pg_lo + win + lane);
+        __builtin_amdgcn_sched_barrier(0);
+        stream_window<FUSED, false>(a, b, h, pg_lo + win, min(64, npg - win), e, sr, app, qr, kr, qop, lane, sm,
+                                    st);
+    }
+}
+
 /* The workspace slot of piece i (the i-th wave to touch segment s, wave w): the first DEC_MERGE_DIRECT pieces of a
- * segment sit together at s * DEC_MERGE_DIRECT + i, so k_merge reads them with the segment's descriptor in one
- * round trip; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's pieces lie in consecutive segments and
- * the waves' slices are in segment order, so w + s never repeats). */
+ * segment sit together at s * DEC_MERGE_DIRECT + i; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's
+ * pieces lie in consecutive segments and the waves' slices are in segment order, so w + s never repeats). */
 __device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, int w) {
     const int S = a.B * a.hkv;
     return i < DEC_MERGE_DIRECT ? (size_t)s * DEC_MERGE_DIRECT + i : (size_t)S * DEC_MERGE_DIRECT + w + s;
 }
 
 /* Finish piece `piece` of segment (b, h), wave w: the whole segment writes the normalised bf16 output; a part of it
- * writes (Σ p v in value units, max, sum) to its merge slot, which k_merge combines. */
+ * writes (Σ p v in value units, max, sum) to its merge slot, which k_merge combines. Lane (j, n) holds dims
+ * (4 j + i) 8 + bb of head n. */
 __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st) {
     const int n = lane & 15, j = lane >> 4;
     float l = st.l;
@@ -531,20 +601,19 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
     }
 }
 
-/* Schedule units of the whole batch: every wave of k_decode and k_merge derives the same value from the live
- * context lengths. k_decode (zero_rows) also keeps them in lds (if not null), and wave b % W writes sequence b's
- * row if it is empty (zeros, or NaN for the fused step's positions out of range) and its next position to
- * pos_out. */
-__device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane, bool zero_rows, int *lds) {
-    long long total = 0;
+/* Schedule units of the whole batch: every wave derives the same value from the live context lengths and keeps
+ * them in lds (if not null); wave b % W writes sequence b's row if it is empty (zeros, or NaN for the fused step's
+ * positions out of range) and its next position to pos_out. 32-bit: the host bounds the total. */
+__device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *lds) {
+    int total = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int b = base + lane;
         const int c = b < a.B ? seq_ctx(a, b) : 0;
         const int pg = units_of(a, c);
         if (lds && b < a.B) lds[b] = c;
-        if (zero_rows && a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
-        if (zero_rows && b < a.B && pg == 0 && b % W == w) {
-            for (int h = 0; h < a.hkv; h++) a.ws_desc[b * a.hkv + h] = make_int2(0, 0); /* nothing to merge */
+        if (a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
+        if (b < a.B && pg == 0 && b % W == w) {
+            for (int hh = 0; hh < a.hkv; hh++) a.ws_desc[b * a.hkv + hh] = make_int2(0, 0); /* nothing to merge */
             const uint32_t f = c < 0 ? 0x7fc07fc0u : 0u;
             const u32x4 z = {f, f, f, f};
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
@@ -555,51 +624,50 @@ __device__ long long schedule_total(const DecodeArgs &a, int w, int W, int lane,
     return total * a.hkv;
 }
 
-template <bool FUSED>
+template <bool FUSED, bool TABLE>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     __shared__ StepLds sm;
     __shared__ int ctx_lds[DEC_LDS_SEQS];
     const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
     int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
 
-    const long long total = schedule_total(a, w, W, lane, true, lds);
+    const int total = schedule_total(a, w, W, lane, lds);
     __syncthreads(); /* lds complete before other lanes' reads */
-    const long long chunk = max((total + W - 1) / W, (long long)DEC_MIN_CHUNK);
-    const long long start = (long long)w * chunk;
+    const int chunk = max((total + W - 1) / W, DEC_MIN_CHUNK);
+    const int start = w * chunk;
     if (start >= total) return;
-    long long remaining = min(chunk, total - start);
+    int remaining = min(chunk, total - start);
 
     /* the segment holding `start`: sequence b0, then kv head and unit offset */
-    long long carry = 0;
-    int b = -1, units_b = 0;
+    int carry = 0, b = -1, units_b = 0;
     for (int base = 0; base < a.B && b < 0; base += 64) {
         const int bb = base + lane;
         const int pg = bb < a.B ? units_of(a, ctx_at(a, lds, bb)) : 0;
         const int incl = wave_inclusive_sum(pg, lane);
-        const unsigned long long hit = __ballot(bb < a.B && carry + (long long)incl * a.hkv > start);
+        const unsigned long long hit = __ballot(bb < a.B && carry + incl * a.hkv > start);
         if (hit) {
             const int first = __builtin_ctzll(hit);
             b = base + first;
             units_b = __shfl(pg, first, 64);
-            carry += (long long)__shfl(incl - pg, first, 64) * a.hkv;
+            carry += __shfl(incl - pg, first, 64) * a.hkv;
         } else {
-            carry += (long long)__shfl(incl, 63, 64) * a.hkv;
+            carry += __shfl(incl, 63, 64) * a.hkv;
         }
     }
-    const long long into = start - carry; /* flattened offset inside sequence b */
-    int h = (int)(into / units_b), off = (int)(into % units_b);
-    long long seg_base = start - off; /* the segment's first unit in the flattened list */
+    const int into = start - carry; /* offset inside sequence b */
+    int h = into / units_b, off = into % units_b;
+    int seg_base = start - off; /* the segment's first unit in the flattened list */
 
     while (remaining > 0) {
         const SeqRange sr = seq_range_of(a, ctx_at(a, lds, b));
         const int seg_pages = sr.last - sr.first + 1;
         /* this slice takes units [off, off + take) of the segment; its pages are [lo, hi) */
         const int units = seg_pages + a.unit_start + a.unit_end;
-        const int take = (int)min((long long)(units - off), remaining);
+        const int take = min(units - off, remaining);
         const int lo = max(off - a.unit_start, 0), hi = min(off + take - a.unit_start, seg_pages);
         /* the waves holding the segment's first and last pages: piece i of the segment is wave w_first + i */
-        const long long page0 = seg_base + a.unit_start;
-        const int w_first = (int)(page0 / chunk), pieces = (int)((page0 + seg_pages - 1) / chunk) - w_first + 1;
+        const int page0 = seg_base + a.unit_start;
+        const int w_first = page0 / chunk, pieces = (page0 + seg_pages - 1) / chunk - w_first + 1;
         remaining -= take;
         off = 0;
         seg_base += units;
@@ -618,7 +686,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             }
             State st;
             state_init(st);
-            attend_run<FUSED>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
+            attend_run<FUSED, TABLE>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
             finish_piece(a, b, h, w, w - w_first, lo == 0 && hi == seg_pages, lane, st);
             if (lo == 0 && lane == 0) a.ws_desc[b * a.hkv + h] = make_int2(pieces, w_first);
             if (FUSED && hi == seg_pages) store_new_kv(a, h, sr.p, lane, sm);
@@ -634,10 +702,10 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 }
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
- * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale, combined online. Thread t holds head t / 16,
- * dims 8 (t % 16)..+8 (16 lanes per head, ceil(G / 4) waves). The kernel is latency-bound, so it needs no schedule:
- * the segment's descriptor (piece count, first wave) and the first DEC_MERGE_DIRECT pieces' slots are loaded
- * together, in one round trip; a segment with more pieces reads the rest in a second. */
+ * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale, combined online in piece order. Thread t holds
+ * head t / 16, dims 8 (t % 16)..+8 (16 lanes per head, ceil(G / 4) waves). The kernel is latency-bound, so it needs
+ * no schedule: the segment's descriptor (piece count, first wave) and the first DEC_MERGE_DIRECT pieces' slots are
+ * loaded together, in one round trip; a segment with more pieces reads the rest in a second. */
 #define MERGE_LANES 16
 
 __global__ void __launch_bounds__(256) k_merge(DecodeArgs a) {
@@ -695,9 +763,13 @@ static int decode_waves() {
     if (!cached[dev]) {
         int per_cu = 0, cus = 0;
         int per_cu_fused = 0;
-        NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<false>, DEC_THREADS, 0));
-        NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_fused, k_decode<true>, DEC_THREADS, 0));
-        if (per_cu_fused < per_cu) per_cu = per_cu_fused; /* one grid size for both: the same schedule */
+        const void *kernels[4] = {(const void *)k_decode<false, false>, (const void *)k_decode<false, true>,
+                                  (const void *)k_decode<true, false>, (const void *)k_decode<true, true>};
+        per_cu = 1 << 30;
+        for (const void *k : kernels) { /* one grid size for all: the same schedule */
+            NC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_fused, k, DEC_THREADS, 0));
+            if (per_cu_fused < per_cu) per_cu = per_cu_fused;
+        }
         NC_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         /* CDNA: 4 SIMDs per CU. Resident waves beyond DEC_WAVES_PER_SIMD per SIMD are not used: a second wave on
          * a SIMD loses issue arbitration to the older one and finishes its equal share last. */
@@ -720,7 +792,7 @@ extern "C" long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_c
                        S * sizeof(int2));
 }
 
-/* Checks shared by both entry points, then the launch of k_decode<FUSED> and k_merge. */
+/* Checks shared by both entry points, then the launch of k_decode<FUSED, TABLE>. */
 static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void *workspace, long long workspace_bytes,
                          int max_ctx, float sm_scale, void *stream) {
     const int B = a.B, hq = a.hq, hkv = a.hkv;
@@ -737,6 +809,9 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
                "tensors must be 16-byte aligned");
     const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
     NC_REQUIRE(workspace_bytes >= need, "workspace %lld bytes, %lld needed", workspace_bytes, need);
+    /* the kernel's schedule counts units in 32 bits: every segment's pages plus its start and end units */
+    NC_REQUIRE((long long)B * hkv * ((long long)a.max_blocks + DEC_UNITS_START + DEC_UNITS_END) < (1ll << 31),
+               "%d sequences x %d kv heads x %d pages exceed the schedule's 2^31 units", B, hkv, a.max_blocks);
     a.group = hq / hkv;
     a.score_scale = sm_scale * 1.4426950408889634f;
     a.out = (bf16_t *)out;
@@ -751,13 +826,15 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     a.unit_start = DEC_UNITS_START;
     a.unit_end = DEC_UNITS_END;
     const int W = decode_waves();
-    if (fused)
-        hipLaunchKernelGGL(k_decode<true>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL(k_decode<false>, dim3(W), dim3(DEC_THREADS), 0, (hipStream_t)stream, a);
+    const dim3 grid(W), block(DEC_THREADS);
+    hipStream_t st = (hipStream_t)stream;
+    if (fused && a.block_table) hipLaunchKernelGGL((k_decode<true, true>), grid, block, 0, st, a);
+    else if (fused) hipLaunchKernelGGL((k_decode<true, false>), grid, block, 0, st, a);
+    else if (a.block_table) hipLaunchKernelGGL((k_decode<false, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
     const unsigned merge_threads = (unsigned)(((a.group * MERGE_LANES + NC_WAVE - 1) / NC_WAVE) * NC_WAVE);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(merge_threads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(merge_threads), 0, st, a);
     NC_LAUNCH_CHECK();
     return 0;
 }
@@ -817,13 +894,13 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const i
 
 /* ------------------------------------------------------------------------------------------------------------
  * The fused step without a workspace argument, for callers that cannot allocate (code under graph capture, tight
- * serving loops): the partial results between k_decode and k_merge live in `scratch`, a static device array of
+ * serving loops): the partial results and the segments' counters live in `scratch`, a static device array of
  * NC_DECODE_SCRATCH_BYTES that every device running this library holds until the process ends. Its device address
- * is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernels like the
- * workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. No cell of it needs
- * to start at zero: every segment's descriptor is written before k_merge reads it, and only the slots of pieces
- * that exist are folded. Calls share their device's array, so two calls that may overlap on one device (two streams)
- * race; calls in one stream do not. */
+ * is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernel like the
+ * workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. The array starts at
+ * zero (a static device array is zero-initialised when the code object loads) and every call leaves the counters
+ * at zero, as a caller's workspace must be. Calls share their device's array, so two calls that may overlap on one
+ * device (two streams) race; calls in one stream do not. */
 #define NC_DECODE_SCRATCH_BYTES (64ll << 20)
 #define NC_MAX_DEVICES 64
 

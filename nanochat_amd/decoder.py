@@ -116,8 +116,11 @@ class Weights:
         """False when every layer's mix is the identity (resid 1, x0 0: the reference's initialisation)."""
         return bool((self.resid_lambdas != 1).any() or (self.x0_lambdas != 0).any())
 
-    def weight_bytes(self) -> int:
-        n = self.wte.numel() + self.lm_head.numel()
+    def weight_bytes(self, rows: int | None = None) -> int:
+        """bf16 weight bytes a decode step reads: every matrix whole, except the embedding table, of which only
+        the `rows` rows looked up (one per sequence) are read; rows None counts the whole table."""
+        wte = self.wte.numel() if rows is None else min(rows, self.wte.shape[0]) * self.wte.shape[1]
+        n = wte + self.lm_head.numel()
         for lw in self.layers:
             n += sum(lw[k].numel() for k in ("wqkv", "wo", "wup", "wdown"))
         return 2 * n
@@ -424,5 +427,5 @@ def generate(cfg: E2EConfig, device, steps: int | None = None, timing: bool = Fa
     toks = dec.tokens(steps)
     prefill_ms, decode_ms = e[0].elapsed_time(e[1]), e[2].elapsed_time(e[3])
     info = {"prefill_ms": prefill_ms, "decode_ms": decode_ms, "decode_ms_per_step": decode_ms / max(steps, 1),
-            "weight_bytes": model.weight_bytes()}
+            "weight_bytes": model.weight_bytes(rows=cfg.batch)}
     return toks, info, (model, dec, prompts)
