@@ -125,6 +125,21 @@ int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos
                        int hq, int hkv, int max_ctx, float sm_scale, void *out, void *workspace,
                        long long workspace_bytes, void *stream);
 
+/* nc_decode_step_fp8 with the sequence-local piece plan: every (sequence, kv head) segment of n pages (its keys'
+ * pages) is cut into fixed pieces of max(piece_pages, ceil(n / 8)) pages from its first page, each piece's softmax
+ * starts afresh, and the pieces merge in piece order; a wave takes whole pieces (the balanced split's slice ends
+ * rounded to the nearest piece boundary). A sequence's output bits are then a function of its own query, context
+ * and cache alone: decoded alone or in any batch, it gets the same bits, as with the reference's one block per
+ * (head, slot). Arguments as nc_decode_step_fp8, plus piece_pages >= 1 (the balanced split, the plain entry point,
+ * rebalances every sequence's pieces with the batch and is faster on few, long sequences).
+ * Replaces: k_prologue's append and k_attn (model/kernels/decode.cu:550-675), whose tokens depend on neither the
+ * batch nor the store (inference/decoder.py:124-125); the decoder handle (dec_*) runs this entry point. */
+int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                              const float *q_gain, const float *k_gain, const float *cos, const float *sin,
+                              int rope_len, uint8_t *cache, const int32_t *block_table, int max_blocks,
+                              int num_blocks, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
+                              int piece_pages, void *out, void *workspace, long long workspace_bytes, void *stream);
+
 /* nc_decode_step_fp8 without the workspace: the partial results between its two kernels live in a static device
  * array of 64 MiB (67108864 bytes) that the library holds on every device it runs on until the process ends, so the
  * call allocates nothing. A shape whose workspace (nc_decode_workspace_bytes) exceeds 64 MiB is rejected with an

@@ -67,12 +67,14 @@ def decode_attention(q: Tensor, cache: Fp8KVCache, ctx_len: Tensor, *, max_ctx: 
 
 def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_gain: Tensor, cos: Tensor,
                 sin: Tensor, hq: int, *, max_ctx: int, window: int = -1, sm_scale: float | None = None,
-                out: Tensor | None = None, workspace: Tensor | None = None, pos_out: Tensor | None = None) -> Tensor:
+                out: Tensor | None = None, workspace: Tensor | None = None, pos_out: Tensor | None = None,
+                piece_pages: int = 0) -> Tensor:
     """Fp8KVCache.append (row b into sequence b at pos[b]) and decode_attention (ctx_len = pos + 1) in one call of
     two launches, with bit-identical cache bytes and output: the reference's decode-body append (decode.cu:550-565)
     and k_attn. qkv bf16 [B][>= (hq + 2 hkv) 128] row-major; pos int32 [B]. A row with pos < 0 gets a zero row, a
     row with pos at or past max_ctx or len(cos) a NaN row; neither writes the cache. pos_out (int32 [B], another
-    tensor than pos) receives pos + 1. Returns bf16 [B][hq][128]."""
+    tensor than pos) receives pos + 1. piece_pages > 0: the sequence-local piece plan (nc_decode_step_fp8_pieces),
+    every sequence's output bits independent of the batch. Returns bf16 [B][hq][128]."""
     if qkv.dim() != 2 or qkv.dtype != torch.bfloat16 or not qkv.is_cuda or qkv.stride(1) != 1:
         raise ValueError("qkv must be a row-major bf16 [B][width] GPU tensor")
     B = qkv.shape[0]
@@ -99,11 +101,15 @@ def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_g
         workspace = decode_workspace(B, hq, cache.hkv, max_ctx, qkv.device)
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
-    check(hip_library().nc_decode_step_fp8(
-        pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos),
-        pointer(sin), cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks,
-        cache.num_blocks, window, B, hq, cache.hkv, max_ctx, scale, pointer(out), pointer(workspace),
-        workspace.numel() * workspace.element_size(), stream()))
+    args = (pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(q_gain), pointer(k_gain), pointer(cos),
+            pointer(sin), cos.shape[0], pointer(cache.pages), pointer(cache.block_table), cache.max_blocks,
+            cache.num_blocks, window, B, hq, cache.hkv, max_ctx, scale)
+    tail = (pointer(out), pointer(workspace), workspace.numel() * workspace.element_size(), stream())
+    lib = hip_library()
+    if piece_pages > 0:
+        check(lib.nc_decode_step_fp8_pieces(*args, piece_pages, *tail))
+    else:
+        check(lib.nc_decode_step_fp8(*args, *tail))
     return out
 
 

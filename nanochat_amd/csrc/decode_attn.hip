@@ -101,6 +101,7 @@ struct DecodeArgs {
     int2 *ws_desc;            /* [S]: each segment's piece count and first piece's wave */
     int max_ctx;              /* ctx_len is clamped to it */
     int unit_start, unit_end; /* schedule units a non-empty segment costs before its first and after its last page */
+    int piece_pages;          /* 0: pieces cut by the balanced split; > 0: fixed pieces (piece_len) */
 };
 
 /* The key range of sequence b: pages [first, last] (none if last < first), keys [begin, p]. */
@@ -142,6 +143,13 @@ __device__ __forceinline__ int pages_of(const DecodeArgs &a, int ctx) {
 __device__ __forceinline__ int units_of(const DecodeArgs &a, int ctx) {
     const int pg = pages_of(a, ctx);
     return pg > 0 ? pg + a.unit_start + a.unit_end : 0;
+}
+
+/* Fixed pieces: a segment of `pages` pages is cut into pieces of max(piece_pages, ceil(pages / DEC_MERGE_DIRECT))
+ * pages from its first page on (at most DEC_MERGE_DIRECT pieces, so k_merge reads them in one round trip). A
+ * function of the segment's own length only: its output bits do not depend on the batch. */
+__device__ __forceinline__ int piece_len(const DecodeArgs &a, int pages) {
+    return max(a.piece_pages, (pages + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT);
 }
 
 /* A k_decode wave's context lengths: seq_ctx of every sequence, in LDS when the batch fits (read from memory once
@@ -223,11 +231,21 @@ __device__ __forceinline__ void state_init(State &st) {
 
 /* The fused step's new key and value (codes and scales in LDS, key t = p % 16 of the last page): t >= 0 when
  * the piece appends. */
+/* Staged partial results: a piece that is a part of its segment leaves (Σ p v, max, sum) here, not in the
+ * workspace, while the wave still streams pages: stores issued between page loads hold up those loads' waits (the
+ * memory counter completes in order; measured: 10 µs on a config-5 layer cut into 8 pieces per segment). They go
+ * to the workspace when the stage is full and at the end of the wave. */
+#define DEC_PART_FLOATS 4096 /* 16 KB: pieces of G (128 + 2) floats each, at least one at G = 16 */
+#define DEC_PART_MAX 32
+
 struct StepLds {
     bf16_t q[DEC_MAX_G][NC_HEAD_DIM];
     uint8_t codes[2][NC_HEAD_DIM]; /* new key, new value */
     float scale[2];
     int blk;                       /* their block, -1: none */
+    int nparts;                    /* staged pieces */
+    int part_slot[DEC_PART_MAX];   /* their merge slots */
+    float part[DEC_PART_FLOATS];   /* piece i at i G 130: o [G][128] (value units), then (max, sum) [G][2] */
 };
 
 /* Put the new key and value into a page loaded before they were stored: lane (j, n) holds K row n, dims 32 j..,
@@ -490,10 +508,24 @@ __device__ __forceinline__ int block_checked(const DecodeArgs &a, int entry, int
 /* One window of at most 64 pages [base, base + nw) of segment (b, h): lane i's entry is page base + i's. The first
  * window of a fused piece also builds q once its pages are in flight, and the appending piece's key and value after
  * its first page (before the last). */
+__device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st,
+                             StepLds &sm);
+
+/* Fixed pieces: at the first page of the next piece (page number next_cut), finish the piece before it into its
+ * merge slot and start the next one from a fresh state. */
+__device__ __forceinline__ void cut_piece(const DecodeArgs &a, int b, int h, int page, const SeqRange &sr, int lane,
+                                          int &next_cut, State &st, StepLds &sm) {
+    if (page != next_cut) return;
+    const int len = piece_len(a, sr.last - sr.first + 1);
+    finish_piece(a, b, h, 0, (page - sr.first) / len - 1, false, lane, st, sm);
+    state_init(st);
+    next_cut += len;
+}
+
 template <bool FUSED, bool FIRST>
 __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h, int base, int nw, int entry,
                                               const SeqRange &sr, bool app, const QRows &qr, const KvRows &kr,
-                                              bf16x8 *qop, int lane, StepLds &sm, State &st) {
+                                              bf16x8 *qop, int lane, StepLds &sm, State &st, int &next_cut) {
     const int n = lane & 15, j = lane >> 4;
     const int patch_t = FUSED && app ? sr.p % NC_PAGE : -1;
     const int ids = lane < nw ? block_checked(a, entry, base + lane) : -1;
@@ -519,7 +551,10 @@ __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h,
             load_page(a, __builtin_amdgcn_readlane(ids, min(k + u + DEC_DEPTH - 1, last)), h, n, j,
                       r[(u + DEC_DEPTH - 1) % DEC_DEPTH]);
             __builtin_amdgcn_sched_barrier(0);
-            if (u == 0 || k + u < nw) attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
+            if (u == 0 || k + u < nw) {
+                if (a.piece_pages > 0) cut_piece(a, b, h, base + k + u, sr, lane, next_cut, st, sm);
+                attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
+            }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (FUSED && FIRST) {
                 if (app && k == 0 && u == 0 && !(nw == 1 && sr.p / NC_PAGE == base)) {
@@ -538,6 +573,8 @@ __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h,
 template <bool FUSED, bool TABLE>
 __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
                                            bool app, bf16x8 *qop, int lane, StepLds &sm, State &st) {
+    /* fixed pieces: the first cut after the run's first page */
+    int next_cut = a.piece_pages > 0 ? pg_lo + piece_len(a, sr.last - sr.first + 1) : -1;
     QRows qr;
     KvRows kr;
     const int entry = block_entry<TABLE>(a, b, pg_lo + lane);
@@ -546,12 +583,12 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
         load_kvrows<TABLE>(a, b, h, sr.p, lane, kr);
     }
     __builtin_amdgcn_sched_barrier(0);
-    stream_window<FUSED, true>(a, b, h, pg_lo, min(64, npg), entry, sr, app, qr, kr, qop, lane, sm, st);
+    stream_window<FUSED, true>(a, b, h, pg_lo, min(64, npg), entry, sr, app, qr, kr, qop, lane, sm, st, next_cut);
     for (int win = 64; win < npg; win += 64) {
         const int e = block_entry<TABLE>(a, b, pg_lo + win + lane);
         __builtin_amdgcn_sched_barrier(0);
         stream_window<FUSED, false>(a, b, h, pg_lo + win, min(64, npg - win), e, sr, app, qr, kr, qop, lane, sm,
-                                    st);
+                                    st, next_cut);
     }
 }
 
@@ -563,19 +600,34 @@ __device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, 
     return i < DEC_MERGE_DIRECT ? (size_t)s * DEC_MERGE_DIRECT + i : (size_t)S * DEC_MERGE_DIRECT + w + s;
 }
 
+/* The staged pieces to their workspace slots (slot [G][128] of ws_o, [G][2] of ws_ml, both contiguous per slot). */
+__device__ void flush_parts(const DecodeArgs &a, int lane, StepLds &sm) {
+    __syncthreads(); /* the stage's writes before other lanes' reads */
+    const int G = a.group, np = sm.nparts, per = G * (NC_HEAD_DIM + 2);
+    for (int i = 0; i < np; i++) {
+        const size_t slot = (size_t)sm.part_slot[i];
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(&sm.part[i * per]);
+        f32x4 *dst = reinterpret_cast<f32x4 *>(a.ws_o + slot * G * NC_HEAD_DIM);
+        for (int v = lane; v < G * NC_HEAD_DIM / 4; v += NC_WAVE) dst[v] = src[v];
+        if (lane < 2 * G) a.ws_ml[slot * G * 2 + lane] = sm.part[i * per + G * NC_HEAD_DIM + lane];
+    }
+    __syncthreads(); /* the reads done before the stage is reused */
+    sm.nparts = 0;
+}
+
 /* Finish piece `piece` of segment (b, h), wave w: the whole segment writes the normalised bf16 output; a part of it
- * writes (Σ p v in value units, max, sum) to its merge slot, which k_merge combines. Lane (j, n) holds dims
+ * stages (Σ p v in value units, max, sum) for its merge slot, which k_merge combines. Lane (j, n) holds dims
  * (4 j + i) 8 + bb of head n. */
-__device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st) {
-    const int n = lane & 15, j = lane >> 4;
+__device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st,
+                             StepLds &sm) {
+    const int n = lane & 15, j = lane >> 4, G = a.group;
     float l = st.l;
     l += shfl_xor_f(l, 16);
     l += shfl_xor_f(l, 32);
-    if (n >= a.group) return;
     const float unit = exp2i(st.e_ref - 126); /* o * unit: Σ p v in value units */
-    const int head = h * a.group + n;
     if (whole) {
-        bf16_t *dst = a.out + ((size_t)b * a.hq + head) * NC_HEAD_DIM;
+        if (n >= G) return;
+        bf16_t *dst = a.out + ((size_t)b * a.hq + h * G + n) * NC_HEAD_DIM;
         const float inv = l > 0.f ? unit / l : 0.f; /* 0: every block of the segment was missing */
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -586,19 +638,27 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
         }
         return;
     }
-    const size_t slot = merge_slot(a, b * a.hkv + h, piece, w) * a.group + n;
-    float *dst = a.ws_o + slot * NC_HEAD_DIM;
+    const int per = G * (NC_HEAD_DIM + 2);
+    if ((sm.nparts + 1) * per > DEC_PART_FLOATS || sm.nparts == DEC_PART_MAX) flush_parts(a, lane, sm);
+    const int at = sm.nparts * per;
+    if (n < G) {
+        float *o = &sm.part[at + n * NC_HEAD_DIM];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const f32x4 lo = {st.o[0][i] * unit, st.o[1][i] * unit, st.o[2][i] * unit, st.o[3][i] * unit};
-        const f32x4 hi = {st.o[4][i] * unit, st.o[5][i] * unit, st.o[6][i] * unit, st.o[7][i] * unit};
-        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[0] = lo;
-        reinterpret_cast<f32x4 *>(dst + (4 * j + i) * 8)[1] = hi;
+        for (int i = 0; i < 4; i++) {
+            const f32x4 lo = {st.o[0][i] * unit, st.o[1][i] * unit, st.o[2][i] * unit, st.o[3][i] * unit};
+            const f32x4 hi = {st.o[4][i] * unit, st.o[5][i] * unit, st.o[6][i] * unit, st.o[7][i] * unit};
+            reinterpret_cast<f32x4 *>(o + (4 * j + i) * 8)[0] = lo;
+            reinterpret_cast<f32x4 *>(o + (4 * j + i) * 8)[1] = hi;
+        }
+        if (j == 0) {
+            sm.part[at + G * NC_HEAD_DIM + 2 * n] = st.m;
+            sm.part[at + G * NC_HEAD_DIM + 2 * n + 1] = l;
+        }
     }
-    if (j == 0) {
-        a.ws_ml[2 * slot] = st.m;
-        a.ws_ml[2 * slot + 1] = l;
-    }
+    if (lane == 0) sm.part_slot[sm.nparts] = (int)merge_slot(a, b * a.hkv + h, piece, w);
+    __syncthreads();
+    sm.nparts = sm.nparts + 1; /* every lane writes the same value */
+    __syncthreads();
 }
 
 /* Schedule units of the whole batch: every wave derives the same value from the live context lengths and keeps
@@ -624,27 +684,16 @@ __device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *
     return total * a.hkv;
 }
 
-template <bool FUSED, bool TABLE>
-__global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
-    __shared__ StepLds sm;
-    __shared__ int ctx_lds[DEC_LDS_SEQS];
-    const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
-    int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
-
-    const int total = schedule_total(a, w, W, lane, lds);
-    __syncthreads(); /* lds complete before other lanes' reads */
-    const int chunk = max((total + W - 1) / W, DEC_MIN_CHUNK);
-    const int start = w * chunk;
-    if (start >= total) return;
-    int remaining = min(chunk, total - start);
-
-    /* the segment holding `start`: sequence b0, then kv head and unit offset */
-    int carry = 0, b = -1, units_b = 0;
+/* The segment holding unit u of the flattened list: sequence b, kv head h and the segment's first unit. */
+__device__ __forceinline__ void find_segment(const DecodeArgs &a, const int *lds, int u, int lane, int &b, int &h,
+                                             int &seg_base) {
+    int carry = 0, units_b = 0;
+    b = -1;
     for (int base = 0; base < a.B && b < 0; base += 64) {
         const int bb = base + lane;
         const int pg = bb < a.B ? units_of(a, ctx_at(a, lds, bb)) : 0;
         const int incl = wave_inclusive_sum(pg, lane);
-        const unsigned long long hit = __ballot(bb < a.B && carry + incl * a.hkv > start);
+        const unsigned long long hit = __ballot(bb < a.B && carry + incl * a.hkv > u);
         if (hit) {
             const int first = __builtin_ctzll(hit);
             b = base + first;
@@ -654,9 +703,49 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             carry += __shfl(incl, 63, 64) * a.hkv;
         }
     }
-    const int into = start - carry; /* offset inside sequence b */
-    int h = into / units_b, off = into % units_b;
-    int seg_base = start - off; /* the segment's first unit in the flattened list */
+    const int into = u - carry; /* offset inside sequence b */
+    h = into / units_b;
+    seg_base = u - into % units_b;
+}
+
+/* Fixed pieces: the piece boundary nearest to unit u. A segment's boundaries are its first unit, the units of its
+ * pieces' first pages after the first (its start units go with its first piece) and its end (its end units go with
+ * its last piece). Every wave rounds a shared slice end alike, so the snapped slices still tile the list. */
+__device__ __forceinline__ int snap_unit(const DecodeArgs &a, const int *lds, int u, int lane) {
+    int b, h, seg_base;
+    find_segment(a, lds, u, lane, b, h, seg_base);
+    const int pages = pages_of(a, ctx_at(a, lds, b)), len = piece_len(a, pages), np = (pages + len - 1) / len;
+    const int units = pages + a.unit_start + a.unit_end;
+    const int k = min(max((u - seg_base - a.unit_start + len / 2) / len, 0), np); /* numerator >= -unit_start */
+    const int at = u - seg_base < a.unit_start ? 0 : k;
+    return seg_base + (at == 0 ? 0 : at == np ? units : a.unit_start + at * len);
+}
+
+template <bool FUSED, bool TABLE>
+__global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
+    __shared__ StepLds sm;
+    __shared__ int ctx_lds[DEC_LDS_SEQS];
+    const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
+    int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
+
+    if (lane == 0) sm.nparts = 0;
+    const int total = schedule_total(a, w, W, lane, lds);
+    __syncthreads(); /* lds complete before other lanes' reads */
+    const int chunk = max((total + W - 1) / W, DEC_MIN_CHUNK);
+    int start = w * chunk;
+    if (start >= total) return;
+    int end = min(start + chunk, total);
+    if (a.piece_pages > 0) { /* whole fixed pieces: both ends at the nearest piece boundary */
+        start = snap_unit(a, lds, start, lane);
+        end = end >= total ? total : snap_unit(a, lds, end, lane);
+        if (start >= end) return;
+    }
+    int remaining = end - start;
+
+    /* the segment holding `start`: sequence b, kv head h, its first unit seg_base */
+    int b, h, seg_base;
+    find_segment(a, lds, start, lane, b, h, seg_base);
+    int off = start - seg_base;
 
     while (remaining > 0) {
         const SeqRange sr = seq_range_of(a, ctx_at(a, lds, b));
@@ -672,6 +761,12 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
         off = 0;
         seg_base += units;
         if (hi > lo) {
+            /* the piece this run ends with (finished after it) and the segment's piece count; fixed pieces from
+             * the segment's first page, else one per wave (piece i of the segment is wave w_first + i) */
+            const int len = a.piece_pages > 0 ? piece_len(a, seg_pages) : 0;
+            const int piece = len ? (hi - 1) / len : w - w_first;
+            const int seg_pieces = len ? (seg_pages + len - 1) / len : pieces;
+            const bool whole = seg_pieces == 1;
             bf16x8 qop[4]; /* the fused step builds it in attend_run */
             if constexpr (!FUSED) {
                 if (n < a.group) {
@@ -687,8 +782,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             State st;
             state_init(st);
             attend_run<FUSED, TABLE>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
-            finish_piece(a, b, h, w, w - w_first, lo == 0 && hi == seg_pages, lane, st);
-            if (lo == 0 && lane == 0) a.ws_desc[b * a.hkv + h] = make_int2(pieces, w_first);
+            finish_piece(a, b, h, w, piece, whole, lane, st, sm);
+            if (lo == 0 && lane == 0) a.ws_desc[b * a.hkv + h] = make_int2(seg_pieces, len ? 0 : w_first);
             if (FUSED && hi == seg_pages) store_new_kv(a, h, sr.p, lane, sm);
         }
         if (++h == a.hkv) {
@@ -699,6 +794,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             if (b >= a.B) break;
         }
     }
+    flush_parts(a, lane, sm); /* after the last pages: these stores hold up no wait */
 }
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
@@ -853,11 +949,11 @@ extern "C" int nc_decode_attn_fp8(const void *q, const uint8_t *cache, const int
     return decode_launch(a, false, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
 }
 
-/* The fused step's checks and launch, shared by the workspace and the static-scratch entry points. */
+/* The fused step's checks and launch, shared by the workspace, fixed-piece and static-scratch entry points. */
 static int decode_step(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
                        const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
                        uint8_t *cache, const int32_t *block_table, int max_blocks, int num_blocks, int window, int B,
-                       int hq, int hkv, int max_ctx, float sm_scale, void *out, void *workspace,
+                       int hq, int hkv, int max_ctx, float sm_scale, int piece_pages, void *out, void *workspace,
                        long long workspace_bytes, void *stream) {
     NC_REQUIRE(B >= 0, "B = %d < 0", B);
     if (B == 0) return 0;
@@ -879,6 +975,7 @@ static int decode_step(const void *qkv, long long row_stride, const int32_t *pos
     a.qkv = (const bf16_t *)qkv; a.row_stride = row_stride; a.q_gain = q_gain; a.k_gain = k_gain;
     a.cos = cos; a.sin = sin; a.rope_len = rope_len;
     a.window = window; a.B = B; a.hq = hq; a.hkv = hkv;
+    a.piece_pages = piece_pages;
     return decode_launch(a, true, out, workspace, workspace_bytes, max_ctx, sm_scale, stream);
 }
 
@@ -888,8 +985,20 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long row_stride, const i
                                   int num_blocks, int window, int B, int hq, int hkv, int max_ctx, float sm_scale,
                                   void *out, void *workspace, long long workspace_bytes, void *stream) {
     return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
-                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, workspace, workspace_bytes,
-                       stream);
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,
+                                         const float *q_gain, const float *k_gain, const float *cos,
+                                         const float *sin, int rope_len, uint8_t *cache, const int32_t *block_table,
+                                         int max_blocks, int num_blocks, int window, int B, int hq, int hkv,
+                                         int max_ctx, float sm_scale, int piece_pages, void *out, void *workspace,
+                                         long long workspace_bytes, void *stream) {
+    NC_REQUIRE(piece_pages >= 1 && piece_pages <= 1 << 16, "piece_pages = %d outside [1, 65536]", piece_pages);
+    return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, piece_pages, out, workspace,
+                       workspace_bytes, stream);
 }
 
 /* ------------------------------------------------------------------------------------------------------------
@@ -936,8 +1045,8 @@ extern "C" int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride,
                hq, hkv, need, NC_DECODE_SCRATCH_BYTES);
     if (B <= 0 || need == 0) /* nothing to launch: the shared checks report a bad B or head count */
         return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
-                           max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, nullptr, 0, stream);
+                           max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, nullptr, 0, stream);
     return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
-                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, out, scratch_address(),
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, scratch_address(),
                        NC_DECODE_SCRATCH_BYTES, stream);
 }

@@ -22,8 +22,9 @@
  *
  * A decode step is dec_set_active, dec_launch_body, dec_launch_head, dec_tokens. The body runs per layer: the
  * residual mix (nc_mix_bf16, where it is not the identity), the qkv slot GEMM of the normed rows, the
- * value-embedding mix (nc_value_embed_bf16), the fused append + attention (nc_decode_step_fp8), the o projection
- * (RESID), up (RELU2_NORM) and down (RESID) GEMMs. The head is the lm_head GEMM (NORM_F32) and nc_choose_tokens,
+ * value-embedding mix (nc_value_embed_bf16), the fused append + attention (nc_decode_step_fp8_pieces: sequence-local
+ * pieces, so a request's bits do not depend on the batch), the o projection (RESID), up (RELU2_NORM) and down
+ * (RESID) GEMMs. The head is the lm_head GEMM (NORM_F32) and nc_choose_tokens,
  * which writes each active slot's choice as its next input token and advances its position (k_commit). Idle slots
  * carry position -1: the decode step does no work for them and the choice leaves them untouched.
  *
@@ -50,6 +51,9 @@
 #define DEC_GLOBAL_PTRS 4
 #define DEC_LAYER_PTRS 8
 #define DEC_SM_SCALE 0.08838834764831845f /* 1 / sqrt(128) */
+/* The decode attention's sequence-local pieces (nc_decode_step_fp8_pieces): a request's tokens depend on neither the
+ * batch nor the store, as the reference promises (inference/decoder.py:124-125). */
+#define DEC_PIECE_PAGES 16
 
 struct DecLayer {
     const void *qkv, *o, *up, *down, *ve; /* bf16 weights [out][in]; ve [vocab][Hkv 128] or null */
@@ -168,9 +172,10 @@ static int enqueue_body(Decoder *d, int n) {
     for (int l = 0; l < d->L; l++) {
         const DecLayer &ly = d->layer[l];
         DEC_TRY(enqueue_qkv(d, r, n, l));
-        DEC_TRY(nc_decode_step_fp8(r.qkv, cols, r.pos, nullptr, ly.q_gain, ly.k_gain, d->cos, d->sin, d->max_len,
-                                   pool(d, l), nullptr, d->max_blocks, d->B * d->max_blocks, ly.window, n, d->H,
-                                   d->Hkv, d->max_len, DEC_SM_SCALE, r.o, d->ws_dec, d->ws_dec_bytes, d->stream));
+        DEC_TRY(nc_decode_step_fp8_pieces(r.qkv, cols, r.pos, nullptr, ly.q_gain, ly.k_gain, d->cos, d->sin,
+                                          d->max_len, pool(d, l), nullptr, d->max_blocks, d->B * d->max_blocks,
+                                          ly.window, n, d->H, d->Hkv, d->max_len, DEC_SM_SCALE, DEC_PIECE_PAGES, r.o,
+                                          d->ws_dec, d->ws_dec_bytes, d->stream));
         DEC_TRY(enqueue_mlp(d, r, n, l));
     }
     return 0;

@@ -42,6 +42,9 @@ from nanochat_amd.sampling import choose_tokens, choose_workspace
 from nanochat_amd.slot_gemm import NORM_F32, NORM_STORE, RELU2_NORM, RESID, slot_gemm
 
 EPS = torch.finfo(torch.float32).eps  # the RMS norms' epsilon (model/ops/linear.py:20)
+# the decode attention's sequence-local pieces (nc_decode_step_fp8_pieces, as the dec_* handle): a request's tokens
+# depend on neither the batch nor the other requests (inference/decoder.py:124-125)
+PIECE_PAGES = 16
 
 
 @dataclass(frozen=True)
@@ -352,7 +355,8 @@ class Fp8Decoder:
             self._value_embed(l, qkv, x, tok)
             # the append (decode.cu:550-565) and attention in one call: sequence b is cache row b
             o = decode_step(qkv, self.caches[l], pos, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
-                            max_ctx=self.max_len, window=self.cfg.window(l), workspace=self.ws)
+                            max_ctx=self.max_len, window=self.cfg.window(l), workspace=self.ws,
+                            piece_pages=PIECE_PAGES)
             slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
             u = slot_gemm(x, lw["wup"], RELU2_NORM)
             slot_gemm(u, lw["wdown"], RESID, res=x, out=x)

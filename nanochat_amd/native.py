@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
     "nc_decode_attn_fp8": (I32, [P, P, P, I32, I32, P, I32, I32, I32, I32, I32, F32, P, P, I64, P]),
     "nc_decode_step_fp8": (I32, [P, I64, P, P, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P,
                                  P, I64, P]),
+    "nc_decode_step_fp8_pieces": (I32, [P, I64, P, P, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, I32, F32,
+                                        I32, P, P, I64, P]),
     "nc_decode_step_fp8_noalloc": (I32, [P, I64, P, P, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, I32,
                                          F32, P, P]),
     "nc_prefill_attn_fp8": (I32, [P, P, P, I32, P, P, I32, I32, I32, I32, I32, I32, F32, P, P]),
