@@ -126,12 +126,13 @@ int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos
                        long long workspace_bytes, void *stream);
 
 /* nc_decode_step_fp8 with the sequence-local piece plan: every (sequence, kv head) segment of n pages (its keys'
- * pages) is cut into fixed pieces of max(piece_pages, ceil(n / 8)) pages from its first page, each piece's softmax
- * starts afresh, and the pieces merge in piece order; a wave takes whole pieces (the balanced split's slice ends
- * rounded to the nearest piece boundary). A sequence's output bits are then a function of its own query, context
- * and cache alone: decoded alone or in any batch, it gets the same bits, as with the reference's one block per
- * (head, slot). Arguments as nc_decode_step_fp8, plus piece_pages >= 1 (the balanced split, the plain entry point,
- * rebalances every sequence's pieces with the batch and is faster on few, long sequences).
+ * pages) is cut into fixed pieces of max(piece_pages, ceil(n / 32)) pages from its first page, each piece's
+ * softmax starts afresh, and the pieces merge in a fixed order set by the piece count; a wave takes whole pieces
+ * (the balanced split's slice ends rounded to the nearest piece boundary). A sequence's output bits are then a
+ * function of its own query, context and cache alone: decoded alone or in any batch, it gets the same bits, as
+ * with the reference's one block per (head, slot). Arguments as nc_decode_step_fp8, plus piece_pages in
+ * [1, 65536]; 16 measured fastest. The plain entry point's balanced split is 3 % faster on a config-5 layer and
+ * 11 % on config 3's ragged batch, but its bits depend on the batch.
  * Replaces: k_prologue's append and k_attn (model/kernels/decode.cu:550-675), whose tokens depend on neither the
  * batch nor the store (inference/decoder.py:124-125); the decoder handle (dec_*) runs this entry point. */
 int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,

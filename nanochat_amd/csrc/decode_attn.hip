@@ -8,6 +8,8 @@
  * contiguous slice of it, computed in the kernel from the live context lengths, so a ragged batch stays balanced.
  * A slice is processed as pieces, one per segment (b, h) it touches. All G = Hq / Hkv query heads of a kv head
  * ride in the same wave, so every fp8 byte is read from HBM once.
+ * The piece plan (nc_decode_step_fp8_pieces) instead cuts every segment into fixed pieces set by its own length
+ * (piece_len) and rounds the slice ends to piece boundaries, so a sequence's bits do not depend on the batch.
  *
  * Per page (16 keys) a wave computes
  *   scores  Sᵀ[16 keys][16 heads] = K[16][128] · Qᵀ, 4 v_mfma_f32_16x16x32_bf16. A is the K tile as loaded (lane:
@@ -56,6 +58,7 @@
 #define DEC_MAX_G 16
 #define DEC_MAX_WAVES 8192  /* workspace slots are sized for this many waves */
 #define DEC_MERGE_DIRECT 8  /* pieces of a segment k_merge reads in its first round trip */
+#define DEC_PIECES_MAX 32   /* fixed pieces of a segment at most */
 #define DEC_MIN_CHUNK 8     /* pages per wave at least: fewer pieces to merge on small problems */
 #define DEC_LAZY 8.0f       /* log2 headroom before the softmax reference moves */
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
@@ -145,11 +148,11 @@ __device__ __forceinline__ int units_of(const DecodeArgs &a, int ctx) {
     return pg > 0 ? pg + a.unit_start + a.unit_end : 0;
 }
 
-/* Fixed pieces: a segment of `pages` pages is cut into pieces of max(piece_pages, ceil(pages / DEC_MERGE_DIRECT))
- * pages from its first page on (at most DEC_MERGE_DIRECT pieces, so k_merge reads them in one round trip). A
- * function of the segment's own length only: its output bits do not depend on the batch. */
+/* Fixed pieces: a segment of `pages` pages is cut into pieces of max(piece_pages, ceil(pages / DEC_PIECES_MAX))
+ * pages from its first page on (at most DEC_PIECES_MAX pieces, each with its own workspace slot). A function of
+ * the segment's own length only: its output bits do not depend on the batch. */
 __device__ __forceinline__ int piece_len(const DecodeArgs &a, int pages) {
-    return max(a.piece_pages, (pages + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT);
+    return max(a.piece_pages, (pages + DEC_PIECES_MAX - 1) / DEC_PIECES_MAX);
 }
 
 /* A k_decode wave's context lengths: seq_ctx of every sequence, in LDS when the batch fits (read from memory once
@@ -235,7 +238,7 @@ __device__ __forceinline__ void state_init(State &st) {
  * workspace, while the wave still streams pages: stores issued between page loads hold up those loads' waits (the
  * memory counter completes in order; measured: 10 µs on a config-5 layer cut into 8 pieces per segment). They go
  * to the workspace when the stage is full and at the end of the wave. */
-#define DEC_PART_FLOATS 4096 /* 16 KB: pieces of G (128 + 2) floats each, at least one at G = 16 */
+#define DEC_PART_FLOATS 6144 /* 24 KB: pieces of G (128 + 2) floats each, 11 at G = 4, 2 at G = 16 */
 #define DEC_PART_MAX 32
 
 struct StepLds {
@@ -592,11 +595,13 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
     }
 }
 
-/* The workspace slot of piece i (the i-th wave to touch segment s, wave w): the first DEC_MERGE_DIRECT pieces of a
- * segment sit together at s * DEC_MERGE_DIRECT + i; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's
- * pieces lie in consecutive segments and the waves' slices are in segment order, so w + s never repeats). */
+/* The workspace slot of piece i of segment s, made by wave w. Fixed pieces: s * DEC_PIECES_MAX + i. Pieces cut
+ * by the balanced split (piece i is the i-th wave to touch the segment): the first DEC_MERGE_DIRECT sit together
+ * at s * DEC_MERGE_DIRECT + i; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's pieces lie in
+ * consecutive segments and the waves' slices are in segment order, so w + s never repeats). */
 __device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, int w) {
     const int S = a.B * a.hkv;
+    if (a.piece_pages > 0) return (size_t)s * DEC_PIECES_MAX + i;
     return i < DEC_MERGE_DIRECT ? (size_t)s * DEC_MERGE_DIRECT + i : (size_t)S * DEC_MERGE_DIRECT + w + s;
 }
 
@@ -798,56 +803,111 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 }
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
- * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale, combined online in piece order. Thread t holds
- * head t / 16, dims 8 (t % 16)..+8 (16 lanes per head, ceil(G / 4) waves). The kernel is latency-bound, so it needs
- * no schedule: the segment's descriptor (piece count, first wave) and the first DEC_MERGE_DIRECT pieces' slots are
- * loaded together, in one round trip; a segment with more pieces reads the rest in a second. */
+ * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale. A thread holds head n, dims 8 c..8 c + 8 (16
+ * lanes per head) of one of Q = 256 / (16 G) groups. Group q folds, in order, pieces 8 q..8 q + 7, then
+ * 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a given
+ * piece count and head group, so the bits depend on nothing else. The kernel is latency-bound: the first round's
+ * slots do not depend on the segment's descriptor (fixed pieces: s * DEC_PIECES_MAX + i; the balanced split's first
+ * DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, one round trip for up to 8 Q fixed
+ * pieces (8 for the balanced split, every segment of config 3). */
 #define MERGE_LANES 16
+#define MERGE_THREADS 256
 
-__global__ void __launch_bounds__(256) k_merge(DecodeArgs a) {
-    const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, n = t / MERGE_LANES, c = t % MERGE_LANES;
-    if (n >= a.group) return; /* whole 16-lane groups */
-    const int2 d = a.ws_desc[s];
+struct MergeAcc {
+    float m, l, o[8];
+};
+
+__device__ __forceinline__ void merge_fold(MergeAcc &r, float m_k, float l_k, const float *o_k) {
+    const float m_new = fmaxf(r.m, m_k);
+    const float a_old = __builtin_amdgcn_exp2f(r.m - m_new), a_new = __builtin_amdgcn_exp2f(m_k - m_new);
+    r.l = r.l * a_old + l_k * a_new;
+#pragma unroll
+    for (int e = 0; e < 8; e++) r.o[e] = r.o[e] * a_old + o_k[e] * a_new;
+    r.m = m_new;
+}
+
+/* Pieces base..base + 7 (those below `pieces`) of segment s into r: slots from merge_slot, or, with `spec`, the
+ * first round's fixed slots loaded before the piece count is known (every one of them inside the workspace). */
+__device__ __forceinline__ void merge_round(const DecodeArgs &a, int s, int2 d, int base, int n, int c,
+                                            MergeAcc &r) {
     f32x2 ml[DEC_MERGE_DIRECT];
     f32x4 ov[DEC_MERGE_DIRECT][2];
 #pragma unroll
-    for (int k = 0; k < DEC_MERGE_DIRECT; k++) { /* speculative: slots past the piece count are not used */
-        const size_t slot = ((size_t)s * DEC_MERGE_DIRECT + k) * a.group + n;
-        ml[k] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
-        ov[k][0] = src[0];
-        ov[k][1] = src[1];
+    for (int k = 0; k < DEC_MERGE_DIRECT; k++) {
+        if (base + k < d.x) {
+            const size_t slot = merge_slot(a, s, base + k, d.y + base + k) * a.group + n;
+            ml[k] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
+            ov[k][0] = src[0];
+            ov[k][1] = src[1];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < DEC_MERGE_DIRECT; k++) {
+        if (base + k < d.x) {
+            const float o_k[8] = {ov[k][0][0], ov[k][0][1], ov[k][0][2], ov[k][0][3],
+                                  ov[k][1][0], ov[k][1][1], ov[k][1][2], ov[k][1][3]};
+            merge_fold(r, ml[k][0], ml[k][1], o_k);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(MERGE_THREADS) k_merge(DecodeArgs a) {
+    __shared__ MergeAcc grp[MERGE_THREADS];
+    const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, G = a.group;
+    const int row = G * MERGE_LANES, Q = MERGE_THREADS / row, q = t / row, n = (t % row) / MERGE_LANES,
+              c = t % MERGE_LANES;
+    const int2 d = a.ws_desc[s];
+    /* the first round's slots, loaded with the descriptor: slot(i) needs no d where spec holds */
+    const bool fixed = a.piece_pages > 0;
+    const bool spec = q < Q && (fixed ? DEC_MERGE_DIRECT * (q + 1) <= DEC_PIECES_MAX : q == 0);
+    f32x2 ml[DEC_MERGE_DIRECT];
+    f32x4 ov[DEC_MERGE_DIRECT][2];
+    if (spec) {
+#pragma unroll
+        for (int k = 0; k < DEC_MERGE_DIRECT; k++) {
+            const int i = DEC_MERGE_DIRECT * q + k;
+            const size_t slot = ((size_t)s * (fixed ? DEC_PIECES_MAX : DEC_MERGE_DIRECT) + i) * G + n;
+            ml[k] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
+            ov[k][0] = src[0];
+            ov[k][1] = src[1];
+        }
     }
     const int pieces = d.x;
     if (pieces <= 1) return; /* one piece: k_decode wrote the output; none: an empty sequence's zero row */
-    float mmax = DEC_M_INIT, sum = 0.f, acc[8];
+    MergeAcc r;
+    r.m = DEC_M_INIT, r.l = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] = 0.f;
-    auto fold = [&](f32x2 m_l, const f32x4 &o0, const f32x4 &o1) {
-        const float m_new = fmaxf(mmax, m_l[0]);
-        const float a_old = __builtin_amdgcn_exp2f(mmax - m_new), a_new = __builtin_amdgcn_exp2f(m_l[0] - m_new);
-        sum = sum * a_old + m_l[1] * a_new;
+    for (int e = 0; e < 8; e++) r.o[e] = 0.f;
+    if (q < Q) {
+        if (spec) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            acc[e] = acc[e] * a_old + o0[e] * a_new;
-            acc[4 + e] = acc[4 + e] * a_old + o1[e] * a_new;
+            for (int k = 0; k < DEC_MERGE_DIRECT; k++) {
+                if (DEC_MERGE_DIRECT * q + k < pieces) {
+                    const float o_k[8] = {ov[k][0][0], ov[k][0][1], ov[k][0][2], ov[k][0][3],
+                                          ov[k][1][0], ov[k][1][1], ov[k][1][2], ov[k][1][3]};
+                    merge_fold(r, ml[k][0], ml[k][1], o_k);
+                }
+            }
+        } else if (DEC_MERGE_DIRECT * q < pieces) {
+            merge_round(a, s, d, DEC_MERGE_DIRECT * q, n, c, r);
         }
-        mmax = m_new;
-    };
-#pragma unroll
-    for (int k = 0; k < DEC_MERGE_DIRECT; k++)
-        if (k < pieces) fold(ml[k], ov[k][0], ov[k][1]);
-    for (int k = DEC_MERGE_DIRECT; k < pieces; k++) {
-        const size_t slot = merge_slot(a, s, k, d.y + k) * a.group + n;
-        const f32x2 m_l = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
-        fold(m_l, src[0], src[1]);
+        for (int base = DEC_MERGE_DIRECT * (q + Q); base < pieces; base += DEC_MERGE_DIRECT * Q)
+            merge_round(a, s, d, base, n, c, r);
     }
-    const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+    grp[t] = r;
+    __syncthreads();
+    if (q != 0) return;
+    for (int g = 1; g < Q && DEC_MERGE_DIRECT * g < pieces; g++) {
+        const MergeAcc &o = grp[g * row + t];
+        merge_fold(r, o.m, o.l, o.o);
+    }
+    const float inv = r.l > 0.f ? 1.0f / r.l : 0.f;
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = acc[e] * inv;
-    store_bf16x8(a.out + ((size_t)b * a.hq + h * a.group + n) * NC_HEAD_DIM + 8 * c, v);
+    for (int e = 0; e < 8; e++) v[e] = r.o[e] * inv;
+    store_bf16x8(a.out + ((size_t)b * a.hq + h * G + n) * NC_HEAD_DIM + 8 * c, v);
 }
 
 /* Resident single-wave workgroups of k_decode on the current device (cached per device). */
@@ -878,8 +938,12 @@ static int decode_waves() {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-/* Partial-result slots: the first DEC_MERGE_DIRECT pieces of every segment, then one per (wave, segment) offset. */
-static size_t merge_slots(size_t S) { return S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S; }
+/* Partial-result slots: for the balanced split the first DEC_MERGE_DIRECT pieces of every segment, then one per
+ * (wave, segment) offset; for fixed pieces DEC_PIECES_MAX per segment. */
+static size_t merge_slots(size_t S) {
+    const size_t balanced = S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S, fixed = S * DEC_PIECES_MAX;
+    return balanced > fixed ? balanced : fixed;
+}
 
 extern "C" long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx) {
     if (B <= 0 || hq <= 0 || hkv <= 0 || max_ctx <= 0 || hq % hkv) return 0;
@@ -929,8 +993,7 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else if (a.block_table) hipLaunchKernelGGL((k_decode<false, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
-    const unsigned merge_threads = (unsigned)(((a.group * MERGE_LANES + NC_WAVE - 1) / NC_WAVE) * NC_WAVE);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(merge_threads), 0, st, a);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(MERGE_THREADS), 0, st, a);
     NC_LAUNCH_CHECK();
     return 0;
 }
