@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
-    ap.add_argument("--only", choices=["decode1", "decode2", "prefill4", "e2e5", "handle5"],
+    ap.add_argument("--only", choices=["decode1", "decode2", "prefill4", "e2e5", "handle5", "gemm5"],
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
     ap.add_argument("--unfused", action="store_true",
@@ -361,6 +361,52 @@ def extra_e2e_cfg5(dev, steps: int | None = None, cpu_s: float | None = None) ->
     return res
 
 
+def extra_gemm_cfg5(dev, stream) -> dict:
+    """Config 5's four decode-step GEMMs at M = 128 (qkv 4992x1664 NORM_STORE, o 1664x1664 RESID, up 6656x1664
+    RELU2_NORM, down 1664x6656 RESID): nc_slot_gemm_bf16 against the library's torch.matmul(x, Wᵀ) (plain bf16
+    product, no epilogue), each over LAYERS weight copies in turn so that every call reads its W cold, as the
+    decode step does; graphs of LAYERS calls, HIP events on their stream."""
+    import torch
+
+    from nanochat_amd.decoder import CONFIG5
+    from nanochat_amd.slot_gemm import NORM_STORE, RELU2_NORM, RESID, slot_gemm
+
+    d, m, layers = CONFIG5.model.d_model, CONFIG5.batch, CONFIG5.model.layers
+    g = torch.Generator(device=dev).manual_seed(5)
+    shapes = (("qkv", 3 * d, d, NORM_STORE), ("o", d, d, RESID), ("up", 4 * d, d, RELU2_NORM),
+              ("down", d, 4 * d, RESID))
+    res = {"workload": "cfg5 decode GEMMs, M 128, bf16 W [n][k]", "weight_copies": layers}
+    total = {"slot_gemm": 0.0, "torch_matmul": 0.0}
+    for name, n, k, epi in shapes:
+        ws = [torch.randn(n, k, generator=g, device=dev).mul_(k ** -0.5).to(torch.bfloat16) for _ in range(layers)]
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        r = torch.randn(m, n, generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        turn = [0, 0]
+
+        def ours():
+            w = ws[turn[0] % layers]
+            turn[0] += 1
+            slot_gemm(x, w, epi, res=r if epi == RESID else None, out=out)
+
+        def lib():
+            w = ws[turn[1] % layers]
+            turn[1] += 1
+            torch.matmul(x, w.t(), out=out)
+
+        row = {"n": n, "k": k, "w_bytes": n * k * 2}
+        for key, fn in (("slot_gemm", ours), ("torch_matmul", lib)):
+            ms = time_calls(fn, layers, 20, stream)
+            row[f"{key}_us"] = round(ms * 1e3, 3)
+            row[f"{key}_GB_s"] = round(n * k * 2 / (ms * 1e-3) / 1e9, 1)
+            total[key] += ms * 1e3
+        res[name] = row
+        del ws
+        torch.cuda.empty_cache()
+    res["per_layer_us"] = {key: round(v, 2) for key, v in total.items()}
+    return res
+
+
 def extra_e2e_cfg5_handle(dev, steps: int | None = None) -> dict:
     """Config 5 through the dec_* handle (csrc/decoder.hip, the reference's NativeDecoder protocol,
     inference/decoder.py:194-232): the model and prompts of e2e_cfg5; every prompt admitted (dec_set_prompt, greedy),
@@ -618,7 +664,8 @@ def main():
         run = {"decode1": lambda: extra_decode_cfg1(dev, s, cpu_s), "decode2": lambda: extra_decode_cfg2(dev, s, cpu_s),
                "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
                "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s),
-               "handle5": lambda: extra_e2e_cfg5_handle(dev, args.e2e_steps)}[args.only]
+               "handle5": lambda: extra_e2e_cfg5_handle(dev, args.e2e_steps),
+               "gemm5": lambda: extra_gemm_cfg5(dev, s)}[args.only]
         print(json.dumps(run()), flush=True)
         return
     cfg = CONFIG3
