@@ -102,3 +102,23 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
 /* ------------------------------------------------------------------------------------------ lane exchanges */
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, NC_WAVE); }
+
+/* v of lane (lane ^ MASK), MASK 1, 2 or 4: exchanges inside 8-lane rows as DPP moves (VALU latency, no LDS
+ * round trip): quad_perm [1,0,3,2] and [2,3,0,1]; for 4, row_shl:4 (lane + 4) where lane bit 2 is clear and
+ * row_shr:4 (lane - 4) where it is set, both inside the lane's 16-lane DPP row. */
+template <int MASK> __device__ __forceinline__ uint32_t xor8_u32(uint32_t v) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4, "exchanges inside 8-lane rows");
+    const int i = (int)v;
+    if constexpr (MASK == 1) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0xB1, 0xf, 0xf, false);
+    } else if constexpr (MASK == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0x4E, 0xf, 0xf, false);
+    } else {
+        const int up = __builtin_amdgcn_mov_dpp(i, 0x104, 0xf, 0xf, false);
+        const int dn = __builtin_amdgcn_mov_dpp(i, 0x114, 0xf, 0xf, false);
+        return (uint32_t)((__lane_id() & 4) ? dn : up);
+    }
+}
+template <int MASK> __device__ __forceinline__ float xor8_f(float v) {
+    return __uint_as_float(xor8_u32<MASK>(__float_as_uint(v)));
+}

@@ -163,12 +163,15 @@ __device__ __forceinline__ int ctx_at(const DecodeArgs &a, const int *lds, int b
     return lds ? lds[b] : seq_ctx(a, b);
 }
 
+/* The inclusive prefix sum of v over the wave's 64 lanes. */
 __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(v, d, 64);
-        if (lane >= d) v += t;
-    }
+    (void)lane; /* DPP: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast15 / row_bcast31 across rows */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); /* row 0's total into row 1, row 2's into 3 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); /* rows 0-1's total into rows 2 and 3 */
     return v;
 }
 
@@ -684,7 +687,7 @@ __device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
                 reinterpret_cast<u32x4 *>(a.out + (size_t)b * a.hq * NC_HEAD_DIM)[r] = z;
         }
-        total += __shfl(wave_inclusive_sum(pg, lane), 63, 64);
+        total += __builtin_amdgcn_readlane(wave_inclusive_sum(pg, lane), 63);
     }
     return total * a.hkv;
 }
@@ -702,10 +705,10 @@ __device__ __forceinline__ void find_segment(const DecodeArgs &a, const int *lds
         if (hit) {
             const int first = __builtin_ctzll(hit);
             b = base + first;
-            units_b = __shfl(pg, first, 64);
-            carry += __shfl(incl - pg, first, 64) * a.hkv;
+            units_b = __builtin_amdgcn_readlane(pg, first);
+            carry += __builtin_amdgcn_readlane(incl - pg, first) * a.hkv;
         } else {
-            carry += __shfl(incl, 63, 64) * a.hkv;
+            carry += __builtin_amdgcn_readlane(incl, 63) * a.hkv;
         }
     }
     const int into = u - carry; /* offset inside sequence b */

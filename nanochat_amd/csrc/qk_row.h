@@ -28,9 +28,9 @@ __device__ __forceinline__ float row_rstd(const float *x1, const float *x2) {
     s[0] = s[0] + s[2];
     s[1] = s[1] + s[3];
     float t = s[0] + s[1];
-    t = t + shfl_xor_f(t, 4);
-    t = t + shfl_xor_f(t, 2);
-    t = t + shfl_xor_f(t, 1);
+    t = t + xor8_f<4>(t);
+    t = t + xor8_f<2>(t);
+    t = t + xor8_f<1>(t);
     return 1.0f / sqrtf(t / 128.0f + 1.1920928955078125e-07f);
 }
 
@@ -59,9 +59,9 @@ __device__ __forceinline__ float row_quantize_exact(const float *x1, const float
     float a = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) a = fmaxf(a, fmaxf(fabsf(x1[e]), fabsf(x2[e])));
-    a = fmaxf(a, shfl_xor_f(a, 4));
-    a = fmaxf(a, shfl_xor_f(a, 2));
-    a = fmaxf(a, shfl_xor_f(a, 1));
+    a = fmaxf(a, xor8_f<4>(a));
+    a = fmaxf(a, xor8_f<2>(a));
+    a = fmaxf(a, xor8_f<1>(a));
     const float scale = a / NC_FP8_MAX;
     uint64_t w1 = 0, w2 = 0;
     if (scale != 0.0f) {
@@ -100,9 +100,9 @@ __device__ __forceinline__ float row_quantize(const float *x1, const float *x2, 
 #pragma unroll
     for (int e = 0; e < 8; e++)
         m = max(m, max(__float_as_uint(x1[e]) & 0x7fffffffu, __float_as_uint(x2[e]) & 0x7fffffffu));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 4, NC_WAVE));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 2, NC_WAVE));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 1, NC_WAVE));
+    m = max(m, xor8_u32<4>(m));
+    m = max(m, xor8_u32<2>(m));
+    m = max(m, xor8_u32<1>(m));
     const float scale = __uint_as_float(m) / NC_FP8_MAX; /* not used when m is not finite */
     if (m >= 0x7f800000u || scale < 0x1p-126f) return row_quantize_exact(x1, x2, c1, c2);
     const float r = 1.0f / scale;
