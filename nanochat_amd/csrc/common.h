@@ -49,11 +49,12 @@ int nc_fail(const char *fmt, ...);
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-/* fp32 -> bf16 bits, round to nearest even (NaN kept quiet). */
+/* fp32 -> bf16 bits, round to nearest even (NaN kept quiet). Both results are formed and one is selected, so the
+ * NaN test is a v_cndmask, not a divergent branch per element. */
 __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
     const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16, quiet = (u >> 16) | 0x40u;
+    return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
 }
 
 /* 8 bf16 (one 16-byte load) as fp32. */
