@@ -397,9 +397,17 @@ __device__ __forceinline__ void load_kvrows(const DecodeArgs &a, int b, int h, i
         kr.kg[i] = kg[2 * g + i];
         kr.kg[2 + i] = kg[16 + 2 * g + i];
     }
-    /* the new key's page: p < max_ctx keeps it in the table (contiguous: computed in build_kv) */
-    if constexpr (TABLE) kr.blk = a.block_table[(size_t)b * a.max_blocks + p / NC_PAGE];
-    else kr.blk = 0;
+    /* the new key's page: p < max_ctx keeps it in the table (contiguous: computed in build_kv). The index gets a
+     * zero the compiler cannot see through, so the entry stays a per-lane value: read as a uniform one it would
+     * be moved to a scalar register here, and the wait for it would hold the first page loads behind every row
+     * load (1 us per fused piece); only build_kv, after the first page, reads it. */
+    if constexpr (TABLE) {
+        int opaque_zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(opaque_zero));
+        kr.blk = a.block_table[(size_t)b * a.max_blocks + p / NC_PAGE + opaque_zero];
+    } else {
+        kr.blk = 0;
+    }
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const u32x4 u, float *v) {
