@@ -159,8 +159,10 @@ int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride, const int3
  * position pos[r] of sequence seq[r] attends keys [max(pos - window, 0), pos] of that sequence in the cache
  * (window < 0: all), query head h reading kv head h / (Hq / Hkv), scores times sm_scale, fp32 softmax, bf16 out
  * [n][Hq][128]. The rows' own keys must be in the cache already (append the whole chunk first), so each row sees
- * the chunk's earlier rows causally. Rows with pos < 0 or seq outside [0, num_seqs) get zero rows; keys of a
- * missing block are skipped. Rows may come in any order; a sequence's rows being consecutive is fastest.
+ * the chunk's earlier rows causally. Rows with pos < 0 or seq outside [0, num_seqs) get zero rows; a row's G
+ * heads of one kv head whose q holds an infinity or a NaN (nc_kv_append_fp8's q rows past the rotary table) get
+ * NaN rows, as the fused decode step does there, and change no other row. Keys of a missing block are skipped.
+ * Rows may come in any order; a sequence's rows being consecutive is fastest.
  * Hq / Hkv <= 16.
  * Replaces: dec_prefill, model/kernels/decode.cu:1039-1051, whose rows each run k_attn (decode.cu:567-675). */
 int nc_prefill_attn_fp8(const void *q, const int32_t *pos, const int32_t *seq, int n, const uint8_t *cache,

@@ -116,7 +116,8 @@ def decode_step(qkv: Tensor, cache: Fp8KVCache, pos: Tensor, q_gain: Tensor, k_g
 def prefill_attention(q: Tensor, cache: Fp8KVCache, pos: Tensor, seq: Tensor, *, window: int = -1,
                       sm_scale: float | None = None, out: Tensor | None = None) -> Tensor:
     """q bf16 [n][Hq][128] (Fp8KVCache.append's q_out for the chunk); pos, seq int32 [n] on the GPU. The chunk's
-    keys must already be in the cache. Rows with pos < 0 or seq outside the cache's sequences get zero rows.
+    keys must already be in the cache. Rows with pos < 0 or seq outside the cache's sequences get zero rows; the
+    heads of one kv head of a row whose q is not finite (the append's rows past the rotary table) get NaN rows.
     Fastest when each sequence's rows are consecutive. Returns bf16 [n][Hq][128]."""
     _require(q, "q", torch.bfloat16, 3)
     n, hq, D = q.shape

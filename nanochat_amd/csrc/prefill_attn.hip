@@ -277,16 +277,29 @@ typedef short pf_i16x2 __attribute__((ext_vector_type(2)));
 
 /* 32 bf16 of q (this lane's dims 32j .. 32j+31 of its column) -> the two e4m3 terms (exact for a bf16 value whose low
  * term stays in e4m3's normal range: 4 + 4 significant bits); the column's exponent from its absmax over the four
- * lanes holding it (xor 16, 32). A zero column gives zero terms. */
-__device__ PfQ8 quantize_q(const u32x4 (&u)[4]) {
+ * lanes holding it (xor 16, 32). A zero column gives zero terms. A column holding an infinity or a NaN (the append's
+ * q rows past the rotary table) sets `bad` on its four lanes and gives zero terms: no NaN enters the MFMAs of a
+ * kernel compiled without NaN semantics. The test is on the bf16 bits (exponent all ones), which that compilation
+ * cannot fold away. */
+__device__ PfQ8 quantize_q(const u32x4 (&u)[4], bool &bad) {
 #pragma clang fp contract(off)
+    uint32_t nonfinite = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            nonfinite |= ((u[c][i] & 0x7f80u) == 0x7f80u) | ((u[c][i] & 0x7f800000u) == 0x7f800000u);
+    nonfinite |= (uint32_t)__shfl_xor((int)nonfinite, 16, 64);
+    nonfinite |= (uint32_t)__shfl_xor((int)nonfinite, 32, 64);
+    bad = nonfinite != 0;
+    const uint32_t keep = bad ? 0u : 0xffffffffu;
     float x[32];
 #pragma unroll
     for (int c = 0; c < 4; c++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            x[8 * c + 2 * i] = __uint_as_float(u[c][i] << 16);
-            x[8 * c + 2 * i + 1] = __uint_as_float(u[c][i] & 0xffff0000u);
+            x[8 * c + 2 * i] = __uint_as_float((u[c][i] << 16) & keep);
+            x[8 * c + 2 * i + 1] = __uint_as_float(u[c][i] & 0xffff0000u & keep);
         }
     float amax = 0.f;
 #pragma unroll
@@ -362,12 +375,12 @@ __device__ __forceinline__ void pair_softmax(const PrefillArgs &a, const f32x4 (
     unsigned ok[PF_BLOCKS];
     float vm[PF_BLOCKS]; /* the largest v_scale among the keys each column keeps (this lane's 8) */
     {
-        const float v = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])),
-                              fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
+        const float vmax = fmaxf(fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])),
+                                 fmaxf(fmaxf(vs[4], vs[5]), fmaxf(vs[6], vs[7])));
 #pragma unroll
         for (int bl = 0; bl < PF_BLOCKS; bl++) {
             ok[bl] = 0xffu;
-            vm[bl] = v; /* a pair on the fast path: every column keeps every key */
+            vm[bl] = vmax; /* a pair on the fast path: every column keeps every key */
         }
     }
     if (!fast) {
@@ -481,6 +494,9 @@ __device__ __forceinline__ bool row_valid(const PrefillArgs &a, int p, int s) {
     return p >= 0 && s >= 0 && s < a.num_seqs;
 }
 
+/* Bit k of bits: tile row k's q holds an infinity or a NaN. */
+__device__ __forceinline__ bool row_bad(const unsigned *bits, int k) { return (bits[k >> 5] >> (k & 31)) & 1u; }
+
 /* The first key of a row at position p. */
 __device__ __forceinline__ int key_lo(const PrefillArgs &a, int p) {
     return (a.window < 0 || p <= a.window) ? 0 : p - a.window;
@@ -492,6 +508,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
     __shared__ __attribute__((aligned(16))) unsigned char ring[PF_RING * PF_PAIR_BYTES];
     __shared__ __attribute__((aligned(16))) int ids[PF_IDS];
     __shared__ int2 rows_ps[PF_WAVES * PF_BLOCKS * 16]; /* the tile's (position, sequence) pairs */
+    __shared__ unsigned rows_bad[PF_WAVES * PF_BLOCKS * 16 / 32]; /* rows whose q is not finite */
 
     /* XCD-aware unit order: workgroup b runs on XCD b % 8, which takes a contiguous range of units, so the row
      * tiles of one (sequence, kv head) -- the readers of the same pages -- share an L2. Within the range, every
@@ -512,6 +529,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
 
     /* this lane's q operands: column n of block bl is row row0 + (wv PF_BLOCKS + bl) R + n / G, head h G + n % G */
     PfQ8 q8[PF_BLOCKS];
+    unsigned qbad = 0; /* bit bl: this lane's column of block bl is a used row whose q is not finite */
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
@@ -521,7 +539,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
             u[kk] = used ? *reinterpret_cast<const u32x4 *>(qr + 8 * kk) : u32x4{0u, 0u, 0u, 0u};
-        q8[bl] = quantize_q(u);
+        bool bad;
+        q8[bl] = quantize_q(u, bad);
+        qbad |= (used && bad) ? 1u << bl : 0u;
     }
 
     PfState st;
@@ -547,6 +567,14 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         const int r = row0 + k;
         rows_ps[k] = r < a.n ? make_int2(pos[r], seq[r]) : make_int2(-1, -1);
     }
+    if (tid < PF_WAVES * PF_BLOCKS * 16 / 32) rows_bad[tid] = 0u; /* every word: TR need not be a multiple of 32 */
+    __syncthreads();
+    /* rows whose q is not finite: attended by no segment (like invalid rows), NaN rows at the end */
+#pragma unroll
+    for (int bl = 0; bl < PF_BLOCKS; bl++) {
+        const int k = (wv * PF_BLOCKS + bl) * R + n / G;
+        if ((qbad >> bl) & 1u && j == 0) atomicOr(&rows_bad[k >> 5], 1u << (k & 31));
+    }
     __syncthreads();
 
     /* rows of the tile still to attend, 4 per lane (row0 + lane + 64 i); every wave derives the same segments */
@@ -554,7 +582,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int k = lane + 64 * i;
-        if (k < TR && row_valid(a, rows_ps[k].x, rows_ps[k].y)) pend |= 1u << i;
+        if (k < TR && row_valid(a, rows_ps[k].x, rows_ps[k].y) && !row_bad(rows_bad, k)) pend |= 1u << i;
     }
 
     for (;;) {
@@ -593,7 +621,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
             const bool used = n < R * G && r < a.n;
             const int2 ps = used ? rows_ps[r - row0] : make_int2(-1, -1);
             const int p = ps.x, sq = ps.y;
-            const bool ok = used && row_valid(a, p, sq), in_seg = ok && sq == s;
+            const bool ok = used && row_valid(a, p, sq) && !row_bad(rows_bad, r - row0), in_seg = ok && sq == s;
             other |= ok && !in_seg;
             mine |= in_seg;
             c.lo[bl] = in_seg ? key_lo(a, p) : (ok ? PF_NO_KEY : 0);
@@ -706,7 +734,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         }
     }
 
-    /* normalise and store; rows with an invalid position or sequence get zeros */
+    /* normalise and store; rows with an invalid position or sequence get zeros, other rows whose q (the G heads of
+     * this kv head) is not finite NaN (as the decode step's rows past the rotary table) */
 #pragma unroll
     for (int bl = 0; bl < PF_BLOCKS; bl++) {
         float l = st.l[bl];
@@ -715,7 +744,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
         const int r = row0 + (wv * PF_BLOCKS + bl) * R + n / G;
         if (!(n < R * G && r < a.n)) continue;
         const int2 ps = rows_ps[r - row0];
-        const bool zero = !(row_valid(a, ps.x, ps.y) && l > 0.f); /* +0, not o * 0 (which keeps signs) */
+        const bool valid = row_valid(a, ps.x, ps.y), nan_row = valid && row_bad(rows_bad, r - row0);
+        const bool zero = !(valid && l > 0.f); /* +0, not o * 0 (which keeps signs) */
         const float inv = zero ? 0.f : 1.0f / l; /* o and l both carry w */
         bf16_t *dst = a.out + ((size_t)r * a.hq + h * G + n % G) * NC_HEAD_DIM;
 #pragma unroll
@@ -723,7 +753,11 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
             float v[8];
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) v[bb] = zero ? 0.f : st.o[bl][bb][i] * inv;
-            store_bf16x8(dst + (4 * j + i) * 8, v);
+            u32x4 bits;
+#pragma unroll
+            for (int c = 0; c < 4; c++) bits[c] = f32_to_bf16(v[2 * c]) | (f32_to_bf16(v[2 * c + 1]) << 16);
+            if (nan_row) bits = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+            *reinterpret_cast<u32x4 *>(dst + (4 * j + i) * 8) = bits;
         }
     }
 }

@@ -103,6 +103,52 @@ def test_rows_in_any_order_and_invalid_rows(gpu):
     assert_attention_close(out, want, "shuffled")
 
 
+def test_rows_whose_q_is_not_finite(gpu):
+    """Rows past the rotary table get NaN q rows from the append (and write no cache byte); the prefill gives them
+    NaN rows, as the decode step does for the same positions, and every other row keeps the bits it has without
+    them and the oracle's result. A NaN or an infinity in one head of an otherwise valid row makes the G heads that
+    share its kv head NaN; the row's other heads keep their bits. Rows with pos < 0 stay zero whatever their q."""
+    dev = gpu
+    cfg = PrefillConfig("nonfinite", 2, 8, 2, cached=(120, 300), chunk=(40, 33), paged=True, seed=71)
+    case = build_prefill_case(cfg, dev)
+    G_ = cfg.hq // cfg.hkv
+    rope_len = case.cos.shape[0]
+    pos = case.pos.clone()
+    past = [3, 17, 50]
+    pos[past] = rope_len + torch.tensor([0, 5, 1000], dtype=torch.int32, device=dev)
+    before = oracle_cache(case.cache)
+    q = case.cache.append(case.qkv, pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    torch.cuda.synchronize()
+    assert (bits(q[past]) == 0x7fc0).all()
+    keep = [i for i in range(q.shape[0]) if i not in past]
+    # the append skipped the rows past the table: the cache equals one written without them
+    G.append(before, bits(case.qkv[keep]), case.pos[keep].cpu().numpy(), case.seq[keep].cpu().numpy(),
+             case.q_gain.cpu().numpy(), case.k_gain.cpu().numpy(), case.cos.cpu().numpy(), case.sin.cpu().numpy(),
+             cfg.hq, cfg.hkv, table(case.cache), case.cache.max_blocks)
+    assert_same_cache(case.cache, before)
+    q_bad = q.clone()
+    q_bad[8, 3, 77] = float("nan")   # kv head 0's group of row 8
+    q_bad[9, G_, 0] = float("inf")   # kv head 1's group of row 9
+    pos_bad = pos.clone()
+    pos_bad[12] = -1
+    q_bad[12, 1, 5] = float("nan")   # pos < 0: zero row whatever its q
+    out = prefill_attention(q_bad, case.cache, pos_bad, case.seq)
+    clean = prefill_attention(q[[8, 9]].contiguous(), case.cache, pos[[8, 9]].contiguous(),
+                              case.seq[[8, 9]].contiguous())
+    torch.cuda.synchronize()
+    assert (bits(out[past]) == 0x7fc0).all()
+    assert (bits(out[8, :G_]) == 0x7fc0).all() and (bits(out[9, G_:]) == 0x7fc0).all()
+    assert np.array_equal(bits(out[8, G_:]), bits(clean[0, G_:])) and np.array_equal(bits(out[9, :G_]),
+                                                                                      bits(clean[1, :G_]))
+    assert not bits(out[12]).any()
+    rest = torch.tensor([i for i in range(q.shape[0]) if i not in past + [8, 9, 12]], device=dev)
+    alone = prefill_attention(q[rest].contiguous(), case.cache, pos[rest].contiguous(), case.seq[rest].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(out[rest].view(torch.int16), alone.view(torch.int16))
+    want = oracle_rows(case, q[rest].contiguous(), pos[rest].contiguous(), case.seq[rest].contiguous(), -1)
+    assert_attention_close(out[rest], want, "nonfinite neighbours")
+
+
 def test_missing_blocks_are_skipped(gpu):
     dev = gpu
     cfg = PrefillConfig("holes", 2, 4, 2, cached=(300, 300), chunk=(40, 40), paged=True, seed=61)
