@@ -62,15 +62,17 @@
 #define DEC_MIN_CHUNK 8     /* pages per wave at least: fewer pieces to merge on small problems */
 #define DEC_LAZY 8.0f       /* log2 headroom before the softmax reference moves */
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
-#ifndef DEC_DEPTH
 #define DEC_DEPTH 4         /* page buffers per wave: 3 pages (12.4 KiB) in flight while one is computed */
-#endif
+/* Only DEC_DEPTH 4 is supported: builds with 5 and 6 buffers (which fit in registers at one wave per SIMD) took
+ * a GPU memory fault in their first timing run, with no cause found in the code; they stay disabled. */
+static_assert(DEC_DEPTH == 4, "the page ring is 4 buffers deep");
+
 /* Schedule units (page equivalents, measured on config 3 by sweeping these values) of a piece start (the
  * segment's context length and block ids: two dependent round trips) and of a segment's end (the fused step's q
  * rows and the append's quantisation; the same in both entry points, so that they split the work alike and give
  * bit-identical outputs). */
 #ifndef DEC_UNITS_START
-#define DEC_UNITS_START 4
+#define DEC_UNITS_START 3
 #endif
 #ifndef DEC_UNITS_END
 #define DEC_UNITS_END 10
