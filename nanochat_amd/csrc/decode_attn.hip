@@ -114,14 +114,17 @@ struct SeqRange {
     int first, last, begin, p;
 };
 
-/* The context length of sequence b: ctx_len[b] clamped to [0, max_ctx]. The fused step reads a position p and
- * gives p + 1, 0 for p < 0, and -1 (no append, a NaN output row) for p at or past max_ctx or rope_len. */
-__device__ __forceinline__ int seq_ctx(const DecodeArgs &a, int b) {
-    const int v = a.ctx_len[b];
+/* The context length of a sequence whose ctx_len entry is v: v clamped to [0, max_ctx]. The fused step's entry is
+ * a position p, giving p + 1, 0 for p < 0, and -1 (no append, a NaN output row) for p at or past max_ctx or
+ * rope_len. */
+__device__ __forceinline__ int seq_ctx_of(const DecodeArgs &a, int v) {
     if (!a.qkv) return max(min(v, a.max_ctx), 0);
     if (v < 0) return 0;
     return (v >= a.max_ctx || v >= a.rope_len) ? -1 : v + 1;
 }
+
+/* seq_ctx_of sequence b's entry. */
+__device__ __forceinline__ int seq_ctx(const DecodeArgs &a, int b) { return seq_ctx_of(a, a.ctx_len[b]); }
 
 /* The key range of a sequence of context length ctx (seq_ctx). */
 __device__ __forceinline__ SeqRange seq_range_of(const DecodeArgs &a, int ctx) {
@@ -681,15 +684,20 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
 
 /* Schedule units of the whole batch: every wave derives the same value from the live context lengths and keeps
  * them in lds (if not null); wave b % W writes sequence b's row if it is empty (zeros, or NaN for the fused step's
- * positions out of range) and its next position to pos_out. 32-bit: the host bounds the total. */
-__device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *lds) {
+ * positions out of range) and its next position to pos_out: sequence w's (own_pos, in lane w % 64) after its pages
+ * (put_own_pos), any later ones (a batch larger than the grid) here. 32-bit: the host bounds the total. */
+__device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *lds, int &own_pos) {
     int total = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int b = base + lane;
-        const int c = b < a.B ? seq_ctx(a, b) : 0;
+        const int raw = b < a.B ? a.ctx_len[b] : 0;
+        const int c = b < a.B ? seq_ctx_of(a, raw) : 0;
         const int pg = units_of(a, c);
         if (lds && b < a.B) lds[b] = c;
-        if (a.pos_out && b < a.B && b % W == w) a.pos_out[b] = a.ctx_len[b] + 1;
+        if (a.pos_out && b < a.B && b % W == w) {
+            if (b == w) own_pos = raw + 1;
+            else a.pos_out[b] = raw + 1;
+        }
         if (b < a.B && pg == 0 && b % W == w) {
             for (int hh = 0; hh < a.hkv; hh++) a.ws_desc[b * a.hkv + hh] = make_int2(0, 0); /* nothing to merge */
             const uint32_t f = c < 0 ? 0x7fc07fc0u : 0u;
@@ -700,6 +708,12 @@ __device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *
         total += __builtin_amdgcn_readlane(wave_inclusive_sum(pg, lane), 63);
     }
     return total * a.hkv;
+}
+
+/* The fused step's next position of sequence w, held since schedule_total: stored after the wave's pages, so that
+ * the store's acknowledgement holds up none of their waits (the memory counter completes in order). */
+__device__ __forceinline__ void put_own_pos(const DecodeArgs &a, int w, int lane, int own_pos) {
+    if (a.pos_out && w < a.B && lane == (w & 63)) a.pos_out[w] = own_pos;
 }
 
 /* The segment holding unit u of the flattened list: sequence b, kv head h and the segment's first unit. */
@@ -747,16 +761,23 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
 
     if (lane == 0) sm.nparts = 0;
-    const int total = schedule_total(a, w, W, lane, lds);
+    int own_pos = 0;
+    const int total = schedule_total(a, w, W, lane, lds, own_pos);
     __syncthreads(); /* lds complete before other lanes' reads */
     const int chunk = max((total + W - 1) / W, DEC_MIN_CHUNK);
     int start = w * chunk;
-    if (start >= total) return;
+    if (start >= total) {
+        put_own_pos(a, w, lane, own_pos);
+        return;
+    }
     int end = min(start + chunk, total);
     if (a.piece_pages > 0) { /* whole fixed pieces: both ends at the nearest piece boundary */
         start = snap_unit(a, lds, start, lane);
         end = end >= total ? total : snap_unit(a, lds, end, lane);
-        if (start >= end) return;
+        if (start >= end) {
+            put_own_pos(a, w, lane, own_pos);
+            return;
+        }
     }
     int remaining = end - start;
 
@@ -813,6 +834,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
         }
     }
     flush_parts(a, lane, sm); /* after the last pages: these stores hold up no wait */
+    put_own_pos(a, w, lane, own_pos);
 }
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
