@@ -48,6 +48,7 @@
  *
  * Roofline: HBM. Per (token, kv head) the kernel reads 128 B of K, 128 B of V and two fp32 scales: 264 B.
  */
+#include <algorithm>
 #include <mutex>
 
 #include "layout.h"
@@ -839,14 +840,15 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
  * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale. A thread holds head n, dims 8 c..8 c + 8 (16
- * lanes per head) of one of Q = 256 / (16 G) groups. Group q folds, in order, pieces 8 q..8 q + 7, then
+ * lanes per head) of one of Q = min(4, 256 / (16 G)) groups. Group q folds, in order, pieces 8 q..8 q + 7, then
  * 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a given
  * piece count and head group, so the bits depend on nothing else. The kernel is latency-bound: the first round's
  * slots do not depend on the segment's descriptor (fixed pieces: s * DEC_PIECES_MAX + i; the balanced split's first
  * DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, one round trip for up to 8 Q fixed
  * pieces (8 for the balanced split, every segment of config 3). */
 #define MERGE_LANES 16
-#define MERGE_THREADS 256
+#define MERGE_THREADS 256 /* at most: Q = min(4, 16 / G) groups of 16 G lanes (64 threads at G = 1) */
+#define MERGE_GROUPS 4
 
 struct MergeAcc {
     float m, l, o[8];
@@ -890,7 +892,7 @@ __device__ __forceinline__ void merge_round(const DecodeArgs &a, int s, int2 d, 
 __global__ void __launch_bounds__(MERGE_THREADS) k_merge(DecodeArgs a) {
     __shared__ MergeAcc grp[MERGE_THREADS];
     const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, G = a.group;
-    const int row = G * MERGE_LANES, Q = MERGE_THREADS / row, q = t / row, n = (t % row) / MERGE_LANES,
+    const int row = G * MERGE_LANES, Q = (int)blockDim.x / row, q = t / row, n = (t % row) / MERGE_LANES,
               c = t % MERGE_LANES;
     const int2 d = a.ws_desc[s];
     /* the first round's slots, loaded with the descriptor: slot(i) needs no d where spec holds */
@@ -1028,7 +1030,11 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else if (a.block_table) hipLaunchKernelGGL((k_decode<false, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3(MERGE_THREADS), 0, st, a);
+    /* the groups: as many as fit in MERGE_THREADS, at most MERGE_GROUPS (enough for DEC_PIECES_MAX pieces in one
+     * round trip at G <= 4); fewer waves per segment for the small head groups of many segments */
+    const int row = a.group * MERGE_LANES, groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3((unsigned)(groups * row + NC_WAVE - 1) / NC_WAVE * NC_WAVE), 0,
+                       st, a);
     NC_LAUNCH_CHECK();
     return 0;
 }
