@@ -67,8 +67,8 @@ def parse():
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="no measurement: summarise rocprofv3 --pmc output directories (counter_collection.csv) "
                          "per kernel of --kernels, as JSON")
-    ap.add_argument("--kernels", default="k_decode<true>,k_merge",
-                    help="--pmc-summary: the kernels (short names) whose last --last dispatches are averaged")
+    ap.add_argument("--kernels", default="k_decode<true, true>;k_merge",
+                    help="--pmc-summary: the kernels (short names, separated by ;) whose last --last dispatches are averaged")
     ap.add_argument("--last", type=int, default=20, help="--pmc-summary: dispatches per kernel averaged")
     ap.add_argument("--stats-summary", metavar="DIR",
                     help="no measurement: print the kernel table of a rocprofv3 --kernel-trace --stats directory")
@@ -89,8 +89,8 @@ def replay_ms(graph, n: int, stream) -> float:
     return start.elapsed_time(end) / n
 
 
-CALL_KERNELS = {"nc_decode_step_fp8": ("k_decode<true>", "k_merge"),
-                "nc_decode_attn_fp8": ("k_decode<false>", "k_merge")}
+CALL_KERNELS = {"nc_decode_step_fp8": ("k_decode<true, true>", "k_merge"),  # config 3: paged (block table)
+                "nc_decode_attn_fp8": ("k_decode<false, true>", "k_merge")}
 
 
 def traffic_bytes(call: str):
@@ -656,7 +656,7 @@ def main():
         print(stats_summary(args.stats_summary))
         return
     if args.pmc_summary:
-        print(json.dumps({"dirs": args.pmc_summary, "summary": pmc_summary(args.pmc_summary, args.kernels.split(","),
+        print(json.dumps({"dirs": args.pmc_summary, "summary": pmc_summary(args.pmc_summary, args.kernels.split(";"),
                                                                             args.last)}, indent=1))
         return
     if args.gpus != 1:
