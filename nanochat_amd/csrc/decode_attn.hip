@@ -1107,13 +1107,13 @@ extern "C" int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, 
 
 /* ------------------------------------------------------------------------------------------------------------
  * The fused step without a workspace argument, for callers that cannot allocate (code under graph capture, tight
- * serving loops): the partial results and the segments' counters live in `scratch`, a static device array of
- * NC_DECODE_SCRATCH_BYTES that every device running this library holds until the process ends. Its device address
- * is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernel like the
- * workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. The array starts at
- * zero (a static device array is zero-initialised when the code object loads) and every call leaves the counters
- * at zero, as a caller's workspace must be. Calls share their device's array, so two calls that may overlap on one
- * device (two streams) race; calls in one stream do not. */
+ * serving loops): the partial results and the segments' piece descriptors live in `scratch`, a static device array
+ * of NC_DECODE_SCRATCH_BYTES that every device running this library holds until the process ends. Its device
+ * address is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernel like
+ * the workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. No value needs
+ * to start at zero: k_decode writes every segment's descriptor and every piece's partial before k_merge reads them,
+ * so what earlier calls left there does not matter. Calls share their device's array, so two calls that may
+ * overlap on one device (two streams) race; calls in one stream do not. */
 #define NC_DECODE_SCRATCH_BYTES (64ll << 20)
 #define NC_MAX_DEVICES 64
 
