@@ -108,6 +108,7 @@ struct DecodeArgs {
     int max_ctx;              /* ctx_len is clamped to it */
     int unit_start, unit_end; /* schedule units a non-empty segment costs before its first and after its last page */
     int piece_pages;          /* 0: pieces cut by the balanced split; > 0: fixed pieces (piece_len) */
+    int merge_groups;         /* k_merge's groups of 16 G lanes per segment */
 };
 
 /* The key range of sequence b: pages [first, last] (none if last < first), keys [begin, p]. */
@@ -840,12 +841,14 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
  * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale. A thread holds head n, dims 8 c..8 c + 8 (16
- * lanes per head) of one of Q = min(4, 256 / (16 G)) groups. Group q folds, in order, pieces 8 q..8 q + 7, then
- * 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a given
- * piece count and head group, so the bits depend on nothing else. The kernel is latency-bound: the first round's
- * slots do not depend on the segment's descriptor (fixed pieces: s * DEC_PIECES_MAX + i; the balanced split's first
- * DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, one round trip for up to 8 Q fixed
- * pieces (8 for the balanced split, every segment of config 3). */
+ * lanes per head) of one of Q = merge_groups groups (at most min(4, 256 / (16 G))). Group q folds, in order, pieces
+ * 8 q..8 q + 7, then 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed
+ * order for a given piece count and head group, so the bits depend on nothing else (with fixed pieces Q only drops
+ * groups that no segment reaches at max_ctx, which leaves the order as it is). The kernel is latency-bound: the
+ * first round's slots do not depend on the segment's descriptor (fixed pieces: s * DEC_PIECES_MAX + i; the balanced
+ * split's first DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, unconditionally (a
+ * predicate per slot puts each load behind a branch and a wait), one round trip for up to 8 Q fixed pieces (8 for
+ * the balanced split, every segment of config 3). */
 #define MERGE_LANES 16
 #define MERGE_THREADS 256 /* at most: Q = min(4, 16 / G) groups of 16 G lanes (64 threads at G = 1) */
 #define MERGE_GROUPS 4
@@ -892,7 +895,7 @@ __device__ __forceinline__ void merge_round(const DecodeArgs &a, int s, int2 d, 
 __global__ void __launch_bounds__(MERGE_THREADS) k_merge(DecodeArgs a) {
     __shared__ MergeAcc grp[MERGE_THREADS];
     const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, G = a.group;
-    const int row = G * MERGE_LANES, Q = (int)blockDim.x / row, q = t / row, n = (t % row) / MERGE_LANES,
+    const int row = G * MERGE_LANES, Q = a.merge_groups, q = t / row, n = (t % row) / MERGE_LANES,
               c = t % MERGE_LANES;
     const int2 d = a.ws_desc[s];
     /* the first round's slots, loaded with the descriptor: slot(i) needs no d where spec holds */
@@ -1031,8 +1034,17 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
     /* the groups: as many as fit in MERGE_THREADS, at most MERGE_GROUPS (enough for DEC_PIECES_MAX pieces in one
-     * round trip at G <= 4); fewer waves per segment for the small head groups of many segments */
-    const int row = a.group * MERGE_LANES, groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
+     * round trip at G <= 4); fewer waves per segment for the small head groups of many segments. Fixed pieces: no
+     * more groups than the pieces of the longest segment at max_ctx need (ceil(max_ctx / 16) pages at most) */
+    const int row = a.group * MERGE_LANES;
+    int groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
+    if (a.piece_pages > 0) {
+        const long long pages = ((long long)max_ctx + NC_PAGE - 1) / NC_PAGE;
+        const int most = pages <= (long long)DEC_PIECES_MAX * a.piece_pages
+                             ? (int)((pages + a.piece_pages - 1) / a.piece_pages) : DEC_PIECES_MAX;
+        groups = std::min(groups, (most + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT);
+    }
+    a.merge_groups = groups;
     hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3((unsigned)(groups * row + NC_WAVE - 1) / NC_WAVE * NC_WAVE), 0,
                        st, a);
     NC_LAUNCH_CHECK();
