@@ -64,8 +64,8 @@
 #define DEC_LAZY 8.0f       /* log2 headroom before the softmax reference moves */
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
 #define DEC_DEPTH 4         /* page buffers per wave: 3 pages (12.4 KiB) in flight while one is computed */
-/* Only DEC_DEPTH 4 is supported: builds with 5 and 6 buffers (which fit in registers at one wave per SIMD) took
- * a GPU memory fault in their first timing run, with no cause found in the code; they stay disabled. */
+/* DEC_DEPTH 4 is the depth built and tested. The ring's rotation and clamped loads work for any depth, and 5 or 6
+ * buffers fit in registers at one wave per SIMD, but the page stream already runs at the in-order ceiling with 4. */
 static_assert(DEC_DEPTH == 4, "the page ring is 4 buffers deep");
 
 /* Schedule units (page equivalents, measured on config 3 by sweeping these values) of a piece start (the
