@@ -93,6 +93,33 @@ def test_pieces_step_is_correct_at_every_piece_length(gpu):
         assert_attention_close(got, want, f"piece_pages {piece_pages}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (16, 4), (16, 2)], ids=["g1", "g4", "g8"])
+def test_pieces_step_bits_do_not_depend_on_max_ctx(gpu, hq, hkv):
+    """k_merge launches only the lane groups that the longest segment allowed by max_ctx can fill (1 to 4 groups of
+    8 pieces). Sequences at the group boundaries (8, 9, 16, 17 and 31 pieces of 16 or 17 pages after the append)
+    keep their bits whatever max_ctx the call names, as long as it admits them."""
+    print(f"piece plan, max_ctx groups: hq {hq} hkv {hkv}", flush=True)
+    cfg = DecodeConfig(f"pieces-max-ctx-{hq}-{hkv}", 7, hq, hkv, ctx=(0, 99, 2047, 2048, 4095, 4096, 8400),
+                       paged=True, seed=306)
+    case = build_decode_case(cfg, gpu, steps=1)
+    pos = case.positions(0)
+    ctx_after = case.ctx + 1
+    full = bits(_step(case, pos, case.cache.capacity))
+    torch.cuda.synchronize()
+    ref = oracle_cache(case.cache)
+    q = case.cache.append(case.qkv[0], pos, case.seq, case.q_gain, case.k_gain, case.cos, case.sin, cfg.hq)
+    want = G.decode_attention(bits(q), ref, table(case.cache), case.cache.max_blocks, ctx_after, cfg.window, cfg.hq,
+                              cfg.hkv, SCALE)
+    assert_attention_close(torch.from_numpy(full.view(np.int16)).view(torch.bfloat16), want, cfg.name)
+    for max_ctx in (4097, 4096, 2048, 100):  # 17, 16, 8 and 1 pieces at most: 3, 2, 1 and 1 groups
+        active = np.flatnonzero(ctx_after <= max_ctx)
+        p = torch.full_like(pos, -1)
+        p[active] = pos[active]
+        got = bits(_step(case, p, max_ctx))  # rewrites the same appended bytes
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got[active], full[active], err_msg=f"max_ctx {max_ctx}")
+
+
 def _ragged_prompts(rng, n, vocab, lo, hi):
     return [rng.integers(0, vocab, int(rng.integers(lo, hi + 1))).astype(np.int32) for _ in range(n)]
 
