@@ -73,11 +73,11 @@ class CpuModel:
         """Rows (token, position, sequence): every row's key and value appended in each layer before any row
         attends its sequence's cached keys up to its position (a chunk of a prompt after its earlier chunks)."""
         tok, pos, seq = np.asarray(tok), np.asarray(pos), np.asarray(seq)
-        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
+        x, x0 = self._embed(tok)
         scale = 128 ** -0.5
         for l in range(self.cfg.layers):
             w = self.cfg.window(l)
-            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.rows_attention(
+            x = self._block(l, x, x0, pos, seq, tok, lambda q, c: G.rows_attention(
                 q, pos, seq, c, None, self.max_blocks, self.batch, w, self.cfg.heads, self.cfg.kv_heads, scale))
 
     def step(self, tok: np.ndarray, position) -> np.ndarray:
@@ -85,10 +85,65 @@ class CpuModel:
         fp32 logits [batch][vocab]."""
         B = self.batch
         pos, seq = np.broadcast_to(np.asarray(position), (B,)).copy(), np.arange(B)
-        x = x0 = cpu_norm(self.wte[torch.from_numpy(tok.astype(np.int64))])
+        x, x0 = self._embed(tok)
         scale = 128 ** -0.5
         for l in range(self.cfg.layers):
             w = self.cfg.window(l)
-            x = self._layer(l, self._mix(l, x, x0), pos, seq, tok, lambda q, c: G.decode_attention(
+            x = self._block(l, x, x0, pos, seq, tok, lambda q, c: G.decode_attention(
                 q, c, None, self.max_blocks, pos + 1, w, self.cfg.heads, self.cfg.kv_heads, scale))
         return (cpu_norm(x).float() @ self.lm_head.float().t()).numpy()
+
+    def _embed(self, tok):
+        """The residual stream and x0 of tokens tok: both the normed embedding, bf16 (modeling_nanochat.py:150-151)."""
+        x0 = cpu_norm(self.wte[torch.from_numpy(np.asarray(tok).astype(np.int64))])
+        return x0, x0
+
+    def _block(self, l, x, x0, pos, seq, tok, attend):
+        return self._layer(l, self._mix(l, x, x0), pos, seq, tok, attend)
+
+
+def _rstd(v: torch.Tensor) -> torch.Tensor:
+    """rsqrt(mean(v^2) + FLT_EPSILON) per row of an fp32 tensor, in fp32 (the sum in fp64, then rounded)."""
+    return torch.rsqrt((v.double().square().mean(-1) + EPS).float())
+
+
+class EngineCpuModel(CpuModel):
+    """CpuModel with the reference CUDA engine's roundings (model/kernels/decode.cu) instead of its torch path's:
+    x0 stays fp32 (k_norm EMBED, decode.cu:413-440: v r unrounded); each layer's mix is fma(l1, h, x0 l2) in fp32
+    with h = x0 at layer 0, rounded to bf16 for the residual, while the qkv input is bf16(v r) of the unrounded v
+    (RESID_NORM); the GEMMs sum in fp32 and round once in their epilogues (decode.cu:169-186); the o-projection's
+    fp32 sum (residual included, before rounding) gives the MLP's rstd (k_rstd, decode.cu:443-455) and RELU2 is
+    bf16(max(p, 0) p) with p = rstd s (decode.cu:173-176). The attention, the append and the head are CpuModel's.
+    Test infrastructure: it measures how often greedy tokens differ between the two roundings; no test pins it to
+    the CUDA engine's bits (parity unpinned: the engine needs CUDA)."""
+
+    def __init__(self, model, batch: int, max_len: int):
+        super().__init__(model, batch, max_len)
+        self.wf = [{k: lw[k].float() for k in ("wqkv", "wo", "wup", "wdown")} for lw in self.w]
+
+    def _embed(self, tok):
+        v = self.wte[torch.from_numpy(np.asarray(tok).astype(np.int64))].float()
+        return None, v * _rstd(v)[:, None]
+
+    def _block(self, l, x, x0, pos, seq, tok, attend):
+        lw, wf, cfg = self.w[l], self.wf[l], self.cfg
+        h = x0 if x is None else x.float()
+        a = (x0 * self.l0[l].float()).double()
+        v = (self.lr[l].double() * h.double() + a).float()  # one rounding: the fma
+        mixed = v.to(torch.bfloat16)
+        n = (v * _rstd(v)[:, None]).to(torch.bfloat16)
+        qkv = (n.float() @ wf["wqkv"].t()).to(torch.bfloat16)
+        if "ve" in lw:
+            H = cfg.kv_heads
+            gate = 2 * torch.sigmoid(F.linear(n.float(), lw["ve_gate"]))
+            vv = qkv[:, (cfg.heads + H) * 128:].reshape(-1, H, 128)
+            ve = lw["ve"][torch.from_numpy(np.asarray(tok, np.int64))].reshape(-1, H, 128)
+            qkv[:, (cfg.heads + H) * 128:] = (vv.float() + gate[..., None] * ve.float()).to(torch.bfloat16).flatten(1)
+        q = G.append(self.caches[l], bits(qkv), pos, seq, lw["q_gain"].numpy(), lw["k_gain"].numpy(), self.cos,
+                     self.sin, cfg.heads, cfg.kv_heads, None, self.max_blocks)
+        o = torch.from_numpy(attend(q, self.caches[l]).astype(np.float32)).to(torch.bfloat16)
+        xf = o.reshape(o.shape[0], -1).float() @ wf["wo"].t() + mixed.float()
+        xo = xf.to(torch.bfloat16)
+        p = (xo.float() @ wf["wup"].t()) * _rstd(xf)[:, None]
+        u = (p.clamp_min(0.0) * p).to(torch.bfloat16)
+        return (xo.float() + u.float() @ wf["wdown"].t()).to(torch.bfloat16)
