@@ -168,6 +168,43 @@ def test_config5_architecture_matches_cpu_model(gpu):
                       mean_tol=CFG5_LOGIT_MEAN, row_chunk=1024)
 
 
+def test_config5_full_batch_anchored_on_two_sequences(gpu):
+    """BASELINE config 5 at its own batch and prompt length (B 128, 2048-token prompts; the full architecture, random
+    init) for 3 greedy steps; sequences 0 and 127 checked against the CPU model run on those two prompts alone:
+    logits within CFG5_LOGIT_ATOL / CFG5_LOGIT_MEAN, greedy tokens equal wherever the CPU logits' top-two margin
+    exceeds twice the tolerance. The piece plan makes a sequence's bits independent of the other 126, so the CPU
+    model needs only the two."""
+    B, T, steps, pick = 128, 2048, 3, [0, 127]
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    model = RandomModel(CFG5_SHAPE, gpu, seed=5)
+    prompts = np.random.default_rng(18).integers(0, CFG5_SHAPE.vocab, (B, T)).astype(np.int32)
+    print("config 5 full batch: GPU prefill of 128 x 2048 tokens", flush=True)
+    dec = Fp8Decoder(model, B, T - 1 + steps, gpu)
+    dec.prefill(torch.from_numpy(prompts).to(gpu))
+    cpu = CpuModel(model, len(pick), T - 1 + steps)
+    sub = prompts[pick]
+    for r in range(0, T - 1, 512):  # the CPU prefill in 4 chunks of positions, each after the earlier ones
+        e = min(r + 512, T - 1)
+        print(f"CPU prefill of positions {r}..{e - 1} of sequences {pick}", flush=True)
+        cpu.prefill_rows(sub[:, r:e].reshape(-1), np.tile(np.arange(r, e), len(pick)),
+                         np.repeat(np.arange(len(pick)), e - r))
+    tok = prompts[:, -1].copy()
+    out = torch.empty(B, dtype=torch.int32, device=gpu)
+    for s in range(steps):
+        p = T - 1 + s
+        logits = dec._step(torch.from_numpy(tok).to(gpu), torch.full((B,), p, dtype=torch.int32, device=gpu), out)
+        want = cpu.step(tok[pick], p)
+        got = logits.cpu().numpy()[pick]
+        diff = np.abs(got - want)
+        print(f"step {s}: logit difference max {diff.max():.3e} mean {diff.mean():.3e}", flush=True)
+        assert diff.max() <= CFG5_LOGIT_ATOL and diff.mean() <= CFG5_LOGIT_MEAN, (s, diff.max(), diff.mean())
+        chosen = out.cpu().numpy()
+        top2 = np.sort(want, axis=1)[:, -2:]
+        sure = top2[:, 1] - top2[:, 0] > 2 * CFG5_LOGIT_ATOL
+        np.testing.assert_array_equal(chosen[pick][sure], want.argmax(1)[sure])
+        tok = chosen
+
+
 def test_prefill_in_chunks_leaves_the_same_bytes(gpu):
     """A prompt prefilled in two calls (positions 0..99, then 100..174) leaves the bytes of one call in every layer:
     each row attends its own key range with its own arithmetic (whatever rows share its workgroup), and a GEMM row's
