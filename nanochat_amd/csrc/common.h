@@ -49,13 +49,18 @@ int nc_fail(const char *fmt, ...);
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-/* fp32 -> bf16 bits, round to nearest even (NaN kept quiet). Both results are formed and one is selected, so the
- * NaN test is a v_cndmask, not a divergent branch per element. */
-__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
-    const uint32_t u = __float_as_uint(x);
-    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16, quiet = (u >> 16) | 0x40u;
-    return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
+/* fp32 -> bf16 by gfx950's v_cvt_pk_bf16_f32: round to nearest even, a NaN's upper 16 bits kept with the quiet bit
+ * set. On this GPU it equals the integer rule ((u + 0x7fff + bit 16 of u) >> 16; a NaN gives (u >> 16) | 0x40) for
+ * all 2^32 inputs, in both halves and with or without IEEE mode (tests/test_gpu_bf16_rounding.py). */
+typedef float nc_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 nc_bf16x2 __attribute__((ext_vector_type(2)));
+
+/* Two fp32 as packed bf16 bits: lo in bits 0-15, hi in bits 16-31 (one instruction). */
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(nc_f32x2{lo, hi}, nc_bf16x2));
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
 /* 8 bf16 (one 16-byte load) as fp32. */
 __device__ __forceinline__ void load_bf16x8(const bf16_t *p, float *v) {
@@ -71,7 +76,7 @@ __device__ __forceinline__ void load_bf16x8(const bf16_t *p, float *v) {
 __device__ __forceinline__ void store_bf16x8(bf16_t *p, const float *v) {
     u32x4 u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) u[i] = f32_to_bf16(v[2 * i]) | (f32_to_bf16(v[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; i++) u[i] = f32x2_to_bf16x2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<u32x4 *>(p) = u;
 }
 

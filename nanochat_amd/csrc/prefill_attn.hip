@@ -755,7 +755,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2)
             for (int bb = 0; bb < 8; bb++) v[bb] = zero ? 0.f : st.o[bl][bb][i] * inv;
             u32x4 bits;
 #pragma unroll
-            for (int c = 0; c < 4; c++) bits[c] = f32_to_bf16(v[2 * c]) | (f32_to_bf16(v[2 * c + 1]) << 16);
+            for (int c = 0; c < 4; c++) bits[c] = f32x2_to_bf16x2(v[2 * c], v[2 * c + 1]);
             if (nan_row) bits = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
             *reinterpret_cast<u32x4 *>(dst + (4 * j + i) * 8) = bits;
         }

@@ -319,8 +319,7 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
                         v[i] = EPI == SG_RELU2_NORM ? fmaxf(p, 0.f) * p : p;
                     }
                 }
-                const u32x2 o = {f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
-                                 f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
+                const u32x2 o = {f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
                 *reinterpret_cast<u32x2 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
             }
         }
@@ -617,7 +616,7 @@ __global__ void __launch_bounds__(RG_THREADS) k_rows_gemm(RowsGemmArgs a) {
                 }
                 u32x4 o;
 #pragma unroll
-                for (int e = 0; e < 4; e++) o[e] = f32_to_bf16(v[2 * e]) | (f32_to_bf16(v[2 * e + 1]) << 16);
+                for (int e = 0; e < 4; e++) o[e] = f32x2_to_bf16x2(v[2 * e], v[2 * e + 1]);
                 *reinterpret_cast<u32x4 *>(reinterpret_cast<bf16_t *>(a.out) + at) = o;
             }
         }
