@@ -65,7 +65,7 @@
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
 #define DEC_DEPTH 4         /* page buffers per wave: 3 pages (12.4 KiB) in flight while one is computed */
 /* DEC_DEPTH 4 is the depth built and tested. The ring's rotation and clamped loads work for any depth, and 5 or 6
- * buffers fit in registers at one wave per SIMD, but the page stream already runs at the in-order ceiling with 4. */
+ * buffers fit in registers at one wave per SIMD, but measured 1-2 us slower per call on configs 2, 3 and 5. */
 static_assert(DEC_DEPTH == 4, "the page ring is 4 buffers deep");
 
 /* Schedule units (page equivalents, measured on config 3 by sweeping these values) of a piece start (the
