@@ -246,6 +246,15 @@ enum {
 int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out, const void *res,
                       int tile_n, int tile_m, void *stream);
 
+/* nc_slot_gemm_bf16 whose launch also reads [prefetch, prefetch + prefetch_bytes) (16-byte aligned; whole 64 KiB
+ * blocks, the rest is skipped) on the compute units the tiles leave idle, and discards it: bytes read so sit in the
+ * memory-side cache for the next kernel. A decode step passes the next GEMM's weights (the up GEMM W_down, the down
+ * GEMM the next layer's W_qkv, the qkv GEMM W_o), which the next GEMM then streams from that cache instead of HBM.
+ * Outputs are bit-identical to nc_slot_gemm_bf16's; with the many-rows tile (m >= 512, tile 0 x 0) nothing is read.
+ * No counterpart in the reference (its k_wgmma streams each layer's weights from HBM). */
+int nc_slot_gemm_bf16_prefetch(const void *w, int n, int k, const void *x, int m, int epi, void *out, const void *res,
+                               int tile_n, int tile_m, const void *prefetch, long long prefetch_bytes, void *stream);
+
 /* ------------------------------------------------------------------------------------------------------------
  * The decoder handle (the reference's dec_* runtime, model/kernels/decode.cu:693-1131, bound by
  * inference/decoder.py:129-324): B slots of at most max_len positions over this library's kernels, an fp8 cache per

@@ -147,7 +147,10 @@ static int enqueue_qkv(Decoder *d, DecRows &r, int n, int l) {
     const int cols = (d->H + 2 * d->Hkv) * NC_HEAD_DIM;
     if (d->mixes && (ly.lr != 1.0f || ly.l0 != 0.0f))
         DEC_TRY(nc_mix_bf16(r.x, r.x0, (long long)n * d->C, ly.lr, ly.l0, d->stream));
-    DEC_TRY(nc_slot_gemm_bf16(ly.qkv, cols, d->C, r.x, n, NC_GEMM_NORM_STORE, r.qkv, nullptr, 0, 0, d->stream));
+    /* each decode GEMM's idle compute units pull the next GEMM's weights into the memory-side cache (here W_o;
+     * the many-rows tile of a long prefill reads nothing extra) */
+    DEC_TRY(nc_slot_gemm_bf16_prefetch(ly.qkv, cols, d->C, r.x, n, NC_GEMM_NORM_STORE, r.qkv, nullptr, 0, 0, ly.o,
+                                       (long long)d->C * d->H * NC_HEAD_DIM * 2, d->stream));
     if (ly.ve)
         DEC_TRY(nc_value_embed_bf16(r.qkv, cols, r.x, d->C, r.tok, ly.ve, d->vocab, ly.ve_gate, n, d->C, d->H, d->Hkv,
                                     d->stream));
@@ -158,9 +161,14 @@ static int enqueue_qkv(Decoder *d, DecRows &r, int n, int l) {
 static int enqueue_mlp(Decoder *d, DecRows &r, int n, int l) {
     const DecLayer &ly = d->layer[l];
     const int hd = d->H * NC_HEAD_DIM;
+    /* the up GEMM pulls W_down, the down GEMM the next layer's W_qkv (the o GEMM is too short to hide W_up's read) */
+    const void *next_qkv = l + 1 < d->L ? d->layer[l + 1].qkv : nullptr;
+    const long long qkv_bytes = next_qkv ? (long long)(d->H + 2 * d->Hkv) * NC_HEAD_DIM * d->C * 2 : 0;
     DEC_TRY(nc_slot_gemm_bf16(ly.o, d->C, hd, r.o, n, NC_GEMM_RESID, r.x, r.x, 0, 0, d->stream));
-    DEC_TRY(nc_slot_gemm_bf16(ly.up, d->F, d->C, r.x, n, NC_GEMM_RELU2_NORM, r.u, nullptr, 0, 0, d->stream));
-    DEC_TRY(nc_slot_gemm_bf16(ly.down, d->C, d->F, r.u, n, NC_GEMM_RESID, r.x, r.x, 0, 0, d->stream));
+    DEC_TRY(nc_slot_gemm_bf16_prefetch(ly.up, d->F, d->C, r.x, n, NC_GEMM_RELU2_NORM, r.u, nullptr, 0, 0, ly.down,
+                                       (long long)d->C * d->F * 2, d->stream));
+    DEC_TRY(nc_slot_gemm_bf16_prefetch(ly.down, d->C, d->F, r.u, n, NC_GEMM_RESID, r.x, r.x, 0, 0, next_qkv, qkv_bytes,
+                                       d->stream));
     return 0;
 }
 

@@ -29,6 +29,7 @@
  * logits for nc_argmax_f32).
  */
 #include "common.h"
+#include <algorithm>
 
 #define SG_THREADS 256
 #define SG_WAVES 4
@@ -48,6 +49,9 @@ struct SlotGemmArgs {
     const bf16_t *res; /* [m][n] RESID's addend, may equal out */
     int n, k, m;
     int n_tiles, m_slices, units_per_xcd;
+    const unsigned char *pf; /* read by the pf_wgs workgroups past the tiles' (null: none) */
+    long long pf_bytes;
+    int pf_wgs;
 };
 
 /* The 4 waves as WN (over W rows) x 4/WN (over batch rows): the split that reads the fewest fragments per wave
@@ -100,6 +104,25 @@ __device__ __forceinline__ void sg_dma(const unsigned char *const *src, size_t o
  * chunk moves rows 8i..8i+7: lane l lands at slot + 1024 i + 16 l (row 8i + l/8, position l % 8) and therefore
  * fetches piece (l % 8) ^ (row & 7) of its row -- every instruction reads 8 whole 128-byte row segments.
  */
+/* A prefetch workgroup's part of [pf, pf + pf_bytes): whole 64 KiB blocks b = wg, wg + pf_wgs, ... read with 16
+ * loads in flight per lane and discarded, so that the bytes sit in the memory-side cache for the next kernel (the
+ * next GEMM's weights). Plain loads: the nontemporal hint would keep them out of that cache. */
+__device__ __forceinline__ void sg_prefetch(const SlotGemmArgs &a) {
+    constexpr int U = 16;
+    constexpr long long BLOCK = (long long)SG_THREADS * 16 * U;
+    const long long blocks = a.pf_bytes / BLOCK;
+    u32x4 acc = u32x4{0u, 0u, 0u, 0u};
+    for (long long b = (long long)blockIdx.x - 8 * a.units_per_xcd; b < blocks; b += a.pf_wgs) {
+        const unsigned char *p = a.pf + b * BLOCK + (long long)threadIdx.x * 16;
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const u32x4 *>(p + (long long)u * SG_THREADS * 16);
+#pragma unroll
+        for (int u = 0; u < U; u++) acc |= v[u];
+    }
+    asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3])); /* the loads stay */
+}
+
 template <int NT, int MT, int EPI>
 __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
     constexpr int ROWS = NT + MT, DMAS = ROWS / 8, DPW = DMAS / SG_WAVES; /* DMA instructions per chunk, per wave */
@@ -112,6 +135,10 @@ __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
     static_assert(D >= 3, "ring depth");
     __shared__ __attribute__((aligned(1024))) unsigned char ring[D * SLOT];
 
+    if ((int)blockIdx.x >= 8 * a.units_per_xcd) { /* a prefetch workgroup (nc_slot_gemm_bf16_prefetch) */
+        sg_prefetch(a);
+        return;
+    }
     const int unit = (blockIdx.x & 7) * a.units_per_xcd + (blockIdx.x >> 3);
     if (unit >= a.n_tiles * a.m_slices) return;
     const int nt = unit / a.m_slices, ms = unit % a.m_slices;
@@ -671,8 +698,22 @@ static void sg_auto_tile(int n, int m, int &nt, int &mt) {
     }
 }
 
-extern "C" int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out,
-                                 const void *res, int nt, int mt, void *stream) {
+/* Compute units of the current device (cached per device). */
+static int sg_device_cus() {
+    static int cached[64];
+    int dev = 0;
+    NC_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) dev = 0;
+    if (!cached[dev]) {
+        int cus = 0;
+        NC_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cached[dev] = cus > 0 ? cus : 1;
+    }
+    return cached[dev];
+}
+
+static int slot_gemm(const void *w, int n, int k, const void *x, int m, int epi, void *out, const void *res, int nt,
+                     int mt, const void *prefetch, long long prefetch_bytes, void *stream) {
     NC_REQUIRE(n > 0 && k > 0 && m >= 0, "nc_slot_gemm_bf16: n %d, k %d, m %d", n, k, m);
     NC_REQUIRE(n % 32 == 0 && k % SG_CHUNK == 0, "nc_slot_gemm_bf16: n = %d must be a multiple of 32 and k = %d of %d",
                n, k, SG_CHUNK);
@@ -721,7 +762,24 @@ extern "C" int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int
     a.m_slices = (m + mt - 1) / mt;
     const long long units = (long long)a.n_tiles * a.m_slices;
     a.units_per_xcd = (int)((units + 7) / 8);
-    hipLaunchKernelGGL(kern, dim3(8 * a.units_per_xcd), dim3(SG_THREADS), 0, (hipStream_t)stream, a);
+    /* prefetch workgroups on the compute units the tiles leave idle, behind the tiles in dispatch order */
+    a.pf = (const unsigned char *)prefetch;
+    a.pf_bytes = prefetch ? prefetch_bytes : 0;
+    a.pf_wgs = a.pf_bytes >= 65536 ? std::max(0, sg_device_cus() - 8 * a.units_per_xcd) : 0;
+    hipLaunchKernelGGL(kern, dim3(8 * a.units_per_xcd + a.pf_wgs), dim3(SG_THREADS), 0, (hipStream_t)stream, a);
     NC_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int nc_slot_gemm_bf16(const void *w, int n, int k, const void *x, int m, int epi, void *out,
+                                 const void *res, int nt, int mt, void *stream) {
+    return slot_gemm(w, n, k, x, m, epi, out, res, nt, mt, nullptr, 0, stream);
+}
+
+extern "C" int nc_slot_gemm_bf16_prefetch(const void *w, int n, int k, const void *x, int m, int epi, void *out,
+                                          const void *res, int nt, int mt, const void *prefetch,
+                                          long long prefetch_bytes, void *stream) {
+    NC_REQUIRE(prefetch_bytes >= 0 && (prefetch || prefetch_bytes == 0) && (uintptr_t)prefetch % 16 == 0,
+               "nc_slot_gemm_bf16_prefetch: prefetch %p of %lld bytes", prefetch, prefetch_bytes);
+    return slot_gemm(w, n, k, x, m, epi, out, res, nt, mt, prefetch, prefetch_bytes, stream);
 }

@@ -350,16 +350,19 @@ class Fp8Decoder:
         x0 = x.clone() if self.mixes else None
         for l in range(self.cfg.layers):
             lw = self.model.layers[l]
+            nxt = self.model.layers[l + 1]["wqkv"] if l + 1 < self.cfg.layers else None
             self._mix(l, x, x0)
-            qkv = slot_gemm(x, lw["wqkv"], NORM_STORE)
+            # each GEMM's idle compute units pull the next GEMM's weights into the memory-side cache (the o GEMM
+            # is too short to hide the up weights' read)
+            qkv = slot_gemm(x, lw["wqkv"], NORM_STORE, prefetch=lw["wo"])
             self._value_embed(l, qkv, x, tok)
             # the append (decode.cu:550-565) and attention in one call: sequence b is cache row b
             o = decode_step(qkv, self.caches[l], pos, lw["q_gain"], lw["k_gain"], self.cos, self.sin, self.cfg.heads,
                             max_ctx=self.max_len, window=self.cfg.window(l), workspace=self.ws,
                             piece_pages=PIECE_PAGES)
             slot_gemm(o.reshape(o.shape[0], -1), lw["wo"], RESID, res=x, out=x)
-            u = slot_gemm(x, lw["wup"], RELU2_NORM)
-            slot_gemm(u, lw["wdown"], RESID, res=x, out=x)
+            u = slot_gemm(x, lw["wup"], RELU2_NORM, prefetch=lw["wdown"])
+            slot_gemm(u, lw["wdown"], RESID, res=x, out=x, prefetch=nxt)
         logits = slot_gemm(x, self.lm_head, NORM_F32)
         choose_tokens(logits, self.cfg.vocab, pos, temperature=part(self.temperature), top_p=part(self.top_p),
                       seed=part(self.seeds), first=part(self.first), slots=self.slots if slots is None else slots,

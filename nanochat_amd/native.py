@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple] = {
     "nc_embed_rms_norm": (I32, [P, I32, I64, P, I32, I32, P, P]),
     "nc_mix_bf16": (I32, [P, P, I64, F32, F32, P]),
     "nc_slot_gemm_bf16": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P]),
+    "nc_slot_gemm_bf16_prefetch": (I32, [P, I32, I32, P, I32, I32, P, P, I32, I32, P, I64, P]),
     "dec_create": (P, [P, P, P, P, P]),
     "dec_create_v2": (P, [P, I32, P, P, P, P]),
     "dec_destroy": (None, [P]),

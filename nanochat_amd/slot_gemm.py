@@ -22,9 +22,11 @@ STORE, NORM_STORE, RESID, RELU2_NORM, NORM_F32 = range(5)
 
 
 def slot_gemm(x: Tensor, w: Tensor, epi: int = STORE, *, res: Tensor | None = None, out: Tensor | None = None,
-              tile: tuple[int, int] = (0, 0)) -> Tensor:
+              tile: tuple[int, int] = (0, 0), prefetch: Tensor | None = None) -> Tensor:
     """x bf16 [m][k], w bf16 [n][k] (contiguous): the [m][n] result (bf16, fp32 for NORM_F32), into out if given.
-    tile = (rows of w, rows of x) per work unit; (0, 0) picks one from the shape."""
+    tile = (rows of w, rows of x) per work unit; (0, 0) picks one from the shape. prefetch: a contiguous GPU tensor
+    (the next GEMM's weights) that the launch's idle compute units read into the memory-side cache
+    (nc_slot_gemm_bf16_prefetch); the result is the same."""
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
         raise ValueError("slot_gemm takes bf16 x [m][k] and w [n][k]")
     if not (x.is_contiguous() and w.is_contiguous()):
@@ -41,6 +43,13 @@ def slot_gemm(x: Tensor, w: Tensor, epi: int = STORE, *, res: Tensor | None = No
     if epi == RESID:
         if res is None or res.shape != (m, n) or res.dtype != torch.bfloat16 or not res.is_contiguous():
             raise ValueError(f"RESID needs a contiguous bf16 res [{m}][{n}]")
-    check(hip_library().nc_slot_gemm_bf16(pointer(w), n, k, pointer(x), m, epi, pointer(out), pointer(res),
-                                          tile[0], tile[1], stream()))
+    if prefetch is None:
+        check(hip_library().nc_slot_gemm_bf16(pointer(w), n, k, pointer(x), m, epi, pointer(out), pointer(res),
+                                              tile[0], tile[1], stream()))
+        return out
+    if not (prefetch.is_cuda and prefetch.is_contiguous()):
+        raise ValueError("prefetch must be a contiguous GPU tensor")
+    check(hip_library().nc_slot_gemm_bf16_prefetch(pointer(w), n, k, pointer(x), m, epi, pointer(out), pointer(res),
+                                                   tile[0], tile[1], pointer(prefetch),
+                                                   prefetch.numel() * prefetch.element_size(), stream()))
     return out

@@ -126,3 +126,28 @@ def test_many_rows_in_place_residual(gpu):
     slot_gemm(x, w, RESID, res=h, out=h)
     torch.cuda.synchronize()
     assert torch.equal(h, want)
+
+
+@pytest.mark.parametrize("m, n, k, pf_bytes", [
+    (128, 4992, 1664, 1664 * 1664 * 2),  # config 5 qkv, prefetching W_o
+    (128, 6656, 1664, 1664 * 6656 * 2),  # up, prefetching W_down
+    (128, 1664, 6656, 4992 * 1664 * 2),  # down, prefetching the next W_qkv
+    (37, 224, 192, 65536 * 3 + 4096),    # whole 64 KiB blocks and a remainder that is skipped
+    (5, 64, 64, 60000),                  # under one block: nothing read
+    (600, 1664, 1664, 1664 * 1664 * 2),  # the many-rows tile: nothing read
+])
+@pytest.mark.parametrize("epi", [NORM_STORE, RESID, RELU2_NORM])
+def test_prefetch_leaves_the_result_bit_identical(gpu, m, n, k, pf_bytes, epi):
+    """nc_slot_gemm_bf16_prefetch: the workgroups past the tiles read the prefetch range on the idle compute units;
+    the GEMM's outputs equal nc_slot_gemm_bf16's bit for bit, in place (RESID) too."""
+    x, w, res = data(m, n, k, gpu, 41)
+    pf = torch.randint(0, 1 << 15, (pf_bytes // 2,), dtype=torch.int16, device=gpu)
+    if epi == RESID:
+        r1, r2 = res.clone(), res.clone()
+        plain = slot_gemm(x, w, epi, res=r1, out=r1)
+        fetched = slot_gemm(x, w, epi, res=r2, out=r2, prefetch=pf)
+    else:
+        plain = slot_gemm(x, w, epi)
+        fetched = slot_gemm(x, w, epi, prefetch=pf)
+    torch.cuda.synchronize()
+    assert torch.equal(plain.view(torch.int16), fetched.view(torch.int16))
