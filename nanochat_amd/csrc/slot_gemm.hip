@@ -98,12 +98,6 @@ __device__ __forceinline__ void sg_dma(const unsigned char *const *src, size_t o
         __builtin_amdgcn_global_load_lds(src[d] + off, dst + 1024 * (wv + SG_WAVES * d), 16, 0, 0);
 }
 
-/*
- * LDS layout of a slot: row r (W rows 0..NT-1, then x rows) at 128 r; its 16-byte piece p (k columns 8p..8p+7 of
- * the chunk) at position p ^ (r & 7), so the fragment reads below are bank-conflict free. DMA instruction i of a
- * chunk moves rows 8i..8i+7: lane l lands at slot + 1024 i + 16 l (row 8i + l/8, position l % 8) and therefore
- * fetches piece (l % 8) ^ (row & 7) of its row -- every instruction reads 8 whole 128-byte row segments.
- */
 /* A prefetch workgroup's part of [pf, pf + pf_bytes): whole 64 KiB blocks b = wg, wg + pf_wgs, ... read with 16
  * loads in flight per lane and discarded, so that the bytes sit in the memory-side cache for the next kernel (the
  * next GEMM's weights). Plain loads: the nontemporal hint would keep them out of that cache. */
@@ -123,6 +117,12 @@ __device__ __forceinline__ void sg_prefetch(const SlotGemmArgs &a) {
     asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3])); /* the loads stay */
 }
 
+/*
+ * LDS layout of a slot: row r (W rows 0..NT-1, then x rows) at 128 r; its 16-byte piece p (k columns 8p..8p+7 of
+ * the chunk) at position p ^ (r & 7), so the fragment reads below are bank-conflict free. DMA instruction i of a
+ * chunk moves rows 8i..8i+7: lane l lands at slot + 1024 i + 16 l (row 8i + l/8, position l % 8) and therefore
+ * fetches piece (l % 8) ^ (row & 7) of its row -- every instruction reads 8 whole 128-byte row segments.
+ */
 template <int NT, int MT, int EPI>
 __global__ void __launch_bounds__(SG_THREADS) k_slot_gemm(SlotGemmArgs a) {
     constexpr int ROWS = NT + MT, DMAS = ROWS / 8, DPW = DMAS / SG_WAVES; /* DMA instructions per chunk, per wave */
