@@ -168,6 +168,22 @@ def test_slot_gemm_rejects_bad_arguments():
     assert lib.nc_slot_gemm_bf16(FAKE, 32, 64, FAKE, 0, 0, FAKE, NULL, 0, 0, NULL) == 0  # m = 0: nothing launched
 
 
+def test_slot_gemm_prefetch_rejects_bad_arguments():
+    """The prefetch range is checked before the GEMM's own arguments; the GEMM's checks still apply."""
+    lib = native.hip_library()
+
+    def rejects(pf, pf_bytes, n, message):
+        rc = lib.nc_slot_gemm_bf16_prefetch(FAKE, n, 64, FAKE, 8, 0, FAKE, NULL, 0, 0, pf, pf_bytes, NULL)
+        assert rc < 0
+        assert message in lib.nc_last_error().decode(), lib.nc_last_error().decode()
+
+    rejects(NULL, 65536, 32, "prefetch")       # bytes without a range
+    rejects(FAKE, -1, 32, "prefetch")          # negative size
+    rejects(ctypes.c_void_p(0x1008), 65536, 32, "prefetch")  # not 16-byte aligned
+    rejects(FAKE, 65536, 48, "multiple of 32")  # a good range, a bad GEMM
+    assert lib.nc_slot_gemm_bf16_prefetch(FAKE, 32, 64, FAKE, 0, 0, FAKE, NULL, 0, 0, FAKE, 65536, NULL) == 0  # m = 0
+
+
 def test_choose_rejects_bad_arguments():
     lib = native.hip_library()
     need = lib.nc_choose_workspace_bytes(8, 1000)
