@@ -1,0 +1,170 @@
+"""Writes golden vectors of the reference's own torch path, run on the CPU of the build container, for the parts of
+the oracle that the mathematics alone leaves open:
+
+    python tests/golden/make_reference_vectors.py
+
+reference_qk_norm_rope.npz   inference/modeling_nanochat.py:37-45 `qk_norm_rope` (torch.rsqrt of torch's mean, then
+                             gain and the -theta rotation, one bf16 rounding) and :29-34 `rotary` on seeded bf16 rows
+                             (N(0, 1), 1 % outliers at 8 sigma, rows scaled from 2^-20 to 2^20, a zero row, one-hot
+                             rows) at seeded positions, theta 1e4 and 1e6: the inputs, the gains, the reference's cos /
+                             sin tables and its output bits.
+reference_model_small.npz    inference/modeling_nanochat.py:136-195 `NanochatForCausalLM` (eager attention, bf16
+                             weights and activations as export_hf.py writes them) on a tiny MHA model whose weights
+                             fixture_model() below derives from a counter hash (no library RNG): 3 layers, d 256,
+                             2 heads, vocab 256, a sliding-window layer pair, a value-embedding layer, a non-identity
+                             residual / x0 mix and non-unit QK-norm gains; the capped logits of every position of two
+                             16-token sequences.
+
+The reference module is imported from /root/reference in this container only, by this script; the tests read the
+fixtures and never import or read the reference.
+"""
+
+from __future__ import annotations
+
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+REFERENCE = "/root/reference/inference/modeling_nanochat.py"
+
+# the tiny model: MHA (the reference's NanochatAttention projects k and v to all H heads)
+MODEL = dict(layers=3, d_model=256, heads=2, vocab=256, theta=1e4, windows=(4, -1, 4), ve_layers=(1,), softcap=15.0)
+SEQS, SEQ_LEN, IDS_SEED = 2, 16, 11
+
+
+def hashed_uniform(n: int, seed: int) -> np.ndarray:
+    """n values in [-sqrt(3), sqrt(3)) (unit variance) from a splitmix64 hash of (index, seed): the same values on
+    every machine and numpy version."""
+    with np.errstate(over="ignore"):
+        x = np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15) + np.uint64(seed) * np.uint64(
+            0xD1B54A32D192ED03)
+        x ^= x >> np.uint64(30)
+        x *= np.uint64(0xBF58476D1CE4E5B9)
+        x ^= x >> np.uint64(27)
+        x *= np.uint64(0x94D049BB133111EB)
+        x ^= x >> np.uint64(31)
+    u = (x >> np.uint64(11)).astype(np.float64) / float(1 << 53)
+    return ((2.0 * u - 1.0) * np.sqrt(3.0)).astype(np.float32)
+
+
+def fixture_model():
+    """The tiny model's weights as a nanochat_amd.decoder.Weights on the CPU (bf16 matrices, fp32 gains, gates and
+    mix), every tensor from hashed_uniform with its own seed."""
+    sys.path.insert(0, REPO)
+    from nanochat_amd.decoder import ModelConfig, Weights
+
+    cfg = ModelConfig(layers=MODEL["layers"], d_model=MODEL["d_model"], heads=MODEL["heads"], vocab=MODEL["vocab"],
+                      theta=MODEL["theta"], windows=MODEL["windows"], ve_layers=MODEL["ve_layers"],
+                      softcap=MODEL["softcap"])
+    seed = iter(range(1000, 2000))
+    d, C = cfg.d_model, cfg.heads * 128
+
+    def t(shape, scale, offset=0.0, dtype=torch.bfloat16):
+        v = hashed_uniform(int(np.prod(shape)), next(seed)).reshape(shape) * np.float32(scale) + np.float32(offset)
+        return torch.from_numpy(v).to(dtype)
+
+    w = Weights()
+    w.cfg = cfg
+    std = 0.06  # ~ 1/sqrt(d): every sublayer moves the residual stream visibly
+    w.wte = t((cfg.vocab, d), 1.0)
+    w.layers = []
+    for i in range(cfg.layers):
+        lw = dict(wqkv=t((3 * C, d), std), wo=t((d, C), std), wup=t((cfg.mlp_mult * d, d), std),
+                  wdown=t((d, cfg.mlp_mult * d), std / 2),
+                  q_gain=t((128,), 0.25, 1.0, torch.float32), k_gain=t((128,), 0.25, 1.0, torch.float32))
+        if i in cfg.ve_layers:
+            lw["ve"] = t((cfg.vocab, C), 0.8)
+            lw["ve_gate"] = t((cfg.heads, d), 0.2, 0.0, torch.float32)
+        w.layers.append(lw)
+    w.lm_head = t((cfg.vocab, d), std)
+    w.resid_lambdas = t((cfg.layers,), 0.2, 1.0, torch.float32)
+    w.x0_lambdas = t((cfg.layers,), 0.1, 0.3, torch.float32)
+    return w
+
+
+def fixture_ids() -> np.ndarray:
+    return np.random.default_rng(IDS_SEED).integers(0, MODEL["vocab"], (SEQS, SEQ_LEN)).astype(np.int64)
+
+
+def _reference():
+    spec = importlib.util.spec_from_file_location("reference_modeling_nanochat", REFERENCE)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def qk_vectors(ref) -> dict:
+    rng = np.random.default_rng(3)
+    n = 128
+    x = rng.standard_normal((n, 128)).astype(np.float32)
+    x[rng.random((n, 128)) < 0.01] = 8.0
+    x[32:64] *= np.float32(2.0) ** rng.integers(-20, 21, (32, 1)).astype(np.float32)  # scales 2^-20 .. 2^20
+    x[64] = 0.0
+    x[65:70] = 0.0
+    x[65:70, rng.integers(0, 128, 5)] = [1.0, -3.0, 0.5, 2.0 ** -30, 1e30]  # one-hot rows
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    gain = torch.from_numpy((0.5 + rng.random(128)).astype(np.float32))
+    pos = torch.from_numpy(rng.integers(0, 8192, n).astype(np.int64))
+    pos[:4] = torch.tensor([0, 1, 8191, 4096])
+    out = {"x_bits": xb.view(torch.int16).numpy().view(np.uint16), "gain": gain.numpy(), "pos": pos.numpy()}
+    eps = float(torch.finfo(torch.float32).eps)
+    for theta in (1e4, 1e6):
+        cos, sin = ref.rotary(pos, 128, theta)  # [n][64] fp32
+        # qk_norm_rope's x is (..., H, D) with cos (..., D/2): one head per row
+        y = ref.qk_norm_rope(xb[:, None, :], gain, cos, sin, eps)[:, 0, :]
+        tag = f"{int(theta):d}"
+        out[f"cos_{tag}"], out[f"sin_{tag}"] = cos.numpy(), sin.numpy()
+        out[f"y_bits_{tag}"] = y.view(torch.int16).numpy().view(np.uint16)
+    return out
+
+
+def model_vectors(ref) -> dict:
+    from safetensors.torch import load_file
+
+    sys.path.insert(0, REPO)
+    from nanochat_amd.checkpoint import save_hf
+
+    w = fixture_model()
+    with tempfile.TemporaryDirectory() as d:
+        save_hf(w, d, max_positions=64)
+        cfg_json = json.loads(open(os.path.join(d, "config.json")).read())
+        state = load_file(os.path.join(d, "model.safetensors"))
+    config = ref.NanochatConfig(**cfg_json)
+    config._attn_implementation = "eager"  # the reference's own eager_attention_forward (bf16 probabilities)
+    model = ref.NanochatForCausalLM(config)
+    keep_fp32 = set(ref.NanochatPreTrainedModel._keep_in_fp32_modules_strict)
+    for name, p in model.named_parameters():  # the export's dtypes: fp32 where the training forward reads fp32
+        p.data = p.data.to(torch.float32 if keep_fp32 & set(name.split(".")) else torch.bfloat16)
+    missing, unexpected = model.load_state_dict(state, strict=True)
+    assert not missing and not unexpected
+    for name, p in model.named_parameters():
+        assert p.dtype == state[name].dtype, name
+    model.eval()
+    ids = fixture_ids()
+    with torch.no_grad():
+        logits = model(input_ids=torch.from_numpy(ids)).logits.float().numpy()
+    return {"ids": ids, "logits": logits, "config_json": np.array(json.dumps(cfg_json))}
+
+
+def main() -> None:
+    import transformers
+
+    ref = _reference()
+    meta = {"torch": torch.__version__, "transformers": transformers.__version__,
+            "reference": "inference/modeling_nanochat.py"}
+    qk = qk_vectors(ref)
+    np.savez_compressed(os.path.join(HERE, "reference_qk_norm_rope.npz"), meta=np.array(json.dumps(meta)), **qk)
+    mv = model_vectors(ref)
+    np.savez_compressed(os.path.join(HERE, "reference_model_small.npz"), meta=np.array(json.dumps(meta)), **mv)
+    print("wrote reference_qk_norm_rope.npz and reference_model_small.npz", meta)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+"""The oracle against vectors of the reference's own torch path (tests/golden/make_reference_vectors.py ran
+inference/modeling_nanochat.py on the build container's CPU and froze its outputs; nothing here imports the
+reference):
+
+* rotary tables (modeling_nanochat.py:29-34): oracle.golden.rotary_tables equals the reference's cos / sin bits;
+* QK-norm + RoPE (modeling_nanochat.py:37-45): the oracle's fixed-tree rule against torch's mean and rsqrt, bit for
+  bit except where the two sums of squares round apart (then one bf16 ulp of the output);
+* the whole model (NanochatForCausalLM, eager attention with bf16 probabilities, bf16 K/V): the independent dense
+  forward of tests/test_oracle_model.py (fp32 probabilities) and the CpuModel (fp8 cache, fp64 attention) against the
+  reference's capped logits, and every structural slip planted in the CpuModel must fall outside the CpuModel's bound.
+"""
+
+import importlib.util
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import golden as G
+from oracle.model import CpuModel
+from test_oracle_model import (MixIgnoresX0, MlpNormOfLayerInput, NoFinalNorm, SwappedMix, VeGateWithoutFactor2,
+                               WindowOffByOne, cpu_logits, dense_logits)
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _maker():
+    spec = importlib.util.spec_from_file_location("make_reference_vectors", os.path.join(HERE,
+                                                                                         "make_reference_vectors.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)  # defines the fixture model; the reference is imported only by its main()
+    return mod
+
+
+QK = np.load(os.path.join(HERE, "reference_qk_norm_rope.npz"))
+MODEL = np.load(os.path.join(HERE, "reference_model_small.npz"))
+
+
+@pytest.mark.parametrize("theta", ["10000", "1000000"])
+def test_rotary_tables_equal_the_reference(theta):
+    cos, sin = G.rotary_tables(8192, float(theta))
+    pos = QK["pos"]
+    np.testing.assert_array_equal(cos[pos], QK[f"cos_{theta}"])
+    np.testing.assert_array_equal(sin[pos], QK[f"sin_{theta}"])
+
+
+@pytest.mark.parametrize("theta", ["10000", "1000000"])
+def test_qk_norm_rope_within_one_ulp_of_the_reference(theta):
+    """Measured: 1 element of 16 384 differs (by 1 ulp) at theta 1e4, none at 1e6. The bound allows 1 ulp on at most
+    0.1 % of the elements; a wrong order of norm, gain and rotation, a rotation by +theta or a dropped epsilon moves
+    most elements by far more."""
+    x, gain = QK["x_bits"], QK["gain"]
+    y = G.qk_norm_rope(x, gain, QK[f"cos_{theta}"], QK[f"sin_{theta}"])
+    want = QK[f"y_bits_{theta}"]
+    ulps = np.abs(y.view(np.int16).astype(np.int64) - want.view(np.int16).astype(np.int64))
+    same_sign = (y >> 15) == (want >> 15)
+    print(f"theta {theta}: {int((y != want).sum())} of {y.size} elements differ")
+    assert np.all(same_sign | (y == want) | ((y & 0x7FFF) == 0) & ((want & 0x7FFF) == 0))
+    assert ulps.max() <= 1
+    assert (y != want).mean() <= 1e-3
+
+
+def _capped(logits: np.ndarray, cap: float) -> np.ndarray:
+    """inference/modeling_nanochat.py:194: c tanh(logits / c) in fp32."""
+    return (cap * np.tanh(logits.astype(np.float32) / np.float32(cap))).astype(np.float32)
+
+
+T_PROMPT = 6
+
+
+def _rel(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
+    spread = MODEL["logits"].std()
+    err = np.abs(got - want)
+    return float(err.max() / spread), float(err.mean() / spread)
+
+
+def _cpu_vs_reference(cls) -> tuple[float, float]:
+    w = _maker().fixture_model()
+    ids = MODEL["ids"]
+    B, T = ids.shape
+    got = np.stack(cpu_logits(cls(w, B, T + 1), ids, T_PROMPT, T - T_PROMPT - 1), 1)
+    want = MODEL["logits"][:, T_PROMPT - 1:T_PROMPT - 1 + got.shape[1]]
+    return _rel(_capped(got, w.cfg.softcap), want)
+
+
+# Measured against the reference's logits (relative to their spread, 0.93): the dense forward max 0.042, mean 0.006
+# (fp32 against bf16 probabilities, summation orders); the CpuModel max 0.077, mean 0.016 (the fp8 cache's own
+# effect: the dense forward with fp8 K/V measures max 0.083, mean 0.016). Bounds about twice those.
+DENSE_MAX, DENSE_MEAN = 0.08, 0.012
+CPU_MAX, CPU_MEAN = 0.15, 0.03
+
+
+def test_fixture_model_is_the_one_the_vectors_were_made_from():
+    w = _maker().fixture_model()
+    cfg = json.loads(str(MODEL["config_json"]))
+    assert cfg["num_hidden_layers"] == w.cfg.layers and cfg["hidden_size"] == w.cfg.d_model
+    assert cfg["value_embedding_layers"] == list(w.cfg.ve_layers)
+    assert cfg["sliding_window"] == 5 and cfg["layer_types"][1] == "full_attention"
+    assert MODEL["logits"].shape == (*MODEL["ids"].shape, w.cfg.vocab)
+
+
+def test_dense_forward_matches_the_reference_model():
+    w = _maker().fixture_model()
+    got = _capped(dense_logits(w, MODEL["ids"], fp8_kv=False).numpy(), w.cfg.softcap)
+    mx, mean = _rel(got, MODEL["logits"])
+    print(f"dense vs reference: max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx <= DENSE_MAX and mean <= DENSE_MEAN, (mx, mean)
+
+
+def test_cpu_model_matches_the_reference_model():
+    mx, mean = _cpu_vs_reference(CpuModel)
+    print(f"CpuModel vs reference: max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx <= CPU_MAX and mean <= CPU_MEAN, (mx, mean)
+
+
+@pytest.mark.parametrize("slip", [MlpNormOfLayerInput, SwappedMix, MixIgnoresX0, NoFinalNorm, VeGateWithoutFactor2,
+                                  WindowOffByOne], ids=lambda c: c.__name__)
+def test_reference_vectors_catch_structural_slips(slip):
+    mx, mean = _cpu_vs_reference(slip)
+    print(f"{slip.__name__} vs reference: max {mx:.4f}, mean {mean:.4f} of the logits' spread")
+    assert mx > CPU_MAX or mean > CPU_MEAN, f"{slip.__name__} passed the comparison: not pinned"
