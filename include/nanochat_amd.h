@@ -142,8 +142,8 @@ int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, const int32
                               int piece_pages, void *out, void *workspace, long long workspace_bytes, void *stream);
 
 /* nc_decode_step_fp8 without the workspace: the partial results between its two kernels live in a static device
- * array of 64 MiB (67108864 bytes) that the library holds on every device it runs on until the process ends, so the
- * call allocates nothing. A shape whose workspace (nc_decode_workspace_bytes) exceeds 64 MiB is rejected with an
+ * array of 64 MiB (67108864 bytes), a code object of its own that a device loads when this entry first runs on it
+ * and holds until the process ends, so the call allocates nothing. A shape whose workspace (nc_decode_workspace_bytes) exceeds 64 MiB is rejected with an
  * error (config 3's B 64, 16 / 4 heads need 21.5 MB; B 128 of 13 MHA heads 11.9 MB). Every call on a device shares
  * its array: calls in one stream are ordered, calls that may overlap on one device (two streams) race. Outputs, cache
  * bytes and pos_out are bit-identical to nc_decode_step_fp8's.

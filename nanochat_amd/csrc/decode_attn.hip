@@ -49,8 +49,8 @@
  * Roofline: HBM. Per (token, kv head) the kernel reads 128 B of K, 128 B of V and two fp32 scales: 264 B.
  */
 #include <algorithm>
-#include <mutex>
 
+#include "decode_scratch.h"
 #include "layout.h"
 #include "qk_row.h"
 
@@ -1119,36 +1119,12 @@ extern "C" int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, 
 
 /* ------------------------------------------------------------------------------------------------------------
  * The fused step without a workspace argument, for callers that cannot allocate (code under graph capture, tight
- * serving loops): the partial results and the segments' piece descriptors live in `scratch`, a static device array
- * of NC_DECODE_SCRATCH_BYTES that every device running this library holds until the process ends. Its device
- * address is taken once per device, with that device current (hipGetSymbolAddress), and passed to the kernel like
- * the workspace of nc_decode_step_fp8; the array's name is never used as an address on the host. No value needs
+ * serving loops): the partial results and the segments' piece descriptors live in a static device array of
+ * NC_DECODE_SCRATCH_BYTES (decode_scratch.hip, a code object of its own, so only devices on which this entry runs
+ * hold it, until the process ends), passed to the kernel like the workspace of nc_decode_step_fp8. No value needs
  * to start at zero: k_decode writes every segment's descriptor and every piece's partial before k_merge reads them,
  * so what earlier calls left there does not matter. Calls share their device's array, so two calls that may
  * overlap on one device (two streams) race; calls in one stream do not. */
-#define NC_DECODE_SCRATCH_BYTES (64ll << 20)
-#define NC_MAX_DEVICES 64
-
-static __device__ __align__(256) unsigned char scratch[NC_DECODE_SCRATCH_BYTES];
-
-static void *scratch_address() {
-    static void *address[NC_MAX_DEVICES];
-    static std::mutex lock;
-    int dev = 0;
-    NC_HIP_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= NC_MAX_DEVICES) {
-        fprintf(stderr, "decode_attn.hip: device %d past the %d the scratch table holds\n", dev, NC_MAX_DEVICES);
-        abort();
-    }
-    std::lock_guard<std::mutex> guard(lock);
-    if (!address[dev]) {
-        void *p = nullptr;
-        NC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        address[dev] = p;
-    }
-    return address[dev];
-}
-
 extern "C" int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride, const int32_t *pos,
                                           int32_t *pos_out, const float *q_gain, const float *k_gain,
                                           const float *cos, const float *sin, int rope_len, uint8_t *cache,
@@ -1163,6 +1139,6 @@ extern "C" int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride,
         return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
                            max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, nullptr, 0, stream);
     return decode_step(qkv, row_stride, pos, pos_out, q_gain, k_gain, cos, sin, rope_len, cache, block_table,
-                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, scratch_address(),
+                       max_blocks, num_blocks, window, B, hq, hkv, max_ctx, sm_scale, 0, out, nc_decode_scratch(),
                        NC_DECODE_SCRATCH_BYTES, stream);
 }

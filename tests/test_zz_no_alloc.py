@@ -38,6 +38,37 @@ def _step(lib, case, cfg, max_ctx, noalloc, ws):
 SHAPES = [CONFIG3, DecodeConfig("small-after-large", 5, 8, 2, ctx_range=(3, 900), paged=True, window=300, seed=97)]
 
 
+def test_scratch_is_reserved_by_the_noalloc_entry_alone(gpu):
+    """The 64 MiB scratch lives in a code object of its own: the decode entries leave it unloaded, and the first
+    no-allocation call on a device loads it (no other test calls that entry, so this one runs first in any run).
+    Every tensor exists before the device's free memory is read."""
+    lib = hip_library()
+    cfg = SHAPES[1]
+    case = build_decode_case(cfg, gpu, steps=1)
+    max_ctx = int(case.ctx.max()) + 1
+    ws = decode_workspace(cfg.batch, cfg.hq, cfg.hkv, max_ctx, gpu)
+    out = torch.empty((cfg.batch, cfg.hq, 128), dtype=torch.bfloat16, device=gpu)
+    pos = case.positions(0)
+    pos_out = torch.empty_like(pos)
+    c, qkv = case.cache, case.qkv[0]
+    args = [pointer(qkv), qkv.stride(0), pointer(pos), pointer(pos_out), pointer(case.q_gain), pointer(case.k_gain),
+            pointer(case.cos), pointer(case.sin), case.cos.shape[0], pointer(c.pages), pointer(c.block_table),
+            c.max_blocks, c.num_blocks, cfg.window, cfg.batch, cfg.hq, cfg.hkv, max_ctx, SCALE, pointer(out)]
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    check(lib.nc_decode_step_fp8(*args, pointer(ws), ws.numel(), stream()))
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    check(lib.nc_decode_step_fp8_noalloc(*args, stream()))
+    torch.cuda.synchronize()
+    free2 = torch.cuda.mem_get_info()[0]
+    mib = 1 << 20
+    print(f"first decode call {(free0 - free1) / mib:.1f} MiB, first no-alloc call {(free1 - free2) / mib:.1f} MiB",
+          flush=True)
+    assert free0 - free1 < 16 * mib
+    assert free1 - free2 >= 64 * mib
+
+
 def test_noalloc_step_equals_workspace_step(gpu):
     lib = hip_library()
     for cfg in SHAPES:  # the larger call first, then the smaller one over the same scratch
