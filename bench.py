@@ -661,7 +661,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the decode path shards by "
-              "(sequence, kv head) with no exchange, see DESIGN.md", file=sys.stderr)
+              "(sequence, kv head) with no exchange, so N GPUs would each run this step on their own share",
+              file=sys.stderr)
         sys.exit(2)
     import torch
 
