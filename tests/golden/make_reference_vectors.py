@@ -13,7 +13,8 @@ reference_model_small.npz    inference/modeling_nanochat.py:136-195 `NanochatFor
                              fixture_model() below derives from a counter hash (no library RNG): 3 layers, d 256,
                              2 heads, vocab 256, a sliding-window layer pair, a value-embedding layer, a non-identity
                              residual / x0 mix and non-unit QK-norm gains; the capped logits of every position of two
-                             16-token sequences.
+                             16-token sequences, from one full forward and from the decode protocol over the
+                             reference's own DynamicCache (5 positions prefilled, then one token per call).
 
 The reference module is imported from /root/reference in this container only, by this script; the tests read the
 fixtures and never import or read the reference.
@@ -37,6 +38,7 @@ REFERENCE = "/root/reference/inference/modeling_nanochat.py"
 # the tiny model: MHA (the reference's NanochatAttention projects k and v to all H heads)
 MODEL = dict(layers=3, d_model=256, heads=2, vocab=256, theta=1e4, windows=(4, -1, 4), ve_layers=(1,), softcap=15.0)
 SEQS, SEQ_LEN, IDS_SEED = 2, 16, 11
+PREFILL = 5  # the cached run: positions 0..4 prefilled, then one call per position 5..15
 
 
 def hashed_uniform(n: int, seed: int) -> np.ndarray:
@@ -148,9 +150,18 @@ def model_vectors(ref) -> dict:
         assert p.dtype == state[name].dtype, name
     model.eval()
     ids = fixture_ids()
+    t = torch.from_numpy(ids)
     with torch.no_grad():
-        logits = model(input_ids=torch.from_numpy(ids)).logits.float().numpy()
-    return {"ids": ids, "logits": logits, "config_json": np.array(json.dumps(cfg_json))}
+        logits = model(input_ids=t).logits.float().numpy()
+        # the decode protocol through the reference's own cache (DynamicCache.update appends each step's keys and
+        # values, modeling_nanochat.py:94-96): positions 0..PREFILL-1 at once, then one token per call
+        out = model(input_ids=t[:, :PREFILL], use_cache=True)
+        cached = [out.logits[:, -1].float()]
+        for p in range(PREFILL, SEQ_LEN):
+            out = model(input_ids=t[:, p:p + 1], past_key_values=out.past_key_values, use_cache=True)
+            cached.append(out.logits[:, -1].float())
+    return {"ids": ids, "logits": logits, "logits_cached": torch.stack(cached, 1).numpy(),
+            "cached_from": np.array(PREFILL - 1), "config_json": np.array(json.dumps(cfg_json))}
 
 
 def main() -> None:

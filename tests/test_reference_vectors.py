@@ -6,8 +6,10 @@ reference):
 * QK-norm + RoPE (modeling_nanochat.py:37-45): the oracle's fixed-tree rule against torch's mean and rsqrt, bit for
   bit except where the two sums of squares round apart (then one bf16 ulp of the output);
 * the whole model (NanochatForCausalLM, eager attention with bf16 probabilities, bf16 K/V): the independent dense
-  forward of tests/test_oracle_model.py (fp32 probabilities) and the CpuModel (fp8 cache, fp64 attention) against the
-  reference's capped logits, and every structural slip planted in the CpuModel must fall outside the CpuModel's bound.
+  forward of tests/test_oracle_model.py (fp32 probabilities) against the reference's full forward, and the CpuModel
+  (fp8 cache, fp64 attention; prefill, then one step per position) against the reference's own decode protocol over
+  its DynamicCache (positions 0..4 prefilled, then one token per call); every structural slip planted in the
+  CpuModel must fall outside the CpuModel's bound.
 """
 
 import importlib.util
@@ -66,7 +68,7 @@ def _capped(logits: np.ndarray, cap: float) -> np.ndarray:
     return (cap * np.tanh(logits.astype(np.float32) / np.float32(cap))).astype(np.float32)
 
 
-T_PROMPT = 6
+T_PROMPT = 5  # positions 0..3 prefilled, then steps at 4..15: the reference's cached logits
 
 
 def _rel(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
@@ -75,13 +77,18 @@ def _rel(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
     return float(err.max() / spread), float(err.mean() / spread)
 
 
+def cached_reference() -> np.ndarray:
+    """The reference's logits at positions T_PROMPT - 1 .. 15 through its DynamicCache."""
+    at = int(MODEL["cached_from"])
+    return MODEL["logits_cached"][:, T_PROMPT - 1 - at:]
+
+
 def _cpu_vs_reference(cls) -> tuple[float, float]:
     w = _maker().fixture_model()
     ids = MODEL["ids"]
     B, T = ids.shape
-    got = np.stack(cpu_logits(cls(w, B, T + 1), ids, T_PROMPT, T - T_PROMPT - 1), 1)
-    want = MODEL["logits"][:, T_PROMPT - 1:T_PROMPT - 1 + got.shape[1]]
-    return _rel(_capped(got, w.cfg.softcap), want)
+    got = np.stack(cpu_logits(cls(w, B, T + 1), ids, T_PROMPT, T - T_PROMPT), 1)
+    return _rel(_capped(got, w.cfg.softcap), cached_reference())
 
 
 # Measured against the reference's logits (relative to their spread, 0.93): the dense forward max 0.042, mean 0.006
@@ -89,6 +96,12 @@ def _cpu_vs_reference(cls) -> tuple[float, float]:
 # effect: the dense forward with fp8 K/V measures max 0.083, mean 0.016). Bounds about twice those.
 DENSE_MAX, DENSE_MEAN = 0.08, 0.012
 CPU_MAX, CPU_MEAN = 0.15, 0.03
+
+
+def test_reference_cached_run_equals_its_full_forward():
+    """The fixture's two reference runs agree (fp32 noise): its cache path appends and masks as its full forward."""
+    at = int(MODEL["cached_from"])
+    np.testing.assert_allclose(MODEL["logits_cached"], MODEL["logits"][:, at:], atol=1e-5, rtol=0)
 
 
 def test_fixture_model_is_the_one_the_vectors_were_made_from():
