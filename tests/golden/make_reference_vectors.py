@@ -16,6 +16,16 @@ reference_model_small.npz    inference/modeling_nanochat.py:136-195 `NanochatFor
                              16-token sequences, from one full forward and from the decode protocol over the
                              reference's own DynamicCache (5 positions prefilled, then one token per call).
 
+reference_attention.npz      inference/modeling_nanochat.py:48-56 `eager_attention_forward` (bf16 scores and
+                             products, probabilities cast to bf16) on three cases: decode with MHA (3 sequences,
+                             4 heads, contexts 37, 300, 1000), decode with GQA (2 sequences, 16 query / 4 kv heads,
+                             contexts 513 and 1500, 1 % of the elements at 8 sigma) and a causal prefill chunk (2
+                             sequences, 8 / 2 heads, 40 and 25 rows onto 100 and 250 cached keys); kv heads are
+                             repeated for the reference's MHA layout. K and V rows come from fp8_exact_rows(), values
+                             both bf16 and e4m3 code x 2^e whose absmax is 448 x 2^e: the reference's bf16 cache and
+                             this build's fp8 cache (absmax / 448 = 2^e, exact codes) hold the same numbers. The
+                             fixture keeps the q rows and the reference's outputs; the tests rebuild K and V.
+
 The reference module is imported from /root/reference in this container only, by this script; the tests read the
 fixtures and never import or read the reference.
 """
@@ -91,6 +101,52 @@ def fixture_model():
     return w
 
 
+def fp8_exact_rows(n: int, seed: int, outliers: float = 0.0) -> np.ndarray:
+    """n rows of 128 fp32 values, each exactly a bf16 and an e4m3 code times 2^e (e in [-7, -5] per row: a standard
+    deviation of 0.44 to 1.75), with the row's absmax exactly 448 x 2^e: codes of a unit-variance draw times 56 (so
+    448 is 8 sigma), one element per row (and, with `outliers`, that fraction of the others) at +-448."""
+    sys.path.insert(0, REPO)
+    from oracle import golden as G
+
+    v = hashed_uniform(n * 128, seed).reshape(n, 128) * np.float32(56.0)
+    v = G.e4m3_decode(G.e4m3_encode(v))
+    sign = np.where(hashed_uniform(n * 128, seed + 1).reshape(n, 128) < 0, -1.0, 1.0).astype(np.float32)
+    at = ((hashed_uniform(n, seed + 2) / np.sqrt(3.0) + 1.0) * 64.0).astype(np.int64).clip(0, 127)
+    v[np.arange(n), at] = 448.0 * sign[np.arange(n), at]
+    if outliers > 0:
+        hit = (hashed_uniform(n * 128, seed + 3).reshape(n, 128) / np.sqrt(3.0) + 1.0) / 2.0 < outliers
+        v = np.where(hit, 448.0 * sign, v)
+    e = -5 - ((hashed_uniform(n, seed + 4) / np.sqrt(3.0) + 1.0) * 1.5).astype(np.int64).clip(0, 2)
+    return (v * np.exp2(e.astype(np.float32))[:, None]).astype(np.float32)
+
+
+def hashed_bf16(shape, seed: int) -> np.ndarray:
+    """Unit-variance values rounded to bf16, as fp32."""
+    x = torch.from_numpy(hashed_uniform(int(np.prod(shape)), seed).reshape(shape))
+    return x.to(torch.bfloat16).float().numpy()
+
+
+# (name, batch, query heads, kv heads, cached keys per sequence, query rows per sequence, outlier fraction, seed);
+# decode: one query row at the last position; prefill: the chunk's rows after the cached keys, causal
+ATTENTION_CASES = [("decode_mha", 3, 4, 4, (36, 299, 999), (1, 1, 1), 0.0, 3000),
+                   ("decode_gqa", 2, 16, 4, (512, 1499), (1, 1), 0.01, 4000),
+                   ("prefill", 2, 8, 2, (100, 250), (40, 25), 0.0, 5000)]
+
+
+def attention_kv(case: tuple, b: int, h: int) -> tuple[np.ndarray, np.ndarray]:
+    """K and V rows [keys][128] of sequence b, kv head h: its cached keys and its query rows' own keys."""
+    name, B, hq, hkv, cached, rows, outl, seed = case
+    n = cached[b] + rows[b]
+    base = seed + 100 * b + 10 * h
+    return fp8_exact_rows(n, base, outl), fp8_exact_rows(n, base + 5, outl)
+
+
+def attention_q(case: tuple, b: int) -> np.ndarray:
+    """Query rows [rows][hq][128] of sequence b."""
+    name, B, hq, hkv, cached, rows, outl, seed = case
+    return hashed_bf16((rows[b], hq, 128), seed + 100 * b + 99)
+
+
 def fixture_ids() -> np.ndarray:
     return np.random.default_rng(IDS_SEED).integers(0, MODEL["vocab"], (SEQS, SEQ_LEN)).astype(np.int64)
 
@@ -164,6 +220,28 @@ def model_vectors(ref) -> dict:
             "cached_from": np.array(PREFILL - 1), "config_json": np.array(json.dumps(cfg_json))}
 
 
+def attention_vectors(ref) -> dict:
+    out = {}
+    for case in ATTENTION_CASES:
+        name, B, hq, hkv, cached, rows, outl, seed = case
+        G = hq // hkv
+        res = []
+        for b in range(B):
+            kv = [attention_kv(case, b, h) for h in range(hkv)]
+            k = torch.tensor(np.stack([kv[hh // G][0] for hh in range(hq)]), dtype=torch.bfloat16)[None]
+            v = torch.tensor(np.stack([kv[hh // G][1] for hh in range(hq)]), dtype=torch.bfloat16)[None]
+            q = torch.tensor(attention_q(case, b), dtype=torch.bfloat16).transpose(0, 1)[None]  # [1][hq][rows][128]
+            n = cached[b] + rows[b]
+            pos = cached[b] + torch.arange(rows[b])
+            allowed = torch.arange(n)[None, :] <= pos[:, None]
+            mask = torch.zeros((rows[b], n), dtype=torch.bfloat16).masked_fill(~allowed,
+                                                                               torch.finfo(torch.bfloat16).min)
+            o, _ = ref.eager_attention_forward(None, q, k, v, mask[None, None], scaling=128 ** -0.5)
+            res.append(o[0].view(torch.int16).numpy().view(np.uint16))  # [rows][hq][128]
+        out[f"{name}_out_bits"] = np.concatenate(res)
+    return out
+
+
 def main() -> None:
     import transformers
 
@@ -174,7 +252,9 @@ def main() -> None:
     np.savez_compressed(os.path.join(HERE, "reference_qk_norm_rope.npz"), meta=np.array(json.dumps(meta)), **qk)
     mv = model_vectors(ref)
     np.savez_compressed(os.path.join(HERE, "reference_model_small.npz"), meta=np.array(json.dumps(meta)), **mv)
-    print("wrote reference_qk_norm_rope.npz and reference_model_small.npz", meta)
+    av = attention_vectors(ref)
+    np.savez_compressed(os.path.join(HERE, "reference_attention.npz"), meta=np.array(json.dumps(meta)), **av)
+    print("wrote reference_qk_norm_rope.npz, reference_model_small.npz and reference_attention.npz", meta)
 
 
 if __name__ == "__main__":

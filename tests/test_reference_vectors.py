@@ -133,3 +133,81 @@ def test_reference_vectors_catch_structural_slips(slip):
     mx, mean = _cpu_vs_reference(slip)
     print(f"{slip.__name__} vs reference: max {mx:.4f}, mean {mean:.4f} of the logits' spread")
     assert mx > CPU_MAX or mean > CPU_MEAN, f"{slip.__name__} passed the comparison: not pinned"
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# attention: the reference's eager_attention_forward (bf16 scores, probabilities cast to bf16) over K / V rows that
+# are exactly the same numbers in its bf16 cache and in the fp8 cache (e4m3 code x 2^e, absmax 448 x 2^e)
+# ---------------------------------------------------------------------------------------------------------------
+
+ATTN = np.load(os.path.join(HERE, "reference_attention.npz"))
+# The reference's own distance from the exact (fp64) result on these vectors, which its bf16 scores, bf16
+# probabilities and bf16 output rounding set: decode MHA max 0.021 / mean 0.0019, decode GQA with 1 % outliers
+# (outputs up to 12) max 0.113 / mean 0.0039, the causal prefill chunk (outputs up to 11) max 0.094 / mean 0.0024.
+# The oracle (fp64) is held to about 1.5x those; a planted slip moves it by far more.
+REF_ATTN_BOUND = {"decode_mha": (0.035, 0.003), "decode_gqa": (0.17, 0.006), "prefill": (0.15, 0.004)}
+
+
+def attention_case(name: str) -> tuple:
+    return next(c for c in _maker().ATTENTION_CASES if c[0] == name)
+
+
+def attention_inputs(case: tuple):
+    """The case's K / V rows per (sequence, kv head), its q rows (bf16 bits [n][hq][128]), positions and sequences
+    (int32 [n])."""
+    mk = _maker()
+    name, B, hq, hkv, cached, rows, outl, seed = case
+    kv = {(b, h): mk.attention_kv(case, b, h) for b in range(B) for h in range(hkv)}
+    q = np.concatenate([G.bf16_bits(mk.attention_q(case, b)) for b in range(B)])
+    pos = np.concatenate([c + np.arange(r) for c, r in zip(cached, rows)]).astype(np.int32)
+    seq = np.concatenate([np.full(r, b) for b, r in enumerate(rows)]).astype(np.int32)
+    return kv, q, pos, seq
+
+
+def oracle_attention(case: tuple, pos_shift: int = 0, head_of=None, scale: float = 128 ** -0.5) -> np.ndarray:
+    """oracle.golden.rows_attention over the case's cache (K / V through the oracle's quantiser, exact here), fp64
+    [n][hq][128]; pos_shift, head_of and scale plant slips (keys up to p + pos_shift, kv head head_of(h))."""
+    name, B, hq, hkv, cached, rows, outl, seed = case
+    kv, q, pos, seq = attention_inputs(case)
+    maxb = max(-(-(c + r + 1) // G.PAGE) for c, r in zip(cached, rows))
+    cache = G.PagedCache(B * maxb, hkv)
+    for (b, h), (k, v) in kv.items():
+        kc, ks = G.quantize_rows(G.bf16_bits(k))
+        vc, vs = G.quantize_rows(G.bf16_bits(v))
+        assert np.array_equal(G.dequantize(kc, ks), k) and np.array_equal(G.dequantize(vc, vs), v)
+        t = np.arange(len(k))
+        cache.write(G.PagedCache.block_of(np.full(len(t), b), t, None, maxb), h, t % G.PAGE, kc, ks, vc, vs)
+    if head_of is None:
+        return G.rows_attention(q, pos + pos_shift, seq, cache, None, maxb, B, -1, hq, hkv, scale)
+    out = np.zeros((len(pos), hq, 128))
+    for h in range(hq):  # each query head alone against kv head head_of(h), copied into a one-head cache
+        one = G.PagedCache(cache.num_blocks, 1)
+        one.pages[:, 0] = cache.pages[:, head_of(h)]
+        out[:, h:h + 1] = G.rows_attention(q[:, h:h + 1], pos + pos_shift, seq, one, None, maxb, B, -1, 1, 1, scale)
+    return out
+
+
+def reference_attention(name: str) -> np.ndarray:
+    return G.bf16_to_f32(ATTN[f"{name}_out_bits"]).astype(np.float64)
+
+
+@pytest.mark.parametrize("name", ["decode_mha", "decode_gqa", "prefill"])
+def test_oracle_attention_matches_the_reference(name):
+    d = np.abs(oracle_attention(attention_case(name)) - reference_attention(name))
+    print(f"{name}: oracle vs reference max {d.max():.4f} mean {d.mean():.5f}")
+    mx, mean = REF_ATTN_BOUND[name]
+    assert d.max() <= mx and d.mean() <= mean, (d.max(), d.mean())
+
+
+@pytest.mark.parametrize("slip", ["own key dropped", "one key too many", "kv head h % hkv", "no 1/sqrt(128)"])
+def test_reference_attention_catches_slips(slip):
+    case = attention_case("decode_gqa" if "kv head" in slip else "prefill")
+    G_ = case[2] // case[3]
+    kw = {"own key dropped": dict(pos_shift=-1), "one key too many": dict(pos_shift=1),
+          "kv head h % hkv": dict(head_of=lambda h: h % case[3]), "no 1/sqrt(128)": dict(scale=1.0)}[slip]
+    if "kv head" in slip:
+        assert G_ > 1
+    d = np.abs(oracle_attention(case, **kw) - reference_attention(case[0]))
+    mx, mean = REF_ATTN_BOUND[case[0]]
+    print(f"{slip}: max {d.max():.4f} mean {d.mean():.5f}")
+    assert d.max() > mx or d.mean() > mean, f"{slip} passed the comparison: not pinned"
