@@ -211,3 +211,21 @@ def test_reference_attention_catches_slips(slip):
     mx, mean = REF_ATTN_BOUND[case[0]]
     print(f"{slip}: max {d.max():.4f} mean {d.mean():.5f}")
     assert d.max() > mx or d.mean() > mean, f"{slip} passed the comparison: not pinned"
+
+
+@pytest.mark.parametrize("theta", ["10000", "1000000"])
+def test_reference_rows_quantise_as_torch_does(theta):
+    """The fp8 scheme (per-row absmax scale, e4m3) on the reference's own QK-norm + RoPE output rows:
+    the oracle's quantize_rows against the same scheme written in torch (absmax / 448 in fp32, x / scale cast by
+    torch to float8_e4m3fn), codes and scales bit for bit (the GPU append equals the oracle's bytes)."""
+    import torch
+
+    y_bits = QK[f"y_bits_{theta}"]
+    codes, scale = G.quantize_rows(y_bits)
+    x = torch.from_numpy(y_bits.view(np.int16)).view(torch.bfloat16).float()
+    s = x.abs().amax(-1) / 448.0
+    safe = torch.where(s == 0, torch.ones_like(s), s)
+    c = (x / safe[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    c = torch.where((s == 0)[:, None], torch.zeros_like(c), c)
+    np.testing.assert_array_equal(scale, s.numpy())
+    np.testing.assert_array_equal(codes, c.numpy())
