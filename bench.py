@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 2 decode, config 4 prefill and config 5 end-to-end lines")
-    ap.add_argument("--only", choices=["decode1", "decode2", "prefill4", "e2e5", "handle5", "gemm5"],
+    ap.add_argument("--only", choices=["decode1", "decode2", "prefill4", "e2e5", "handle5", "gemm5", "sweep"],
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--e2e-steps", type=int, default=None, help="decode steps of the config 5 run (default 512)")
     ap.add_argument("--unfused", action="store_true",
@@ -264,6 +264,66 @@ def extra_decode_cfg2(dev, stream, cpu_s: float | None = None) -> dict:
     if cpu_s:
         res["cpu_baseline"] = cpu_decode(case, case.ctx + 1, qs[0], cpu_s, gbs)
     return res
+
+
+# Shapes of the decode sweep beside the five configs: (name, batch, query heads, kv heads, prior context, paged)
+SWEEP_SHAPES = [("b1-16/4-ctx131072", 1, 16, 4, 131072, True),
+                ("b8-16/4-ctx32768", 8, 16, 4, 32768, True),
+                ("b64-16/4-ctx8192", 64, 16, 4, 8192, True),
+                ("b256-8/8-ctx2048", 256, 8, 8, 2048, False),
+                ("b128-13/13-ctx2304", 128, 13, 13, 2304, False),
+                ("b32-32/8-ctx4096", 32, 32, 8, 4096, True),
+                ("b16-64/4-ctx8192", 16, 64, 4, 8192, True)]
+
+
+def extra_decode_sweep(dev, stream) -> list:
+    """The decode path beyond the benchmark configs: for each of SWEEP_SHAPES (uniform contexts, N(0, 1) values),
+    POOLS pools read cold in turn: the attention call alone (nc_decode_attn_fp8), the fused step
+    (nc_decode_step_fp8, positions fixed so every call appends the same bytes) and the fused step with the
+    batch-independent piece plan (16-page pieces), each as ATTN_REPS calls per graph replay."""
+    import torch
+
+    from nanochat_amd.attention import decode_attention, decode_step, decode_workspace
+    from nanochat_amd.workloads import DecodeConfig, build_decode_case, decode_bytes
+
+    rows = []
+    for name, B, hq, hkv, ctx, paged in SWEEP_SHAPES:
+        cfg = DecodeConfig(name, B, hq, hkv, ctx=(ctx,), paged=paged, seed=11)
+        cases = [build_decode_case(cfg, dev, steps=1) for _ in range(POOLS)]
+        case = cases[0]
+        max_ctx = case.cache.capacity
+        pos = case.positions(0)
+        nxt = torch.empty_like(pos)
+        qs = [c.cache.append(c.qkv[0], pos, c.seq, c.q_gain, c.k_gain, c.cos, c.sin, hq) for c in cases]
+        ctx_len = pos + 1
+        qkv = case.qkv[0].contiguous()
+        ws = decode_workspace(B, hq, hkv, max_ctx, dev)
+        out = torch_empty_like(qs[0])
+        turn = [0]
+
+        def attn():
+            k = turn[0] % POOLS
+            turn[0] += 1
+            decode_attention(qs[k], cases[k].cache, ctx_len, max_ctx=max_ctx, out=out, workspace=ws)
+
+        def step(pieces=0):
+            k = turn[0] % POOLS
+            turn[0] += 1
+            c = cases[k]
+            decode_step(qkv, c.cache, pos, c.q_gain, c.k_gain, c.cos, c.sin, hq, max_ctx=max_ctx, out=out,
+                        workspace=ws, pos_out=nxt, piece_pages=pieces)
+
+        nbytes = decode_bytes(case.ctx + 1, hkv)
+        row = {"shape": name, "batch": B, "hq": hq, "hkv": hkv, "ctx": ctx + 1, "paged": paged, "bytes": int(nbytes)}
+        for leg, fn in (("attn", attn), ("step", step), ("step_pieces", lambda: step(16))):
+            ms = time_calls(fn, ATTN_REPS, 20, stream)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            row[leg] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+        del cases, case, qs, ws, out, qkv
+        torch.cuda.empty_cache()
+    return rows
 
 
 def extra_decode_cfg1(dev, stream, cpu_s: float | None = None) -> dict:
@@ -677,7 +737,7 @@ def main():
                "prefill4": lambda: extra_prefill_cfg4(dev, s, cpu_s),
                "e2e5": lambda: extra_e2e_cfg5(dev, args.e2e_steps, cpu_s),
                "handle5": lambda: extra_e2e_cfg5_handle(dev, args.e2e_steps),
-               "gemm5": lambda: extra_gemm_cfg5(dev, s)}[args.only]
+               "gemm5": lambda: extra_gemm_cfg5(dev, s), "sweep": lambda: extra_decode_sweep(dev, s)}[args.only]
         print(json.dumps(run()), flush=True)
         return
     cfg = CONFIG3

@@ -126,13 +126,15 @@ int nc_decode_step_fp8(const void *qkv, long long row_stride, const int32_t *pos
                        long long workspace_bytes, void *stream);
 
 /* nc_decode_step_fp8 with the sequence-local piece plan: every (sequence, kv head) segment of n pages (its keys'
- * pages) is cut into fixed pieces of max(piece_pages, ceil(n / 32)) pages from its first page, each piece's
- * softmax starts afresh, and the pieces merge in a fixed order set by the piece count; a wave takes whole pieces
- * (the balanced split's slice ends rounded to the nearest piece boundary). A sequence's output bits are then a
- * function of its own query, context and cache alone: decoded alone or in any batch, it gets the same bits, as
- * with the reference's one block per (head, slot). Arguments as nc_decode_step_fp8, plus piece_pages in
- * [1, 65536]; 16 measured fastest. The plain entry point's balanced split is 3 % faster on a config-5 layer and
- * 11 % on config 3's ragged batch, but its bits depend on the batch.
+ * pages) is cut into fixed pieces of max(piece_pages, ceil(n / P)) pages from its first page, P = the pieces
+ * that cut the longest segment max_ctx admits into 16-page pieces (at least 32, at most 256), each piece's softmax
+ * starts afresh, and the pieces merge in a fixed order set by the piece count; a wave takes whole pieces (the
+ * balanced split's slice ends rounded to the nearest piece boundary). A sequence's output bits are then a function
+ * of its own query, context and cache (and, for piece_pages below 16, of max_ctx) alone: decoded alone or in any
+ * batch, it gets the same bits, as with the reference's one block per (head, slot). Arguments as
+ * nc_decode_step_fp8, plus piece_pages in [1, 65536]; 16 measured fastest, and with 16 a segment's pieces are
+ * max(16, ceil(n / 256)) pages whatever max_ctx is. The plain entry point's balanced split is 3 % faster on a
+ * config-5 layer and 11 % on config 3's ragged batch, but its bits depend on the batch.
  * Replaces: k_prologue's append and k_attn (model/kernels/decode.cu:550-675), whose tokens depend on neither the
  * batch nor the store (inference/decoder.py:124-125); the decoder handle (dec_*) runs this entry point. */
 int nc_decode_step_fp8_pieces(const void *qkv, long long row_stride, const int32_t *pos, int32_t *pos_out,

@@ -59,7 +59,8 @@
 #define DEC_MAX_G 16
 #define DEC_MAX_WAVES 8192  /* workspace slots are sized for this many waves */
 #define DEC_MERGE_DIRECT 8  /* pieces of a segment k_merge reads in its first round trip */
-#define DEC_PIECES_MAX 32   /* fixed pieces of a segment at most */
+#define DEC_PIECES_MIN 32   /* fixed pieces of a segment at most: this many ... */
+#define DEC_PIECES_MAX 256  /* ... or, for longer contexts, enough for 16-page pieces, up to this many */
 #define DEC_MIN_CHUNK 8     /* pages per wave at least: fewer pieces to merge on small problems */
 #define DEC_LAZY 8.0f       /* log2 headroom before the softmax reference moves */
 #define DEC_M_INIT -3.0e38f /* finite "no score yet": exp2(m - m') = 0, never NaN */
@@ -108,6 +109,7 @@ struct DecodeArgs {
     int max_ctx;              /* ctx_len is clamped to it */
     int unit_start, unit_end; /* schedule units a non-empty segment costs before its first and after its last page */
     int piece_pages;          /* 0: pieces cut by the balanced split; > 0: fixed pieces (piece_len) */
+    int piece_slots;          /* fixed pieces: the most pieces of a segment (piece_slots_for), its slots apart */
     int merge_groups;         /* k_merge's groups of 16 G lanes per segment */
 };
 
@@ -155,11 +157,11 @@ __device__ __forceinline__ int units_of(const DecodeArgs &a, int ctx) {
     return pg > 0 ? pg + a.unit_start + a.unit_end : 0;
 }
 
-/* Fixed pieces: a segment of `pages` pages is cut into pieces of max(piece_pages, ceil(pages / DEC_PIECES_MAX))
- * pages from its first page on (at most DEC_PIECES_MAX pieces, each with its own workspace slot). A function of
- * the segment's own length only: its output bits do not depend on the batch. */
+/* Fixed pieces: a segment of `pages` pages is cut into pieces of max(piece_pages, ceil(pages / piece_slots)) pages
+ * from its first page on (at most piece_slots pieces, each with its own workspace slot). A function of the segment's
+ * own length and of max_ctx (piece_slots_for) only: its output bits do not depend on the batch. */
 __device__ __forceinline__ int piece_len(const DecodeArgs &a, int pages) {
-    return max(a.piece_pages, (pages + DEC_PIECES_MAX - 1) / DEC_PIECES_MAX);
+    return max(a.piece_pages, (pages + a.piece_slots - 1) / a.piece_slots);
 }
 
 /* A k_decode wave's context lengths: seq_ctx of every sequence, in LDS when the batch fits (read from memory once
@@ -613,13 +615,13 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
     }
 }
 
-/* The workspace slot of piece i of segment s, made by wave w. Fixed pieces: s * DEC_PIECES_MAX + i. Pieces cut
+/* The workspace slot of piece i of segment s, made by wave w. Fixed pieces: s * piece_slots + i. Pieces cut
  * by the balanced split (piece i is the i-th wave to touch the segment): the first DEC_MERGE_DIRECT sit together
  * at s * DEC_MERGE_DIRECT + i; later ones at S * DEC_MERGE_DIRECT + w + s (unique: a wave's pieces lie in
  * consecutive segments and the waves' slices are in segment order, so w + s never repeats). */
 __device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, int w) {
     const int S = a.B * a.hkv;
-    if (a.piece_pages > 0) return (size_t)s * DEC_PIECES_MAX + i;
+    if (a.piece_pages > 0) return (size_t)s * a.piece_slots + i;
     return i < DEC_MERGE_DIRECT ? (size_t)s * DEC_MERGE_DIRECT + i : (size_t)S * DEC_MERGE_DIRECT + w + s;
 }
 
@@ -841,16 +843,19 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 
 /* One workgroup per segment s = (b, h) = blockIdx.x combines the pieces of a segment that more than one wave
  * touched, weights exp2(m_k - max m) as decode.cu:547-548's rescale. A thread holds head n, dims 8 c..8 c + 8 (16
- * lanes per head) of one of Q = merge_groups groups (at most min(4, 256 / (16 G))). Group q folds, in order, pieces
- * 8 q..8 q + 7, then 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed
- * order for a given piece count and head group, so the bits depend on nothing else (with fixed pieces Q only drops
- * groups that no segment reaches at max_ctx, which leaves the order as it is). The kernel is latency-bound: the
- * first round's slots do not depend on the segment's descriptor (fixed pieces: s * DEC_PIECES_MAX + i; the balanced
- * split's first DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, unconditionally (a
- * predicate per slot puts each load behind a branch and a wait), one round trip for up to 8 Q fixed pieces (8 for
- * the balanced split, every segment of config 3). */
+ * lanes per head) of one of Q = merge_groups groups of 16 G lanes. Group q folds, in order, pieces 8 q..8 q + 7,
+ * then 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a
+ * given piece count, head group and Q, so the bits depend on nothing else. The balanced split launches
+ * min(MERGE_GROUPS, 256 / (16 G)) groups; fixed pieces launch as many as the longest segment at max_ctx fills
+ * (ceil(pieces / 8), at most 1024 / (16 G)), so every segment of at most 8 Q pieces folds in one round whatever Q
+ * is, and Q depends on max_ctx alone, not on the batch. The kernel is latency-bound: the first round's slots do not
+ * depend on the segment's descriptor (fixed pieces: s * piece_slots + i; the balanced split's first
+ * DEC_MERGE_DIRECT: s * DEC_MERGE_DIRECT + i), so they load together with it, unconditionally (a predicate per slot
+ * puts each load behind a branch and a wait), one round trip for up to 8 Q fixed pieces (8 for the balanced split,
+ * every segment of config 3). THREADS: 256, or 1024 where the groups need more lanes. */
 #define MERGE_LANES 16
-#define MERGE_THREADS 256 /* at most: Q = min(4, 16 / G) groups of 16 G lanes (64 threads at G = 1) */
+#define MERGE_THREADS 256      /* the workgroup of the balanced split and of fixed pieces that fit */
+#define MERGE_THREADS_MAX 1024 /* fixed pieces of long contexts: up to 1024 / (16 G) groups */
 #define MERGE_GROUPS 4
 
 struct MergeAcc {
@@ -892,22 +897,23 @@ __device__ __forceinline__ void merge_round(const DecodeArgs &a, int s, int2 d, 
     }
 }
 
-__global__ void __launch_bounds__(MERGE_THREADS) k_merge(DecodeArgs a) {
-    __shared__ MergeAcc grp[MERGE_THREADS];
+template <int THREADS>
+__global__ void __launch_bounds__(THREADS) k_merge(DecodeArgs a) {
+    __shared__ MergeAcc grp[THREADS];
     const int s = blockIdx.x, b = s / a.hkv, h = s % a.hkv, t = threadIdx.x, G = a.group;
     const int row = G * MERGE_LANES, Q = a.merge_groups, q = t / row, n = (t % row) / MERGE_LANES,
               c = t % MERGE_LANES;
     const int2 d = a.ws_desc[s];
     /* the first round's slots, loaded with the descriptor: slot(i) needs no d where spec holds */
     const bool fixed = a.piece_pages > 0;
-    const bool spec = q < Q && (fixed ? DEC_MERGE_DIRECT * (q + 1) <= DEC_PIECES_MAX : q == 0);
+    const bool spec = q < Q && (fixed ? DEC_MERGE_DIRECT * (q + 1) <= a.piece_slots : q == 0);
     f32x2 ml[DEC_MERGE_DIRECT];
     f32x4 ov[DEC_MERGE_DIRECT][2];
     if (spec) {
 #pragma unroll
         for (int k = 0; k < DEC_MERGE_DIRECT; k++) {
             const int i = DEC_MERGE_DIRECT * q + k;
-            const size_t slot = ((size_t)s * (fixed ? DEC_PIECES_MAX : DEC_MERGE_DIRECT) + i) * G + n;
+            const size_t slot = ((size_t)s * (fixed ? a.piece_slots : DEC_MERGE_DIRECT) + i) * G + n;
             ml[k] = *reinterpret_cast<const f32x2 *>(a.ws_ml + 2 * slot);
             const f32x4 *src = reinterpret_cast<const f32x4 *>(a.ws_o + slot * NC_HEAD_DIM + 8 * c);
             ov[k][0] = src[0];
@@ -978,18 +984,31 @@ static int decode_waves() {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+/* The most fixed pieces of a segment for contexts up to max_ctx: DEC_PIECES_MIN, or enough to cut the longest
+ * segment (ceil(max_ctx / 16) pages) into 16-page pieces, at most DEC_PIECES_MAX. A function of max_ctx alone, so
+ * a sequence's pieces do not depend on the batch; from 8192 keys on, long segments get more, shorter pieces (and
+ * so more waves) instead of 32 long ones. */
+static int piece_slots_for(int max_ctx) {
+    const long long pages = ((long long)max_ctx + NC_PAGE - 1) / NC_PAGE;
+    return (int)std::min<long long>(DEC_PIECES_MAX, std::max<long long>(DEC_PIECES_MIN, (pages + 15) / 16));
+}
+
 /* Partial-result slots: for the balanced split the first DEC_MERGE_DIRECT pieces of every segment, then one per
- * (wave, segment) offset; for fixed pieces DEC_PIECES_MAX per segment. */
-static size_t merge_slots(size_t S) {
-    const size_t balanced = S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S, fixed = S * DEC_PIECES_MAX;
-    return balanced > fixed ? balanced : fixed;
+ * (wave, segment) offset; for fixed pieces piece_slots_for(max_ctx) per segment. */
+static size_t balanced_slots(size_t S) { return S * DEC_MERGE_DIRECT + DEC_MAX_WAVES + S; }
+static size_t merge_slots(size_t S, int max_ctx, bool fixed) {
+    return fixed ? S * (size_t)piece_slots_for(max_ctx) : balanced_slots(S);
+}
+static long long workspace_bytes(size_t S, size_t G, size_t slots) {
+    return (long long)(align256(slots * G * NC_HEAD_DIM * sizeof(float)) + align256(slots * G * 2 * sizeof(float)) +
+                       S * sizeof(int2));
 }
 
 extern "C" long long nc_decode_workspace_bytes(int B, int hq, int hkv, int max_ctx) {
     if (B <= 0 || hq <= 0 || hkv <= 0 || max_ctx <= 0 || hq % hkv) return 0;
-    const size_t S = (size_t)B * hkv, G = hq / hkv, slots = merge_slots(S);
-    return (long long)(align256(slots * G * NC_HEAD_DIM * sizeof(float)) + align256(slots * G * 2 * sizeof(float)) +
-                       S * sizeof(int2));
+    const size_t S = (size_t)B * hkv, G = hq / hkv;
+    return std::max(workspace_bytes(S, G, merge_slots(S, max_ctx, false)),
+                    workspace_bytes(S, G, merge_slots(S, max_ctx, true)));
 }
 
 /* Checks shared by both entry points, then the launch of k_decode<FUSED, TABLE>. */
@@ -1007,7 +1026,9 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     NC_REQUIRE(a.cache && a.ctx_len && out && workspace, "null argument");
     NC_REQUIRE(((uintptr_t)out | (uintptr_t)a.cache | (uintptr_t)workspace) % 16 == 0,
                "tensors must be 16-byte aligned");
-    const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
+    const bool fixed = a.piece_pages > 0;
+    const size_t S = (size_t)B * hkv, slots = merge_slots(S, max_ctx, fixed);
+    const long long need = ::workspace_bytes(S, (size_t)(hq / hkv), slots);
     NC_REQUIRE(workspace_bytes >= need, "workspace %lld bytes, %lld needed", workspace_bytes, need);
     /* the kernel's schedule counts units in 32 bits: every segment's pages plus its start and end units */
     NC_REQUIRE((long long)B * hkv * ((long long)a.max_blocks + DEC_UNITS_START + DEC_UNITS_END) < (1ll << 31),
@@ -1016,7 +1037,7 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     a.score_scale = sm_scale * 1.4426950408889634f;
     a.out = (bf16_t *)out;
     a.max_ctx = max_ctx;
-    const size_t S = (size_t)B * hkv, slots = merge_slots(S);
+    a.piece_slots = piece_slots_for(max_ctx);
     unsigned char *ws = (unsigned char *)workspace;
     a.ws_o = (float *)ws;
     ws += align256(slots * a.group * NC_HEAD_DIM * sizeof(float));
@@ -1033,20 +1054,21 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else if (a.block_table) hipLaunchKernelGGL((k_decode<false, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
-    /* the groups: as many as fit in MERGE_THREADS, at most MERGE_GROUPS (enough for DEC_PIECES_MAX pieces in one
-     * round trip at G <= 4); fewer waves per segment for the small head groups of many segments. Fixed pieces: no
-     * more groups than the pieces of the longest segment at max_ctx need (ceil(max_ctx / 16) pages at most) */
+    /* the groups. The balanced split: as many as fit in MERGE_THREADS, at most MERGE_GROUPS (fewer waves per segment
+     * for the small head groups of many segments). Fixed pieces: as many as the pieces of the longest segment at
+     * max_ctx fill (ceil(max_ctx / 16) pages at most), up to MERGE_THREADS_MAX lanes, so that a segment of up to
+     * 8 Q pieces folds in one round trip; 1024-lane workgroups only where 256 lanes cannot hold them. */
     const int row = a.group * MERGE_LANES;
     int groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
-    if (a.piece_pages > 0) {
+    if (fixed) {
         const long long pages = ((long long)max_ctx + NC_PAGE - 1) / NC_PAGE;
-        const int most = pages <= (long long)DEC_PIECES_MAX * a.piece_pages
-                             ? (int)((pages + a.piece_pages - 1) / a.piece_pages) : DEC_PIECES_MAX;
-        groups = std::min(groups, (most + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT);
+        const int most = (int)std::min<long long>(a.piece_slots, (pages + a.piece_pages - 1) / a.piece_pages);
+        groups = std::max(1, std::min((most + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT, MERGE_THREADS_MAX / row));
     }
     a.merge_groups = groups;
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)S), dim3((unsigned)(groups * row + NC_WAVE - 1) / NC_WAVE * NC_WAVE), 0,
-                       st, a);
+    const int threads = (groups * row + NC_WAVE - 1) / NC_WAVE * NC_WAVE;
+    if (threads <= MERGE_THREADS) hipLaunchKernelGGL(k_merge<MERGE_THREADS>, dim3((unsigned)S), dim3(threads), 0, st, a);
+    else hipLaunchKernelGGL(k_merge<MERGE_THREADS_MAX>, dim3((unsigned)S), dim3(threads), 0, st, a);
     NC_LAUNCH_CHECK();
     return 0;
 }
@@ -1131,7 +1153,10 @@ extern "C" int nc_decode_step_fp8_noalloc(const void *qkv, long long row_stride,
                                           const int32_t *block_table, int max_blocks, int num_blocks, int window,
                                           int B, int hq, int hkv, int max_ctx, float sm_scale, void *out,
                                           void *stream) {
-    const long long need = nc_decode_workspace_bytes(B, hq, hkv, max_ctx);
+    /* the balanced split's partial results (this entry does not take fixed pieces) */
+    const long long need = B > 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && max_ctx > 0
+                               ? workspace_bytes((size_t)B * hkv, (size_t)(hq / hkv), balanced_slots((size_t)B * hkv))
+                               : 0;
     NC_REQUIRE(need <= NC_DECODE_SCRATCH_BYTES,
                "%d sequences of %d / %d heads need %lld bytes of partial results, the static scratch holds %lld", B,
                hq, hkv, need, NC_DECODE_SCRATCH_BYTES);

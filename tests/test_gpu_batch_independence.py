@@ -34,8 +34,12 @@ PIECES = 16
 KERNEL_CASES = [
     DecodeConfig("gqa-paged-ragged-64", 64, 16, 4, ctx_range=(1, 3000), paged=True, outliers=0.01, seed=301),
     DecodeConfig("mha-contiguous-window-64", 64, 8, 8, ctx_range=(1, 2500), window=700, seed=302),
-    # segments of 1875 and 563 pages: the 32-piece cap (pieces of 59 and 18 pages), every merge group busy, G = 5
-    DecodeConfig("long-segments-32-pieces-g5", 3, 5, 1, ctx=(30000, 9000, 700), paged=True, seed=304),
+    # segments of 1875 and 563 pages: 118 and 36 pieces of 16 pages (the cap follows max_ctx), 12 merge groups in
+    # 1024-lane workgroups folding the long segment in two rounds, G = 5
+    DecodeConfig("long-segments-g5", 3, 5, 1, ctx=(30000, 9000, 700), paged=True, seed=304),
+    # one sequence of 131072 keys beside a short one: 256 pieces of 32 pages per segment, so its 4 segments still
+    # occupy every wave
+    DecodeConfig("long-context-b2", 2, 16, 4, ctx=(131072, 500), paged=True, seed=307),
     # more sequences than the schedule keeps in LDS: context lengths read from memory by every segment walk
     DecodeConfig("batch-past-lds-2100", 2100, 4, 2, ctx_range=(0, 200), seed=305),
 ]
