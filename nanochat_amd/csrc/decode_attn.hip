@@ -846,7 +846,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
  * lanes per head) of one of Q = merge_groups groups of 16 G lanes. Group q folds, in order, pieces 8 q..8 q + 7,
  * then 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a
  * given piece count, head group and Q, so the bits depend on nothing else. The balanced split launches
- * min(MERGE_GROUPS, 256 / (16 G)) groups; fixed pieces launch as many as the longest segment at max_ctx fills
+ * min(MERGE_GROUPS, 256 / (16 G)) groups, and past DEC_LONG_CTX as many as its longest possible segment fills (up to
+ * 1024 / (16 G)); fixed pieces launch as many as the longest segment at max_ctx fills
  * (ceil(pieces / 8), at most 1024 / (16 G)), so every segment of at most 8 Q pieces folds in one round whatever Q
  * is, and Q depends on max_ctx alone, not on the batch. The kernel is latency-bound: the first round's slots do not
  * depend on the segment's descriptor (fixed pieces: s * piece_slots + i; the balanced split's first
@@ -857,6 +858,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 #define MERGE_THREADS 256      /* the workgroup of the balanced split and of fixed pieces that fit */
 #define MERGE_THREADS_MAX 1024 /* fixed pieces of long contexts: up to 1024 / (16 G) groups */
 #define MERGE_GROUPS 4
+#define DEC_LONG_CTX 16384     /* the balanced split's merge takes more groups from this max_ctx on */
 
 struct MergeAcc {
     float m, l, o[8];
@@ -1060,6 +1062,14 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
      * 8 Q pieces folds in one round trip; 1024-lane workgroups only where 256 lanes cannot hold them. */
     const int row = a.group * MERGE_LANES;
     int groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
+    if (!fixed && max_ctx > DEC_LONG_CTX) {
+        /* long contexts: a segment can span up to ceil(pages / DEC_MIN_CHUNK) + 1 waves, so as many groups as that
+         * fills (fewer dependent rounds for one long sequence); shorter contexts keep the groups above */
+        const long long pages = ((long long)max_ctx + NC_PAGE - 1) / NC_PAGE;
+        const long long most = (pages + DEC_MIN_CHUNK - 1) / DEC_MIN_CHUNK + 1;
+        groups = (int)std::max<long long>(groups, std::min<long long>((most + DEC_MERGE_DIRECT - 1) / DEC_MERGE_DIRECT,
+                                                                      MERGE_THREADS_MAX / row));
+    }
     if (fixed) {
         const long long pages = ((long long)max_ctx + NC_PAGE - 1) / NC_PAGE;
         const int most = (int)std::min<long long>(a.piece_slots, (pages + a.piece_pages - 1) / a.piece_pages);
