@@ -169,6 +169,8 @@ def pmc_summary(dirs: list[str], kernels: list[str], last: int) -> dict:
                 for r in csv.DictReader(fh):
                     name = r["Kernel_Name"].split("(")[0]
                     name = name[5:] if name.startswith("void ") else name
+                    if name not in kernels and name.split("<")[0] in kernels:  # a template named by its base name
+                        name = name.split("<")[0]
                     if name not in kernels:
                         name = "copy_probe" if "neg" in r["Kernel_Name"] else None
                     if name:
