@@ -846,7 +846,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
  * lanes per head) of one of Q = merge_groups groups of 16 G lanes. Group q folds, in order, pieces 8 q..8 q + 7,
  * then 8 (q + Q)..8 (q + Q) + 7, and so on; group 0 then folds the groups' results in order: a fixed order for a
  * given piece count, head group and Q, so the bits depend on nothing else. The balanced split launches
- * min(MERGE_GROUPS, 256 / (16 G)) groups, and past DEC_LONG_CTX as many as its longest possible segment fills (up to
+ * MERGE_GROUPS groups, and past DEC_LONG_CTX as many as its longest possible segment fills (up to
  * 1024 / (16 G)); fixed pieces launch as many as the longest segment at max_ctx fills
  * (ceil(pieces / 8), at most 1024 / (16 G)), so every segment of at most 8 Q pieces folds in one round whatever Q
  * is, and Q depends on max_ctx alone, not on the batch. The kernel is latency-bound: the first round's slots do not
@@ -1056,12 +1056,13 @@ static int decode_launch(DecodeArgs &a, bool fused, const void *out, const void 
     else if (a.block_table) hipLaunchKernelGGL((k_decode<false, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((k_decode<false, false>), grid, block, 0, st, a);
     NC_LAUNCH_CHECK();
-    /* the groups. The balanced split: as many as fit in MERGE_THREADS, at most MERGE_GROUPS (fewer waves per segment
-     * for the small head groups of many segments). Fixed pieces: as many as the pieces of the longest segment at
-     * max_ctx fill (ceil(max_ctx / 16) pages at most), up to MERGE_THREADS_MAX lanes, so that a segment of up to
-     * 8 Q pieces folds in one round trip; 1024-lane workgroups only where 256 lanes cannot hold them. */
+    /* the groups. The balanced split: MERGE_GROUPS (in 1024-lane workgroups for head groups of 5 or more, where 256
+     * lanes hold fewer), and past DEC_LONG_CTX as many as its longest possible segment fills. Fixed pieces: as many
+     * as the pieces of the longest segment at max_ctx fill (ceil(max_ctx / 16) pages at most), up to
+     * MERGE_THREADS_MAX lanes, so that a segment of up to 8 Q pieces folds in one round trip. 1024-lane workgroups
+     * only where 256 lanes cannot hold the groups. */
     const int row = a.group * MERGE_LANES;
-    int groups = std::max(1, std::min(MERGE_GROUPS, MERGE_THREADS / row));
+    int groups = std::min(MERGE_GROUPS, MERGE_THREADS_MAX / row);
     if (!fixed && max_ctx > DEC_LONG_CTX) {
         /* long contexts: a segment can span up to ceil(pages / DEC_MIN_CHUNK) + 1 waves, so as many groups as that
          * fills (fewer dependent rounds for one long sequence); shorter contexts keep the groups above */
