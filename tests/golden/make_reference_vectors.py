@@ -170,7 +170,7 @@ def qk_vectors(ref) -> dict:
     xb = torch.from_numpy(x).to(torch.bfloat16)
     gain = torch.from_numpy((0.5 + rng.random(128)).astype(np.float32))
     pos = torch.from_numpy(rng.integers(0, 8192, n).astype(np.int64))
-    pos[:4] = torch.tensor([0, 1, 8191, 4096])
+    pos[:8] = torch.tensor([0, 1, 8191, 4096, 16383, 65535, 100000, 131071])  # and long contexts' positions
     out = {"x_bits": xb.view(torch.int16).numpy().view(np.uint16), "gain": gain.numpy(), "pos": pos.numpy()}
     eps = float(torch.finfo(torch.float32).eps)
     for theta in (1e4, 1e6):

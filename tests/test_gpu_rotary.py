@@ -1,6 +1,6 @@
 """The device-built rotary tables (nanochat_amd.rotary, fp64 on the GPU as model/modeling.py:169-176 builds them)
-against the oracle's (numpy fp64, pinned to the closed form in test_oracle.py), over 8192 positions at both RoPE
-bases the build uses."""
+against the oracle's (numpy fp64, pinned to the closed form in test_oracle.py), over 131072 positions (the longest
+contexts the decode tests run) at both RoPE bases the build uses."""
 
 import numpy as np
 import pytest
@@ -10,7 +10,7 @@ from oracle import golden as G
 
 pytestmark = pytest.mark.gpu
 
-N = 8192
+N = 131072
 
 
 def near_midpoint(v64: np.ndarray, slack: np.ndarray) -> np.ndarray:

@@ -41,7 +41,7 @@ MODEL = np.load(os.path.join(HERE, "reference_model_small.npz"))
 
 @pytest.mark.parametrize("theta", ["10000", "1000000"])
 def test_rotary_tables_equal_the_reference(theta):
-    cos, sin = G.rotary_tables(8192, float(theta))
+    cos, sin = G.rotary_tables(131072, float(theta))
     pos = QK["pos"]
     np.testing.assert_array_equal(cos[pos], QK[f"cos_{theta}"])
     np.testing.assert_array_equal(sin[pos], QK[f"sin_{theta}"])
