@@ -855,8 +855,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
  * puts each load behind a branch and a wait), one round trip for up to 8 Q fixed pieces (8 for the balanced split,
  * every segment of config 3). THREADS: 256, or 1024 where the groups need more lanes. */
 #define MERGE_LANES 16
-#define MERGE_THREADS 256      /* the workgroup of the balanced split and of fixed pieces that fit */
-#define MERGE_THREADS_MAX 1024 /* fixed pieces of long contexts: up to 1024 / (16 G) groups */
+#define MERGE_THREADS 256      /* the workgroup where the groups fit in 256 lanes */
+#define MERGE_THREADS_MAX 1024 /* otherwise (head groups of 5 or more, long contexts): up to 1024 / (16 G) groups */
 #define MERGE_GROUPS 4
 #define DEC_LONG_CTX 16384     /* the balanced split's merge takes more groups from this max_ctx on */
 
