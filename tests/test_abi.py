@@ -35,7 +35,21 @@ def test_workspace_query_is_pure_host():
     assert lib.nc_decode_workspace_bytes(0, 16, 4, 8192) == 0
     w = lib.nc_decode_workspace_bytes(64, 16, 4, 8193)
     assert w >= (8192 + 256) * 4 * 130 * 4  # a slot per wave and per segment, 4 heads of (128 + 2) floats
-    assert lib.nc_decode_workspace_bytes(64, 16, 4, 100) == w  # independent of the context
+    assert lib.nc_decode_workspace_bytes(64, 16, 4, 100) == w  # the same for contexts up to about 8K keys
+
+
+def test_workspace_follows_the_piece_cap():
+    """The piece plan keeps up to max(32, ceil(ceil(max_ctx / 16) / 16)) pieces per (sequence, kv head), at most
+    256, each with a slot of G (128 + 2) floats: past 8192 keys the workspace grows with max_ctx (once those slots
+    outnumber the balanced split's), and from 65536 keys on it stays at 256 slots per segment."""
+    lib = native.hip_library()
+    slot = 4 * 130 * 4  # G = 4 heads of (128 + 2) floats
+    ws = {c: lib.nc_decode_workspace_bytes(1024, 16, 4, c) for c in (4096, 8192, 32768, 65536, 131072, 1 << 20)}
+    assert ws[4096] == ws[8192]
+    assert ws[8192] < ws[32768] < ws[65536]
+    assert ws[65536] == ws[131072] == ws[1 << 20]
+    assert ws[65536] >= 4096 * 256 * slot  # 1024 x 4 segments of 256 slots
+    assert ws[32768] >= 4096 * 128 * slot
 
 
 NULL = ctypes.c_void_p(0)
