@@ -172,6 +172,19 @@ __device__ __forceinline__ int ctx_at(const DecodeArgs &a, const int *lds, int b
     return lds ? lds[b] : seq_ctx(a, b);
 }
 
+/* The contexts a k_decode wave schedules from. A batch of at most 64 stays in registers: lane l holds sequence l's
+ * context, schedule units and inclusive unit sum, read back by readlane; a larger batch keeps its contexts in LDS
+ * (lds, up to DEC_LDS_SEQS) or reads them from memory. */
+struct Ctx {
+    const int *lds;
+    int c, units, incl;
+    bool regs;
+};
+
+__device__ __forceinline__ int ctx_of(const DecodeArgs &a, const Ctx &cx, int b) {
+    return cx.regs ? __builtin_amdgcn_readlane(cx.c, b) : ctx_at(a, cx.lds, b);
+}
+
 /* The inclusive prefix sum of v over the wave's 64 lanes. */
 __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
     (void)lane; /* DPP: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast15 / row_bcast31 across rows */
@@ -686,15 +699,17 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
     __syncthreads();
 }
 
-/* Schedule units of the whole batch: every wave derives the same value from the live context lengths and keeps
- * them in lds (if not null); wave b % W writes sequence b's row if it is empty (zeros, or NaN for the fused step's
+/* Schedule units of the whole batch: every wave derives the same value from the live context lengths (the first
+ * 64 entries already loaded, raw0 in lane b) and keeps them in lds (if not null) or, for a batch of at most 64, in
+ * cx's lanes; wave b % W writes sequence b's row if it is empty (zeros, or NaN for the fused step's
  * positions out of range) and its next position to pos_out: sequence w's (own_pos, in lane w % 64) after its pages
  * (put_own_pos), any later ones (a batch larger than the grid) here. 32-bit: the host bounds the total. */
-__device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *lds, int &own_pos) {
+__device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *lds, int &own_pos, int raw0,
+                              Ctx &cx) {
     int total = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int b = base + lane;
-        const int raw = b < a.B ? a.ctx_len[b] : 0;
+        const int raw = b < a.B ? (base == 0 ? raw0 : a.ctx_len[b]) : 0;
         const int c = b < a.B ? seq_ctx_of(a, raw) : 0;
         const int pg = units_of(a, c);
         if (lds && b < a.B) lds[b] = c;
@@ -709,7 +724,9 @@ __device__ int schedule_total(const DecodeArgs &a, int w, int W, int lane, int *
             for (int r = 0; r < a.hq * NC_HEAD_DIM / 8; r++)
                 reinterpret_cast<u32x4 *>(a.out + (size_t)b * a.hq * NC_HEAD_DIM)[r] = z;
         }
-        total += __builtin_amdgcn_readlane(wave_inclusive_sum(pg, lane), 63);
+        const int incl = wave_inclusive_sum(pg, lane);
+        if (cx.regs) cx.c = c, cx.units = pg, cx.incl = incl;
+        total += __builtin_amdgcn_readlane(incl, 63);
     }
     return total * a.hkv;
 }
@@ -721,13 +738,20 @@ __device__ __forceinline__ void put_own_pos(const DecodeArgs &a, int w, int lane
 }
 
 /* The segment holding unit u of the flattened list: sequence b, kv head h and the segment's first unit. */
-__device__ __forceinline__ void find_segment(const DecodeArgs &a, const int *lds, int u, int lane, int &b, int &h,
+__device__ __forceinline__ void find_segment(const DecodeArgs &a, const Ctx &cx, int u, int lane, int &b, int &h,
                                              int &seg_base) {
     int carry = 0, units_b = 0;
     b = -1;
+    if (cx.regs) { /* the sums schedule_total left in the lanes */
+        const unsigned long long hit = __ballot(lane < a.B && cx.incl * a.hkv > u);
+        const int first = hit ? __builtin_ctzll(hit) : 0;
+        b = first;
+        units_b = __builtin_amdgcn_readlane(cx.units, first);
+        carry = __builtin_amdgcn_readlane(cx.incl - cx.units, first) * a.hkv;
+    }
     for (int base = 0; base < a.B && b < 0; base += 64) {
         const int bb = base + lane;
-        const int pg = bb < a.B ? units_of(a, ctx_at(a, lds, bb)) : 0;
+        const int pg = bb < a.B ? units_of(a, ctx_at(a, cx.lds, bb)) : 0;
         const int incl = wave_inclusive_sum(pg, lane);
         const unsigned long long hit = __ballot(bb < a.B && carry + incl * a.hkv > u);
         if (hit) {
@@ -747,10 +771,10 @@ __device__ __forceinline__ void find_segment(const DecodeArgs &a, const int *lds
 /* Fixed pieces: the piece boundary nearest to unit u. A segment's boundaries are its first unit, the units of its
  * pieces' first pages after the first (its start units go with its first piece) and its end (its end units go with
  * its last piece). Every wave rounds a shared slice end alike, so the snapped slices still tile the list. */
-__device__ __forceinline__ int snap_unit(const DecodeArgs &a, const int *lds, int u, int lane) {
+__device__ __forceinline__ int snap_unit(const DecodeArgs &a, const Ctx &cx, int u, int lane) {
     int b, h, seg_base;
-    find_segment(a, lds, u, lane, b, h, seg_base);
-    const int pages = pages_of(a, ctx_at(a, lds, b)), len = piece_len(a, pages), np = (pages + len - 1) / len;
+    find_segment(a, cx, u, lane, b, h, seg_base);
+    const int pages = pages_of(a, ctx_of(a, cx, b)), len = piece_len(a, pages), np = (pages + len - 1) / len;
     const int units = pages + a.unit_start + a.unit_end;
     const int k = min(max((u - seg_base - a.unit_start + len / 2) / len, 0), np); /* numerator >= -unit_start */
     const int at = u - seg_base < a.unit_start ? 0 : k;
@@ -762,11 +786,15 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     __shared__ StepLds sm;
     __shared__ int ctx_lds[DEC_LDS_SEQS];
     const int w = blockIdx.x, W = gridDim.x, lane = threadIdx.x, n = lane & 15, j = lane >> 4;
-    int *const lds = a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
+    /* the first 64 context entries, loaded before anything else: their round trip overlaps the wave's set-up */
+    const int raw0 = lane < a.B ? a.ctx_len[lane] : 0;
+    int *const lds = a.B > 64 && a.B <= DEC_LDS_SEQS ? ctx_lds : nullptr;
+    Ctx cx;
+    cx.lds = lds, cx.c = 0, cx.units = 0, cx.incl = 0, cx.regs = a.B <= 64;
 
     if (lane == 0) sm.nparts = 0;
     int own_pos = 0;
-    const int total = schedule_total(a, w, W, lane, lds, own_pos);
+    const int total = schedule_total(a, w, W, lane, lds, own_pos, raw0, cx);
     __syncthreads(); /* lds complete before other lanes' reads */
     const int chunk = max((total + W - 1) / W, DEC_MIN_CHUNK);
     int start = w * chunk;
@@ -776,8 +804,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     }
     int end = min(start + chunk, total);
     if (a.piece_pages > 0) { /* whole fixed pieces: both ends at the nearest piece boundary */
-        start = snap_unit(a, lds, start, lane);
-        end = end >= total ? total : snap_unit(a, lds, end, lane);
+        start = snap_unit(a, cx, start, lane);
+        end = end >= total ? total : snap_unit(a, cx, end, lane);
         if (start >= end) {
             put_own_pos(a, w, lane, own_pos);
             return;
@@ -787,11 +815,11 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
 
     /* the segment holding `start`: sequence b, kv head h, its first unit seg_base */
     int b, h, seg_base;
-    find_segment(a, lds, start, lane, b, h, seg_base);
+    find_segment(a, cx, start, lane, b, h, seg_base);
     int off = start - seg_base;
 
     while (remaining > 0) {
-        const SeqRange sr = seq_range_of(a, ctx_at(a, lds, b));
+        const SeqRange sr = seq_range_of(a, ctx_of(a, cx, b));
         const int seg_pages = sr.last - sr.first + 1;
         /* this slice takes units [off, off + take) of the segment; its pages are [lo, hi) */
         const int units = seg_pages + a.unit_start + a.unit_end;
@@ -833,7 +861,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             h = 0;
             do {
                 b++;
-            } while (remaining > 0 && b < a.B && pages_of(a, ctx_at(a, lds, b)) == 0);
+            } while (remaining > 0 && b < a.B && pages_of(a, ctx_of(a, cx, b)) == 0);
             if (b >= a.B) break;
         }
     }
