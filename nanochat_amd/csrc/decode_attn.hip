@@ -271,7 +271,6 @@ struct StepLds {
     uint8_t codes[2][NC_HEAD_DIM]; /* new key, new value */
     float scale[2];
     int blk;                       /* their block, -1: none */
-    int nparts;                    /* staged pieces */
     int part_slot[DEC_PART_MAX];   /* their merge slots */
     float part[DEC_PART_FLOATS];   /* piece i at i G 130: o [G][128] (value units), then (max, sum) [G][2] */
 };
@@ -545,15 +544,15 @@ __device__ __forceinline__ int block_checked(const DecodeArgs &a, int entry, int
  * window of a fused piece also builds q once its pages are in flight, and the appending piece's key and value after
  * its first page (before the last). */
 __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st,
-                             StepLds &sm);
+                             StepLds &sm, int &np);
 
 /* Fixed pieces: at the first page of the next piece (page number next_cut), finish the piece before it into its
  * merge slot and start the next one from a fresh state. */
 __device__ __forceinline__ void cut_piece(const DecodeArgs &a, int b, int h, int page, const SeqRange &sr, int lane,
-                                          int &next_cut, State &st, StepLds &sm) {
+                                          int &next_cut, State &st, StepLds &sm, int &np) {
     if (page != next_cut) return;
     const int len = piece_len(a, sr.last - sr.first + 1);
-    finish_piece(a, b, h, 0, (page - sr.first) / len - 1, false, lane, st, sm);
+    finish_piece(a, b, h, 0, (page - sr.first) / len - 1, false, lane, st, sm, np);
     state_init(st);
     next_cut += len;
 }
@@ -561,7 +560,8 @@ __device__ __forceinline__ void cut_piece(const DecodeArgs &a, int b, int h, int
 template <bool FUSED, bool FIRST>
 __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h, int base, int nw, int entry,
                                               const SeqRange &sr, bool app, const QRows &qr, const KvRows &kr,
-                                              bf16x8 *qop, int lane, StepLds &sm, State &st, int &next_cut) {
+                                              bf16x8 *qop, int lane, StepLds &sm, State &st, int &next_cut,
+                                              int &np) {
     const int n = lane & 15, j = lane >> 4;
     const int patch_t = FUSED && app ? sr.p % NC_PAGE : -1;
     const int ids = lane < nw ? block_checked(a, entry, base + lane) : -1;
@@ -588,7 +588,7 @@ __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h,
                       r[(u + DEC_DEPTH - 1) % DEC_DEPTH]);
             __builtin_amdgcn_sched_barrier(0);
             if (u == 0 || k + u < nw) {
-                if (a.piece_pages > 0) cut_piece(a, b, h, base + k + u, sr, lane, next_cut, st, sm);
+                if (a.piece_pages > 0) cut_piece(a, b, h, base + k + u, sr, lane, next_cut, st, sm, np);
                 attend_page(a, r[u], base + k + u, sr, qop, lane, patch_t, sm, st);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -608,7 +608,7 @@ __device__ __forceinline__ void stream_window(const DecodeArgs &a, int b, int h,
  * ids alone. */
 template <bool FUSED, bool TABLE>
 __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, int pg_lo, int npg, const SeqRange &sr,
-                                           bool app, bf16x8 *qop, int lane, StepLds &sm, State &st) {
+                                           bool app, bf16x8 *qop, int lane, StepLds &sm, State &st, int &np) {
     /* fixed pieces: the first cut after the run's first page */
     int next_cut = a.piece_pages > 0 ? pg_lo + piece_len(a, sr.last - sr.first + 1) : -1;
     QRows qr;
@@ -619,12 +619,13 @@ __device__ __forceinline__ void attend_run(const DecodeArgs &a, int b, int h, in
         load_kvrows<TABLE>(a, b, h, sr.p, lane, kr);
     }
     __builtin_amdgcn_sched_barrier(0);
-    stream_window<FUSED, true>(a, b, h, pg_lo, min(64, npg), entry, sr, app, qr, kr, qop, lane, sm, st, next_cut);
+    stream_window<FUSED, true>(a, b, h, pg_lo, min(64, npg), entry, sr, app, qr, kr, qop, lane, sm, st, next_cut,
+                               np);
     for (int win = 64; win < npg; win += 64) {
         const int e = block_entry<TABLE>(a, b, pg_lo + win + lane);
         __builtin_amdgcn_sched_barrier(0);
         stream_window<FUSED, false>(a, b, h, pg_lo + win, min(64, npg - win), e, sr, app, qr, kr, qop, lane, sm,
-                                    st, next_cut);
+                                    st, next_cut, np);
     }
 }
 
@@ -639,9 +640,9 @@ __device__ __forceinline__ size_t merge_slot(const DecodeArgs &a, int s, int i, 
 }
 
 /* The staged pieces to their workspace slots (slot [G][128] of ws_o, [G][2] of ws_ml, both contiguous per slot). */
-__device__ void flush_parts(const DecodeArgs &a, int lane, StepLds &sm) {
+__device__ void flush_parts(const DecodeArgs &a, int lane, StepLds &sm, int &np) {
     __syncthreads(); /* the stage's writes before other lanes' reads */
-    const int G = a.group, np = sm.nparts, per = G * (NC_HEAD_DIM + 2);
+    const int G = a.group, per = G * (NC_HEAD_DIM + 2);
     for (int i = 0; i < np; i++) {
         const size_t slot = (size_t)sm.part_slot[i];
         const f32x4 *src = reinterpret_cast<const f32x4 *>(&sm.part[i * per]);
@@ -650,14 +651,14 @@ __device__ void flush_parts(const DecodeArgs &a, int lane, StepLds &sm) {
         if (lane < 2 * G) a.ws_ml[slot * G * 2 + lane] = sm.part[i * per + G * NC_HEAD_DIM + lane];
     }
     __syncthreads(); /* the reads done before the stage is reused */
-    sm.nparts = 0;
+    np = 0;
 }
 
 /* Finish piece `piece` of segment (b, h), wave w: the whole segment writes the normalised bf16 output; a part of it
  * stages (Σ p v in value units, max, sum) for its merge slot, which k_merge combines. Lane (j, n) holds dims
  * (4 j + i) 8 + bb of head n. */
 __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece, bool whole, int lane, State &st,
-                             StepLds &sm) {
+                             StepLds &sm, int &np) {
     const int n = lane & 15, j = lane >> 4, G = a.group;
     float l = st.l;
     l += shfl_xor_f(l, 16);
@@ -677,8 +678,8 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
         return;
     }
     const int per = G * (NC_HEAD_DIM + 2);
-    if ((sm.nparts + 1) * per > DEC_PART_FLOATS || sm.nparts == DEC_PART_MAX) flush_parts(a, lane, sm);
-    const int at = sm.nparts * per;
+    if ((np + 1) * per > DEC_PART_FLOATS || np == DEC_PART_MAX) flush_parts(a, lane, sm, np);
+    const int at = np * per;
     if (n < G) {
         float *o = &sm.part[at + n * NC_HEAD_DIM];
 #pragma unroll
@@ -693,10 +694,8 @@ __device__ void finish_piece(const DecodeArgs &a, int b, int h, int w, int piece
             sm.part[at + G * NC_HEAD_DIM + 2 * n + 1] = l;
         }
     }
-    if (lane == 0) sm.part_slot[sm.nparts] = (int)merge_slot(a, b * a.hkv + h, piece, w);
-    __syncthreads();
-    sm.nparts = sm.nparts + 1; /* every lane writes the same value */
-    __syncthreads();
+    if (lane == 0) sm.part_slot[np] = (int)merge_slot(a, b * a.hkv + h, piece, w);
+    np++; /* flush_parts' barrier orders these stage writes before its reads */
 }
 
 /* Schedule units of the whole batch: every wave derives the same value from the live context lengths (the first
@@ -792,7 +791,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
     Ctx cx;
     cx.lds = lds, cx.c = 0, cx.units = 0, cx.incl = 0, cx.regs = a.B <= 64;
 
-    if (lane == 0) sm.nparts = 0;
+    int np = 0; /* staged pieces (one wave: a register) */
     int own_pos = 0;
     const int total = schedule_total(a, w, W, lane, lds, own_pos, raw0, cx);
     __syncthreads(); /* lds complete before other lanes' reads */
@@ -852,8 +851,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             }
             State st;
             state_init(st);
-            attend_run<FUSED, TABLE>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st);
-            finish_piece(a, b, h, w, piece, whole, lane, st, sm);
+            attend_run<FUSED, TABLE>(a, b, h, sr.first + lo, hi - lo, sr, hi == seg_pages, qop, lane, sm, st, np);
+            finish_piece(a, b, h, w, piece, whole, lane, st, sm, np);
             if (lo == 0 && lane == 0) a.ws_desc[b * a.hkv + h] = make_int2(seg_pieces, len ? 0 : w_first);
             if (FUSED && hi == seg_pages) store_new_kv(a, h, sr.p, lane, sm);
         }
@@ -865,7 +864,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode(DecodeArgs a) {
             if (b >= a.B) break;
         }
     }
-    flush_parts(a, lane, sm); /* after the last pages: these stores hold up no wait */
+    flush_parts(a, lane, sm, np); /* after the last pages: these stores hold up no wait */
     put_own_pos(a, w, lane, own_pos);
 }
 
